@@ -1,0 +1,317 @@
+// Causal grouped-query attention for gfx950.
+//
+// Semantics: CPUOps.attentionScores / softmax / attentionApply
+// (CPUOps.swift:162-175, :222-274): query token t sits at absolute position
+// start+t, sees cache rows 0..start+t, query head h reads KV head
+// h / (heads/kv_heads), scores scaled by 1/sqrt(hd).  Cache layout here is
+// [kv_heads][capacity][hd] (f16, or f32 in exact mode).
+//
+// flash_attn_kernel (prefill, f16 cache, hd 64/128): replaces the reference's
+// tensor-op and simdgroup prefill attention (tensor_attention.metal,
+// attention_prefill.metal).  A workgroup takes 64 queries of one head (16 per
+// wave) and walks 64-key blocks staged in LDS (K row-major, V transposed).
+// Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_f16,
+// so each lane owns one query column: the online-softmax max/sum need only
+// two cross-lane shuffles, and the probabilities already sit in the B-operand
+// layout of O^T += V^T P^T (the key order inside a 32-key MFMA step is
+// permuted identically on both operands).  P and V enter MFMA as f16;
+// accumulation and the softmax statistics are float32.
+//
+// attn_generic_kernel: one wave per (query, head, key split) with an online
+// softmax in float32 over an f16 or f32 cache; splits are merged by
+// attn_merge_kernel.  Used for decode (split-K over the context, as the
+// reference's attn_decode_split + attn_decode_merge, attention_decode.metal)
+// and for the exact / f32-KV / odd head-dim cases (attention.metal).
+#include "common.h"
+
+namespace {
+
+struct FlashArgs {
+    const f16* q;
+    int ldq;
+    const f16* kc;
+    const f16* vc;
+    int cap, T, H, KVH, start;
+    float scale_log2;
+    float* out32;
+    f16* out16;
+};
+
+constexpr int BQ = 64, BKV = 64;
+
+template <int HD, bool OUT16>
+__global__ __launch_bounds__(256) void flash_attn_kernel(FlashArgs a) {
+    constexpr int LDK = HD + 8, LDV = BKV + 8, KS = HD / 32, DT = HD / 16;
+    __shared__ __attribute__((aligned(16))) f16 Ks[BKV][LDK];
+    __shared__ __attribute__((aligned(16))) f16 Vt[HD][LDV];
+
+    const int h = blockIdx.x;
+    const int qb = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks first
+    const int kvh = h / (a.H / a.KVH);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int g = lane >> 4, c16 = lane & 15;
+    const int qi = qb * BQ + wave * 16 + c16;
+    const int qc = qi < a.T ? qi : a.T - 1;
+    const int pos_q = a.start + qc;
+
+    f16x8 qf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) qf[ks] = *(const f16x8*)(a.q + (int64_t)qc * a.ldq + h * HD + 32 * ks + 8 * g);
+
+    const int last_q = (qb + 1) * BQ < a.T ? (qb + 1) * BQ : a.T;
+    const int kend = a.start + last_q;  // keys [0, kend) cover every query of this block
+    const int nkb = (kend + BKV - 1) / BKV;
+    const f16* kbase = a.kc + (int64_t)kvh * a.cap * HD;
+    const f16* vbase = a.vc + (int64_t)kvh * a.cap * HD;
+
+    float m = -INFINITY, lsum = 0.f;
+    f32x4 oacc[DT];
+#pragma unroll
+    for (int d = 0; d < DT; d++) oacc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int kb = 0; kb < nkb; kb++) {
+        const int key0 = kb * BKV;
+        __syncthreads();
+        for (int seg = tid; seg < BKV * HD / 8; seg += 256) {
+            const int r = seg / (HD / 8), c = (seg % (HD / 8)) * 8, key = key0 + r;
+            int4 kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
+            if (key < kend) {
+                kv = *(const int4*)(kbase + (int64_t)key * HD + c);
+                vv = *(const int4*)(vbase + (int64_t)key * HD + c);
+            }
+            *(int4*)&Ks[r][c] = kv;
+            const f16* vh = (const f16*)&vv;
+#pragma unroll
+            for (int j = 0; j < 8; j++) Vt[c + j][r] = vh[j];
+        }
+        __syncthreads();
+
+        // S^T tiles: sacc[t][r] = score(key0 + 16t + 4g + r, query qi)
+        f32x4 sacc[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            sacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                const f16x8 kf = *(const f16x8*)&Ks[16 * t + c16][32 * ks + 8 * g];
+                sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], sacc[t], 0, 0, 0);
+            }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int key = key0 + 16 * t + 4 * g + r;
+                float z = sacc[t][r] * a.scale_log2;
+                if (key > pos_q || key >= kend) z = -INFINITY;
+                sacc[t][r] = z;
+                mx = fmaxf(mx, z);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mn = fmaxf(m, mx);  // finite: key 0 is visible to every query in block 0
+        const float alpha = exp2f(m - mn);
+        float ps = 0.f;
+        f16 ph[4][4];
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const f16 pv = (f16)exp2f(sacc[t][r] - mn);
+                ph[t][r] = pv;
+                ps += (float)pv;
+            }
+        lsum = lsum * alpha + ps;
+#pragma unroll
+        for (int d = 0; d < DT; d++) oacc[d] *= alpha;
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const f16x8 pf = {ph[2 * s][0], ph[2 * s][1], ph[2 * s][2], ph[2 * s][3],
+                              ph[2 * s + 1][0], ph[2 * s + 1][1], ph[2 * s + 1][2], ph[2 * s + 1][3]};
+#pragma unroll
+            for (int d = 0; d < DT; d++) {
+                const f16x4 lo = *(const f16x4*)&Vt[16 * d + c16][32 * s + 4 * g];
+                const f16x4 hi = *(const f16x4*)&Vt[16 * d + c16][32 * s + 16 + 4 * g];
+                const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                oacc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, oacc[d], 0, 0, 0);
+            }
+        }
+        m = mn;
+    }
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+    if (qi >= a.T) return;
+    const float inv = 1.0f / lsum;
+    // oacc[d][r] = O(query qi, dim 16d + 4g + r)
+#pragma unroll
+    for (int d = 0; d < DT; d++) {
+        const int64_t o = ((int64_t)qi * a.H + h) * HD + 16 * d + 4 * g;
+        if (OUT16) {
+            const f16x4 v = {(f16)(oacc[d][0] * inv), (f16)(oacc[d][1] * inv), (f16)(oacc[d][2] * inv),
+                             (f16)(oacc[d][3] * inv)};
+            *(f16x4*)(a.out16 + o) = v;
+        } else {
+            *(float4*)(a.out32 + o) = make_float4(oacc[d][0] * inv, oacc[d][1] * inv, oacc[d][2] * inv,
+                                                  oacc[d][3] * inv);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ generic
+constexpr int kMaxHD = 256;
+constexpr int kSplitMin = 64;
+
+template <typename KV>
+__global__ __launch_bounds__(64) void attn_generic_kernel(const float* q, int ldq, const KV* kc, const KV* vc,
+                                                          int cap, int H, int KVH, int hd, int start,
+                                                          int split_len, int splits, float* partials, float* out,
+                                                          float scale) {
+    __shared__ float qs[kMaxHD];
+    const int sp = blockIdx.x, h = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
+    const int kvh = h / (H / KVH);
+    const int len = start + t + 1;
+    const int p0 = sp * split_len;
+    const int p1 = (p0 + split_len < len) ? p0 + split_len : len;
+    for (int d = lane; d < hd; d += 64) qs[d] = q[(int64_t)t * ldq + h * hd + d];
+    __syncthreads();
+
+    const KV* kb = kc + (int64_t)kvh * cap * hd;
+    const KV* vb = vc + (int64_t)kvh * cap * hd;
+    float m = -INFINITY, l = 0.f;
+    float o[kMaxHD / 64] = {0.f, 0.f, 0.f, 0.f};
+    for (int c = p0; c < p1; c += 64) {
+        const int p = c + lane;
+        const bool valid = p < p1;
+        float s = -INFINITY;
+        if (valid) {
+            const KV* kr = kb + (int64_t)p * hd;
+            float acc = 0.f;
+            for (int d = 0; d < hd; d++) acc += qs[d] * (float)kr[d];
+            s = acc * scale;
+        }
+        const float mn = fmaxf(m, wave_max(s));  // lane 0 is always valid
+        const float alpha = expf(m - mn);
+        const float e = valid ? expf(s - mn) : 0.f;
+        l = l * alpha + wave_sum(e);
+#pragma unroll
+        for (int i = 0; i < kMaxHD / 64; i++) o[i] *= alpha;
+        const int nv = p1 - c < 64 ? p1 - c : 64;
+        for (int j = 0; j < nv; j++) {
+            const float ej = __shfl(e, j, 64);
+            const KV* vr = vb + (int64_t)(c + j) * hd;
+#pragma unroll
+            for (int i = 0; i < kMaxHD / 64; i++) {
+                const int d = lane + 64 * i;
+                if (d < hd) o[i] += ej * (float)vr[d];
+            }
+        }
+        m = mn;
+    }
+    if (splits == 1) {
+        const float inv = 1.0f / l;
+#pragma unroll
+        for (int i = 0; i < kMaxHD / 64; i++) {
+            const int d = lane + 64 * i;
+            if (d < hd) out[((int64_t)t * H + h) * hd + d] = o[i] * inv;
+        }
+    } else {
+        float* pp = partials + (((int64_t)t * H + h) * splits + sp) * (hd + 2);
+        if (lane == 0) { pp[0] = m; pp[1] = l; }
+#pragma unroll
+        for (int i = 0; i < kMaxHD / 64; i++) {
+            const int d = lane + 64 * i;
+            if (d < hd) pp[2 + d] = o[i];
+        }
+    }
+}
+
+// Merges per-split (max, sum, unnormalised output) triples.
+__global__ void attn_merge_kernel(const float* partials, int H, int hd, int splits, float* out) {
+    const int th = blockIdx.x;  // t * H + h
+    const float* pp = partials + (int64_t)th * splits * (hd + 2);
+    float mx = -INFINITY;
+    for (int s = 0; s < splits; s++) mx = fmaxf(mx, pp[s * (hd + 2)]);
+    float l = 0.f;
+    for (int s = 0; s < splits; s++) {
+        const float ms = pp[s * (hd + 2)];
+        if (ms != -INFINITY) l += pp[s * (hd + 2) + 1] * expf(ms - mx);
+    }
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+        float acc = 0.f;
+        for (int s = 0; s < splits; s++) {
+            const float ms = pp[s * (hd + 2)];
+            if (ms != -INFINITY) acc += pp[s * (hd + 2) + 2 + d] * expf(ms - mx);
+        }
+        out[(int64_t)th * hd + d] = acc / l;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_flash_attention(const f16* q, int ldq, const f16* kc, const f16* vc, int capacity, int tokens,
+                                  int heads, int kv_heads, int hd, int start, float* out_f32, f16* out_f16,
+                                  hipStream_t st) {
+    if (tokens <= 0) return hipSuccess;
+    FlashArgs a;
+    a.q = q;
+    a.ldq = ldq;
+    a.kc = kc;
+    a.vc = vc;
+    a.cap = capacity;
+    a.T = tokens;
+    a.H = heads;
+    a.KVH = kv_heads;
+    a.start = start;
+    a.scale_log2 = 1.4426950408889634f / sqrtf((float)hd);
+    a.out32 = out_f32;
+    a.out16 = out_f16;
+    dim3 grid(heads, (tokens + BQ - 1) / BQ);
+    if (hd == 64) {
+        if (out_f16) flash_attn_kernel<64, true><<<grid, 256, 0, st>>>(a);
+        else flash_attn_kernel<64, false><<<grid, 256, 0, st>>>(a);
+    } else if (hd == 128) {
+        if (out_f16) flash_attn_kernel<128, true><<<grid, 256, 0, st>>>(a);
+        else flash_attn_kernel<128, false><<<grid, 256, 0, st>>>(a);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// Splits for the generic kernel: decode spreads the context over >= 64-key
+// splits (up to 64 of them); batched queries already fill the chip.
+int attention_splits(int length, int heads, int tokens) {
+    (void)heads;
+    if (tokens > 1) return 1;
+    int s = (length + kSplitMin - 1) / kSplitMin;
+    return s < 1 ? 1 : (s > 64 ? 64 : s);
+}
+
+size_t attention_partial_floats(int heads, int tokens, int splits, int hd) {
+    return (size_t)tokens * heads * splits * (hd + 2);
+}
+
+hipError_t launch_attention_generic(const float* q, int ldq, const void* kc, const void* vc, int kv_f16,
+                                    int capacity, int tokens, int heads, int kv_heads, int hd, int start,
+                                    int splits, float* partials, float* out, hipStream_t st) {
+    if (tokens <= 0) return hipSuccess;
+    if (hd > kMaxHD) return hipErrorInvalidValue;
+    const int max_len = start + tokens;
+    int split_len = (max_len + splits - 1) / splits;
+    split_len = (split_len + 63) / 64 * 64;
+    const float scale = 1.0f / sqrtf((float)hd);
+    dim3 grid(splits, heads, tokens);
+    if (kv_f16)
+        attn_generic_kernel<f16><<<grid, 64, 0, st>>>(q, ldq, (const f16*)kc, (const f16*)vc, capacity, heads,
+                                                      kv_heads, hd, start, split_len, splits, partials, out, scale);
+    else
+        attn_generic_kernel<float><<<grid, 64, 0, st>>>(q, ldq, (const float*)kc, (const float*)vc, capacity,
+                                                        heads, kv_heads, hd, start, split_len, splits, partials,
+                                                        out, scale);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || splits == 1) return e;
+    int bt = hd < 64 ? 64 : (hd > 256 ? 256 : (hd + 63) / 64 * 64);
+    attn_merge_kernel<<<tokens * heads, bt, 0, st>>>(partials, heads, hd, splits, out);
+    return hipGetLastError();
+}

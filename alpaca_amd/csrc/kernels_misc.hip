@@ -1,0 +1,217 @@
+// Small HBM-bound kernels of the forward pass: elementwise ops, RMSNorm,
+// embedding gather, dequantisation, RoPE + KV-cache store and the greedy
+// arg-max.  Semantics follow the reference's CPU ops
+// (Sources/AlpacaCore/Operations/CPUOps.swift) cited per kernel.
+#include "common.h"
+
+#include <float.h>
+#include <limits.h>
+
+namespace {
+
+constexpr int kBlock = 256;
+
+inline int grid_for(int64_t n, int per_block = kBlock) {
+    int64_t g = (n + per_block - 1) / per_block;
+    return (int)(g < 65535 * 16 ? g : 65535 * 16);
+}
+
+// CPUOps.add / mul / silu (CPUOps.swift:29-53) and the SwiGLU gate product.
+__global__ void add_kernel(const float* a, const float* b, float* o, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        o[i] = a[i] + b[i];
+}
+__global__ void mul_kernel(const float* a, const float* b, float* o, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        o[i] = a[i] * b[i];
+}
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+__global__ void silu_kernel(const float* x, float* o, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        o[i] = silu_f(x[i]);
+}
+__global__ void silu_mul_kernel(const float* g, const float* u, float* o, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        o[i] = silu_f(g[i]) * u[i];
+}
+__global__ void f32_to_f16_kernel(const float* x, f16* o, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        o[i] = (f16)x[i];
+}
+
+// CPUOps.rmsNorm (CPUOps.swift:144-159): y = x * (1/sqrt(mean(x^2) + eps)) * w,
+// one block per row, optionally writing f16 for the MFMA GEMM.
+__global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const float* x, const float* w, float* of, f16* oh,
+                                                         int dim, float eps) {
+    __shared__ float red[16];
+    const float* xr = x + (int64_t)blockIdx.x * dim;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < dim; i += kBlock) ss += xr[i] * xr[i];
+    ss = block_sum(ss, red);
+    float scale = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (int i = threadIdx.x; i < dim; i += kBlock) {
+        float y = (xr[i] * scale) * w[i];
+        if (of) of[(int64_t)blockIdx.x * dim + i] = y;
+        if (oh) oh[(int64_t)blockIdx.x * dim + i] = (f16)y;
+    }
+}
+
+// Element k of row r of a resident matrix, dequantised exactly (d * q is exact
+// in float32), Quantization.swift:9-35.
+__device__ __forceinline__ float load_elem(const DevMatrix& m, int64_t r, int k) {
+    if (m.dtype == DT_F16) return (float)((const f16*)m.q)[r * m.cols + k];
+    int nb = m.cols / 32;
+    float d = (float)m.s[r * nb + k / 32];
+    if (m.dtype == DT_Q8_0) return d * (float)(int)((const int8_t*)m.q)[r * m.cols + k];
+    int j = k & 31;
+    uint8_t byte = m.q[(r * nb + k / 32) * 16 + (j & 15)];
+    int nib = j < 16 ? (byte & 15) : (byte >> 4);
+    return d * (float)(nib - 8);
+}
+
+// CPUOps.embed (CPUOps.swift:279-290): rows of the table selected by tokens.
+// Token ids are validated on the host before launch.
+__global__ __launch_bounds__(kBlock) void embed_kernel(const int32_t* tokens, DevMatrix m, float* out) {
+    int64_t r = tokens[blockIdx.x];
+    for (int k = threadIdx.x; k < m.cols; k += kBlock) out[(int64_t)blockIdx.x * m.cols + k] = load_elem(m, r, k);
+}
+
+__global__ void dequant_kernel(DevMatrix m, float* out) {
+    int64_t n = (int64_t)m.rows * m.cols;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = load_elem(m, i / m.cols, (int)(i % m.cols));
+}
+
+// Greedy arg-max: largest logit, lowest index on ties, NaN never wins
+// (Sampler.argmax, Sampler.swift:100-108; all-NaN input yields 0).  Writes the
+// next input token and emitted[slot].  One block of 1024 threads.
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, int n, int32_t* chain, int32_t* emitted,
+                                                      int slot) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    float v = -INFINITY;
+    int idx = INT_MAX;
+    for (int i = threadIdx.x; i < n; i += 1024) {
+        float x = logits[i];
+        if (x > v) { v = x; idx = i; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float v2 = __shfl_xor(v, o, 64);
+        int i2 = __shfl_xor(idx, o, 64);
+        if (v2 > v || (v2 == v && i2 < idx)) { v = v2; idx = i2; }
+    }
+    int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    if (l == 0) { sv[w] = v; si[w] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float bv = sv[0];
+        int bi = si[0];
+        for (int i = 1; i < 16; i++)
+            if (sv[i] > bv || (sv[i] == bv && si[i] < bi)) { bv = sv[i]; bi = si[i]; }
+        int token = bi == INT_MAX ? 0 : bi;
+        if (chain) chain[0] = token;
+        if (emitted) emitted[slot] = token;
+    }
+}
+
+// CPUOps.rope (CPUOps.swift:184-212) fused with the KV-cache append
+// (KVCache.write, KVCache.swift:44-63).  cos/sin come from a table built on
+// the host in double precision and rounded once, as the CPU reference does,
+// and the rotation is evaluated without contraction, so q/k match the CPU
+// bit for bit on the same inputs.
+template <typename KV>
+__global__ __launch_bounds__(kBlock) void rope_store_kernel(float* qkv, int ld, int heads, int kv_heads, int hd,
+                                                            int start, const float2* table, int interleaved,
+                                                            int write_q, f16* q16, KV* kc, KV* vc, int capacity) {
+#pragma clang fp contract(off)
+    int t = blockIdx.x;
+    int half = hd / 2;
+    int pos = start + t;
+    int ny = heads + (kc ? kv_heads : 0);
+    float* row = qkv + (int64_t)t * ld;
+    for (int idx = threadIdx.x; idx < ny * half; idx += kBlock) {
+        int y = idx / half, i = idx - y * half;
+        float2 cs = table[(int64_t)pos * half + i];
+        int ia = interleaved ? 2 * i : i;
+        int ib = interleaved ? 2 * i + 1 : i + half;
+        if (y < heads) {
+            float* p = row + y * hd;
+            float a = p[ia], b = p[ib];
+            float ac = a * cs.x, bs = b * cs.y, as = a * cs.y, bc = b * cs.x;
+            float ra = ac - bs, rb = as + bc;
+            if (write_q) { p[ia] = ra; p[ib] = rb; }
+            if (q16) {
+                f16* o = q16 + ((int64_t)t * heads + y) * hd;
+                o[ia] = (f16)ra;
+                o[ib] = (f16)rb;
+            }
+        } else {
+            int h = y - heads;
+            const float* k = row + heads * hd + h * hd;
+            const float* v = row + heads * hd + kv_heads * hd + h * hd;
+            float a = k[ia], b = k[ib];
+            float ac = a * cs.x, bs = b * cs.y, as = a * cs.y, bc = b * cs.x;
+            int64_t dst = ((int64_t)h * capacity + pos) * hd;
+            kc[dst + ia] = (KV)(ac - bs);
+            kc[dst + ib] = (KV)(as + bc);
+            vc[dst + ia] = (KV)v[ia];
+            vc[dst + ib] = (KV)v[ib];
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_add(const float* a, const float* b, float* out, int64_t n, hipStream_t st) {
+    if (n > 0) add_kernel<<<grid_for(n), kBlock, 0, st>>>(a, b, out, n);
+    return hipGetLastError();
+}
+hipError_t launch_mul(const float* a, const float* b, float* out, int64_t n, hipStream_t st) {
+    if (n > 0) mul_kernel<<<grid_for(n), kBlock, 0, st>>>(a, b, out, n);
+    return hipGetLastError();
+}
+hipError_t launch_silu(const float* x, float* out, int64_t n, hipStream_t st) {
+    if (n > 0) silu_kernel<<<grid_for(n), kBlock, 0, st>>>(x, out, n);
+    return hipGetLastError();
+}
+hipError_t launch_silu_mul(const float* g, const float* u, float* out, int64_t n, hipStream_t st) {
+    if (n > 0) silu_mul_kernel<<<grid_for(n), kBlock, 0, st>>>(g, u, out, n);
+    return hipGetLastError();
+}
+hipError_t launch_f32_to_f16(const float* x, f16* out, int64_t n, hipStream_t st) {
+    if (n > 0) f32_to_f16_kernel<<<grid_for(n), kBlock, 0, st>>>(x, out, n);
+    return hipGetLastError();
+}
+hipError_t launch_rmsnorm(const float* x, const float* w, float* of, f16* oh, int rows, int dim, float eps,
+                          hipStream_t st) {
+    if (rows > 0) rmsnorm_kernel<<<rows, kBlock, 0, st>>>(x, w, of, oh, dim, eps);
+    return hipGetLastError();
+}
+hipError_t launch_embed(const int32_t* tokens, int count, const DevMatrix& table, float* out, hipStream_t st) {
+    if (count > 0) embed_kernel<<<count, kBlock, 0, st>>>(tokens, table, out);
+    return hipGetLastError();
+}
+hipError_t launch_dequant(const DevMatrix& m, float* out, hipStream_t st) {
+    int64_t n = (int64_t)m.rows * m.cols;
+    if (n > 0) dequant_kernel<<<grid_for(n), kBlock, 0, st>>>(m, out);
+    return hipGetLastError();
+}
+hipError_t launch_argmax(const float* logits, int n, int32_t* chain, int32_t* emitted, int slot, hipStream_t st) {
+    argmax_kernel<<<1, 1024, 0, st>>>(logits, n, chain, emitted, slot);
+    return hipGetLastError();
+}
+hipError_t launch_rope_store(float* qkv, int ld, int tokens, int heads, int kv_heads, int hd, int start,
+                             const float2* table, int interleaved, int write_q_f32, f16* q_f16, void* kcache,
+                             void* vcache, int kv_f16, int capacity, hipStream_t st) {
+    if (tokens <= 0) return hipSuccess;
+    if (kv_f16)
+        rope_store_kernel<f16><<<tokens, kBlock, 0, st>>>(qkv, ld, heads, kv_heads, hd, start, table, interleaved,
+                                                          write_q_f32, q_f16, (f16*)kcache, (f16*)vcache,
+                                                          capacity);
+    else
+        rope_store_kernel<float><<<tokens, kBlock, 0, st>>>(qkv, ld, heads, kv_heads, hd, start, table,
+                                                            interleaved, write_q_f32, q_f16, (float*)kcache,
+                                                            (float*)vcache, capacity);
+    return hipGetLastError();
+}

@@ -1,0 +1,1302 @@
+// Host runtime of the gfx950 backend: the C ABI declared in include/alpaca_hip.h.
+//
+// Mirrors the reference's Metal host code (Sources/AlpacaMetal/Backend):
+// MetalLlamaModel (weights uploaded once), MetalLlamaSession (KV cache and
+// scratch per session, chunked prefill, fused single-token decode, GPU greedy
+// chain, stage profiling) and MetalOps (tensor-in / tensor-out kernel API).
+// Every kernel runs on the session's own HIP stream; the host only enqueues,
+// waits and copies logits / emitted tokens through pinned memory.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/alpaca_hip.h"
+#include "common.h"
+
+// ------------------------------------------------------------------ errors
+
+static thread_local std::string g_err;
+
+static int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+#define HIP_OR(expr, what)                                                                                  \
+    do {                                                                                                    \
+        hipError_t e_ = (expr);                                                                             \
+        if (e_ != hipSuccess) return fail(AHIP_ERR_COMMAND_FAILED, std::string(what) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+extern "C" const char* ahip_last_error(void) { return g_err.c_str(); }
+
+extern "C" const char* ahip_version(void) {
+    return "alpaca_hip gfx950 (hand-written HIP; MFMA f16 prefill, dequant GEMV decode)";
+}
+
+// ------------------------------------------------------------------ host f16
+
+// IEEE binary32 -> binary16, round to nearest even.
+static uint16_t f32_to_f16_bits(float f) {
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) return (uint16_t)(sign | 0x7C00u | (ax > 0x7F800000u ? 0x200u : 0u));
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);
+    if (ax < 0x38800000u) {
+        if (ax < 0x33000000u) return (uint16_t)sign;
+        const uint32_t man = (ax & 0x7FFFFFu) | 0x800000u;
+        const int shift = 126 - (int)(ax >> 23);
+        uint32_t q = man >> shift;
+        const uint32_t rem = man & ((1u << shift) - 1), half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t q = ((((ax >> 23) - 112u)) << 10) | ((ax & 0x7FFFFFu) >> 13);
+    const uint32_t rem = ax & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+}
+
+static float f16_bits_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu;
+    uint32_t man = h & 0x3FFu, bits;
+    if (e == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else {
+            int s = -1;
+            do { s++; man <<= 1; } while ((man & 0x400u) == 0);
+            bits = sign | ((uint32_t)(112 - s) << 23) | ((man & 0x3FFu) << 13);
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7F800000u | (man << 13);
+    } else {
+        bits = sign | ((e + 112u) << 23) | (man << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+static int block_elems(int dt) { return dt == AHIP_Q8_0 || dt == AHIP_Q4_0 ? 32 : 1; }
+static int block_bytes(int dt) { return dt == AHIP_F32 ? 4 : dt == AHIP_F16 ? 2 : dt == AHIP_Q8_0 ? 34 : 18; }
+static int64_t raw_bytes(int dt, int64_t elements) { return elements / block_elems(dt) * block_bytes(dt); }
+static bool valid_dtype(int dt) { return dt >= AHIP_F32 && dt <= AHIP_Q4_0; }
+
+// ------------------------------------------------------------------ quantiser
+
+template <typename F>
+static void parallel_for(int64_t n, F f) {
+    const int64_t kMin = 1 << 16;
+    unsigned hw = std::thread::hardware_concurrency();
+    int nt = (int)std::min<int64_t>(std::max(1u, std::min(hw, 16u)), std::max<int64_t>(1, n / kMin));
+    if (nt <= 1) {
+        f(0, n);
+        return;
+    }
+    std::vector<std::thread> th;
+    const int64_t per = (n + nt - 1) / nt;
+    for (int t = 0; t < nt; t++) {
+        const int64_t a = t * per, b = std::min(n, a + per);
+        if (a < b) th.emplace_back([=] { f(a, b); });
+    }
+    for (auto& t : th) t.join();
+}
+
+
+// Quantization.swift:39-73 (ggml quantize_row_q8_0_ref / quantize_row_q4_0_ref).
+extern "C" int ahip_quantize(int dtype, const float* v, int64_t count, void* out) {
+    if (dtype != AHIP_Q8_0 && dtype != AHIP_Q4_0) return fail(AHIP_ERR_INVALID_ARGUMENT, "quantize target must be q8_0 or q4_0");
+    if (count < 0 || count % 32 != 0) return fail(AHIP_ERR_INVALID_ARGUMENT, "element count is not a multiple of 32");
+    if (count && (!v || !out)) return fail(AHIP_ERR_INVALID_ARGUMENT, "null buffer");
+    uint8_t* dst = (uint8_t*)out;
+    parallel_for(count / 32, [&](int64_t b0, int64_t b1) {
+    for (int64_t b = b0; b < b1; b++) {
+        const float* x = v + b * 32;
+        if (dtype == AHIP_Q8_0) {
+            uint8_t* p = dst + b * 34;
+            float amax = 0.f;
+            for (int j = 0; j < 32; j++) amax = std::max(amax, std::fabs(x[j]));
+            const float d = amax / 127.0f;
+            const float id = d != 0.f ? 1.0f / d : 0.f;
+            const uint16_t dh = f32_to_f16_bits(d);
+            std::memcpy(p, &dh, 2);
+            for (int j = 0; j < 32; j++) {
+                volatile float t = x[j] * id;  // one rounding, then round half away from zero
+                p[2 + j] = (uint8_t)(int8_t)std::round((float)t);
+            }
+        } else {
+            uint8_t* p = dst + b * 18;
+            float maxv = 0.f, amax = 0.f;
+            for (int j = 0; j < 32; j++)
+                if (std::fabs(x[j]) > amax) { amax = std::fabs(x[j]); maxv = x[j]; }
+            const float d = maxv / -8.0f;
+            const float id = d != 0.f ? 1.0f / d : 0.f;
+            const uint16_t dh = f32_to_f16_bits(d);
+            std::memcpy(p, &dh, 2);
+            for (int j = 0; j < 16; j++) {
+                volatile float tl = x[j] * id;
+                volatile float th = x[j + 16] * id;
+                volatile float sl = tl + 8.5f;
+                volatile float sh = th + 8.5f;
+                const int lo = std::min(15, (int)sl), hi = std::min(15, (int)sh);
+                p[2 + j] = (uint8_t)((uint8_t)lo | ((uint8_t)hi << 4));
+            }
+        }
+    }
+    });
+    return AHIP_OK;
+}
+
+// ------------------------------------------------------------------ synthetic inputs
+
+static inline uint64_t splitmix_at(uint64_t seed, uint64_t step) {
+    // State after `step` calls of next(): seed + step * gamma (Sampler.swift:30-40).
+    uint64_t z = seed + step * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+extern "C" int ahip_synth_uniform(uint64_t seed, uint64_t offset, int64_t n, float lo, float hi, float* out) {
+    if (n < 0 || (n && !out)) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad buffer");
+    parallel_for(n, [&](int64_t a, int64_t b) {
+        for (int64_t i = a; i < b; i++) {
+            const double u = (double)(splitmix_at(seed, offset + i + 1) >> 11) * 0x1.0p-53;
+            out[i] = (float)(lo + (double)(hi - lo) * u);
+        }
+    });
+    return AHIP_OK;
+}
+
+extern "C" int ahip_synth_normal(uint64_t seed, uint64_t offset, int64_t n, float stdv, float* out) {
+    if (n < 0 || (n && !out)) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad buffer");
+    if (offset % 2) return fail(AHIP_ERR_INVALID_ARGUMENT, "normal stream offset must be even");
+    const int64_t pairs = (n + 1) / 2;
+    parallel_for(pairs, [&](int64_t a, int64_t b) {
+        for (int64_t j = a; j < b; j++) {
+            const uint64_t s = offset + 2 * j;
+            const double u1 = (double)(splitmix_at(seed, s + 1) >> 11) * 0x1.0p-53;
+            const double u2 = (double)(splitmix_at(seed, s + 2) >> 11) * 0x1.0p-53;
+            const double r = std::sqrt(-2.0 * std::log(1.0 - u1));
+            const double th = 6.283185307179586 * u2;
+            out[2 * j] = (float)(r * std::cos(th) * stdv);
+            if (2 * j + 1 < n) out[2 * j + 1] = (float)(r * std::sin(th) * stdv);
+        }
+    });
+    return AHIP_OK;
+}
+
+extern "C" int ahip_synth_ints(uint64_t seed, uint64_t offset, int64_t n, uint64_t range, int64_t bias, int32_t* out) {
+    if (n < 0 || (n && !out) || range == 0) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad arguments");
+    parallel_for(n, [&](int64_t a, int64_t b) {
+        for (int64_t i = a; i < b; i++) out[i] = (int32_t)((int64_t)(splitmix_at(seed, offset + i + 1) % range) + bias);
+    });
+    return AHIP_OK;
+}
+
+// ------------------------------------------------------------------ device
+
+extern "C" int ahip_device_count(int* count) {
+    if (!count) return fail(AHIP_ERR_INVALID_ARGUMENT, "null count");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+    *count = n;
+    return AHIP_OK;
+}
+
+struct ahip_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+};
+
+extern "C" int ahip_context_create(int device, ahip_context** out) {
+    if (!out) return fail(AHIP_ERR_INVALID_ARGUMENT, "null out");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(AHIP_ERR_NO_DEVICE, "no HIP device is available");
+    if (device < 0 || device >= n) return fail(AHIP_ERR_INVALID_ARGUMENT, "device index out of range");
+    HIP_OR(hipSetDevice(device), "hipSetDevice");
+    hipDeviceProp_t prop;
+    HIP_OR(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(AHIP_ERR_MODULE_LOAD, std::string("library is built for gfx950, device is ") + prop.gcnArchName);
+    auto* c = new ahip_context();
+    c->device = device;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return fail(AHIP_ERR_COMMAND_FAILED, "hipStreamCreate failed");
+    }
+    *out = c;
+    return AHIP_OK;
+}
+
+extern "C" int ahip_context_destroy(ahip_context* c) {
+    if (!c) return AHIP_OK;
+    hipSetDevice(c->device);
+    hipStreamSynchronize(c->stream);
+    hipStreamDestroy(c->stream);
+    delete c;
+    return AHIP_OK;
+}
+
+// RAII device allocation.
+struct DevBuf {
+    void* p = nullptr;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    ~DevBuf() {
+        if (p) hipFree(p);
+    }
+    int alloc(size_t bytes) {
+        if (hipMalloc(&p, std::max<size_t>(bytes, 256)) != hipSuccess) {
+            p = nullptr;
+            return fail(AHIP_ERR_ALLOC, "failed to allocate a " + std::to_string(bytes) + "-byte device buffer");
+        }
+        return AHIP_OK;
+    }
+    template <typename T>
+    T* as() const { return (T*)p; }
+};
+
+// A weight matrix uploaded in the split quant/scale layout of DevMatrix.
+struct OwnedMatrix {
+    DevMatrix m;
+    DevBuf q, s;
+    int64_t bytes = 0;
+};
+
+// Repack raw GGUF blocks of `rows` x `cols` into quant and scale streams.
+static void repack_host(int dt, const uint8_t* raw, int64_t rows, int64_t cols, std::vector<uint8_t>& q,
+                        std::vector<uint16_t>& s) {
+    if (dt == AHIP_F16) {
+        q.assign(raw, raw + rows * cols * 2);
+        s.clear();
+        return;
+    }
+    const int64_t nb = cols / 32, bb = block_bytes(dt), qb = dt == AHIP_Q8_0 ? 32 : 16;
+    q.resize(rows * nb * qb);
+    s.resize(rows * nb);
+    for (int64_t b = 0; b < rows * nb; b++) {
+        const uint8_t* p = raw + b * bb;
+        std::memcpy(&s[b], p, 2);
+        std::memcpy(&q[b * qb], p + 2, qb);
+    }
+}
+
+// Uploads one or more matrices with equal dtype and cols stacked in row space.
+static int upload_matrix(int dt, const std::vector<std::pair<const void*, int64_t>>& parts, int64_t cols,
+                         OwnedMatrix& out, hipStream_t st) {
+    int64_t rows = 0;
+    for (auto& p : parts) rows += p.second;
+    const int64_t qbytes = dt == AHIP_F16 ? rows * cols * 2 : dt == AHIP_Q8_0 ? rows * cols : rows * cols / 2;
+    const int64_t sbytes = dt == AHIP_F16 ? 0 : rows * (cols / 32) * 2;
+    if (int rc = out.q.alloc(qbytes)) return rc;
+    if (sbytes)
+        if (int rc = out.s.alloc(sbytes)) return rc;
+    int64_t qoff = 0, soff = 0;
+    std::vector<uint8_t> q;
+    std::vector<uint16_t> s;
+    for (auto& p : parts) {
+        repack_host(dt, (const uint8_t*)p.first, p.second, cols, q, s);
+        HIP_OR(hipMemcpyAsync(out.q.as<uint8_t>() + qoff, q.data(), q.size(), hipMemcpyHostToDevice, st), "upload");
+        if (!s.empty())
+            HIP_OR(hipMemcpyAsync(out.s.as<uint8_t>() + soff, s.data(), s.size() * 2, hipMemcpyHostToDevice, st),
+                   "upload");
+        HIP_OR(hipStreamSynchronize(st), "upload");  // host staging is reused
+        qoff += q.size();
+        soff += s.size() * 2;
+    }
+    out.m.dtype = dt;
+    out.m.rows = (int)rows;
+    out.m.cols = (int)cols;
+    out.m.q = out.q.as<uint8_t>();
+    out.m.s = sbytes ? out.s.as<f16>() : nullptr;
+    out.bytes = qbytes + sbytes;
+    return AHIP_OK;
+}
+
+// RoPE (cos, sin) for positions [0, positions): frequencies and angles in
+// double, rounded once to float (CPUOps.rope, CPUOps.swift:196-201).
+static std::vector<float2> rope_table(int positions, int hd, float theta) {
+    const int half = hd / 2;
+    std::vector<float2> t((size_t)positions * half);
+    std::vector<double> freq(half);
+    for (int i = 0; i < half; i++) freq[i] = std::pow((double)theta, -2.0 * (double)i / (double)hd);
+    for (int p = 0; p < positions; p++)
+        for (int i = 0; i < half; i++) {
+            const double a = (double)p * freq[i];
+            t[(size_t)p * half + i] = make_float2((float)std::cos(a), (float)std::sin(a));
+        }
+    return t;
+}
+
+// ------------------------------------------------------------------ model
+
+struct ahip_model {
+    ahip_context* ctx = nullptr;
+    ahip_llama_config c{};
+    struct Layer {
+        DevBuf attn_norm, ffn_norm;
+        OwnedMatrix qkv, wo, gate, up, down;
+    };
+    std::vector<std::unique_ptr<Layer>> layers;
+    OwnedMatrix embed, output;
+    bool tied = false;
+    DevBuf output_norm, rope;
+    int64_t weight_bytes = 0;
+    const DevMatrix& out_matrix() const { return tied ? embed.m : output.m; }
+};
+
+// LlamaConfig.validate (LlamaConfig.swift:30-43) plus what these kernels need
+// (MetalLlamaModel.swift:44-46: head_dim a multiple of 32 up to 256).
+static int validate_config(const ahip_llama_config* c) {
+    if (!c) return fail(AHIP_ERR_INVALID_ARGUMENT, "null config");
+    if (c->vocab_size <= 0 || c->hidden_size <= 0 || c->layer_count <= 0 || c->head_count <= 0 ||
+        c->kv_head_count <= 0 || c->head_dim <= 0 || c->feed_forward_size <= 0 || c->context_length <= 0)
+        return fail(AHIP_ERR_INVALID_ARGUMENT, "all dimensions must be positive");
+    if (c->head_count % c->kv_head_count) return fail(AHIP_ERR_INVALID_ARGUMENT, "headCount is not a multiple of kvHeadCount");
+    if (c->head_dim % 2) return fail(AHIP_ERR_INVALID_ARGUMENT, "RoPE needs an even headDim");
+    if (!(c->rms_norm_eps > 0) || !(c->rope_theta > 0)) return fail(AHIP_ERR_INVALID_ARGUMENT, "rmsNormEps and ropeTheta must be positive");
+    const int64_t lim = 1 << 28;
+    if (c->vocab_size > lim || c->hidden_size > lim || c->feed_forward_size > lim || c->layer_count > lim ||
+        c->context_length > lim)
+        return fail(AHIP_ERR_INVALID_ARGUMENT, "implausibly large dimension");
+    if (c->head_dim % 32 || c->head_dim > 256)
+        return fail(AHIP_ERR_UNSUPPORTED, "head dimension must be a multiple of 32 up to 256");
+    const int qw = c->head_count * c->head_dim;
+    for (int k : {c->hidden_size, qw, c->feed_forward_size})
+        if (k % 32 || k > 12288) return fail(AHIP_ERR_UNSUPPORTED, "input widths must be multiples of 32 up to 12288");
+    return AHIP_OK;
+}
+
+extern "C" int ahip_model_create(ahip_context* ctx, const ahip_llama_config* config, const ahip_tensor_desc* tensors,
+                                 int count, int prefill_weight_cache, ahip_model** out) {
+    (void)prefill_weight_cache;
+    if (!ctx || !out || (count && !tensors)) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
+    if (int rc = validate_config(config)) return rc;
+    const ahip_llama_config& c = *config;
+    std::map<std::string, const ahip_tensor_desc*> byname;
+    for (int i = 0; i < count; i++) {
+        if (!tensors[i].name) return fail(AHIP_ERR_INVALID_ARGUMENT, "tensor without a name");
+        if (!byname.emplace(tensors[i].name, &tensors[i]).second)
+            return fail(AHIP_ERR_INVALID_ARGUMENT, std::string("duplicate tensor ") + tensors[i].name);
+    }
+    auto get = [&](const std::string& n, int64_t rows, int64_t cols, bool norm, const ahip_tensor_desc** d) -> int {
+        auto it = byname.find(n);
+        if (it == byname.end()) return fail(AHIP_ERR_INVALID_ARGUMENT, "missing tensor " + n);
+        const ahip_tensor_desc* t = it->second;
+        const bool shape_ok = norm ? (t->rows * t->cols == cols && (t->rows == 1 || t->cols == 1))
+                                   : (t->rows == rows && t->cols == cols);
+        if (!shape_ok)
+            return fail(AHIP_ERR_INVALID_ARGUMENT, n + ": expected shape [" + std::to_string(rows) + ", " +
+                                                       std::to_string(cols) + "]");
+        if (!valid_dtype(t->dtype)) return fail(AHIP_ERR_INVALID_ARGUMENT, n + ": unknown dtype");
+        if (norm && t->dtype != AHIP_F32) return fail(AHIP_ERR_INVALID_ARGUMENT, n + ": norm weights must be f32");
+        if (!norm && t->dtype == AHIP_F32)
+            return fail(AHIP_ERR_UNSUPPORTED, n + ": f32 projection matrices (use f16, q8_0 or q4_0)");
+        if (!t->data || t->bytes != raw_bytes(t->dtype, t->rows * t->cols))
+            return fail(AHIP_ERR_INVALID_ARGUMENT, n + ": byte count does not match shape and dtype");
+        *d = t;
+        return AHIP_OK;
+    };
+    const int H = c.hidden_size, QW = c.head_count * c.head_dim, KW = c.kv_head_count * c.head_dim,
+              F = c.feed_forward_size, V = c.vocab_size;
+    HIP_OR(hipSetDevice(ctx->device), "hipSetDevice");
+    auto m = std::make_unique<ahip_model>();
+    m->ctx = ctx;
+    m->c = c;
+    hipStream_t st = ctx->stream;
+    const ahip_tensor_desc *te, *tn, *to = nullptr;
+    if (int rc = get("token_embd", V, H, false, &te)) return rc;
+    if (int rc = get("output_norm", 1, H, true, &tn)) return rc;
+    if (byname.count("output"))
+        if (int rc = get("output", V, H, false, &to)) return rc;
+    if (int rc = upload_matrix(te->dtype, {{te->data, V}}, H, m->embed, st)) return rc;
+    m->weight_bytes += m->embed.bytes;
+    m->tied = to == nullptr;
+    if (to) {
+        if (int rc = upload_matrix(to->dtype, {{to->data, V}}, H, m->output, st)) return rc;
+        m->weight_bytes += m->output.bytes;
+    }
+    auto upload_norm = [&](const ahip_tensor_desc* t, DevBuf& b) -> int {
+        if (int rc = b.alloc(H * 4)) return rc;
+        HIP_OR(hipMemcpy(b.p, t->data, H * 4, hipMemcpyHostToDevice), "upload norm");
+        m->weight_bytes += H * 4;
+        return AHIP_OK;
+    };
+    if (int rc = upload_norm(tn, m->output_norm)) return rc;
+    for (int i = 0; i < c.layer_count; i++) {
+        auto L = std::make_unique<ahip_model::Layer>();
+        const std::string p = "blk." + std::to_string(i) + ".";
+        const ahip_tensor_desc *an, *fn, *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+        if (int rc = get(p + "attn_norm", 1, H, true, &an)) return rc;
+        if (int rc = get(p + "attn_q", QW, H, false, &wq)) return rc;
+        if (int rc = get(p + "attn_k", KW, H, false, &wk)) return rc;
+        if (int rc = get(p + "attn_v", KW, H, false, &wv)) return rc;
+        if (int rc = get(p + "attn_output", H, QW, false, &wo)) return rc;
+        if (int rc = get(p + "ffn_norm", 1, H, true, &fn)) return rc;
+        if (int rc = get(p + "ffn_gate", F, H, false, &wg)) return rc;
+        if (int rc = get(p + "ffn_up", F, H, false, &wu)) return rc;
+        if (int rc = get(p + "ffn_down", H, F, false, &wd)) return rc;
+        if (wq->dtype != wk->dtype || wq->dtype != wv->dtype)
+            return fail(AHIP_ERR_UNSUPPORTED, p + "attn_q/k/v must share one format (they are stacked into one matrix)");
+        if (wg->dtype != wu->dtype) return fail(AHIP_ERR_UNSUPPORTED, p + "ffn_gate/up must share one format");
+        if (int rc = upload_norm(an, L->attn_norm)) return rc;
+        if (int rc = upload_norm(fn, L->ffn_norm)) return rc;
+        if (int rc = upload_matrix(wq->dtype, {{wq->data, QW}, {wk->data, KW}, {wv->data, KW}}, H, L->qkv, st)) return rc;
+        if (int rc = upload_matrix(wo->dtype, {{wo->data, H}}, QW, L->wo, st)) return rc;
+        if (int rc = upload_matrix(wg->dtype, {{wg->data, F}}, H, L->gate, st)) return rc;
+        if (int rc = upload_matrix(wu->dtype, {{wu->data, F}}, H, L->up, st)) return rc;
+        if (int rc = upload_matrix(wd->dtype, {{wd->data, H}}, F, L->down, st)) return rc;
+        m->weight_bytes += L->qkv.bytes + L->wo.bytes + L->gate.bytes + L->up.bytes + L->down.bytes;
+        m->layers.push_back(std::move(L));
+    }
+    auto table = rope_table(c.context_length, c.head_dim, c.rope_theta);
+    if (int rc = m->rope.alloc(table.size() * sizeof(float2))) return rc;
+    HIP_OR(hipMemcpy(m->rope.p, table.data(), table.size() * sizeof(float2), hipMemcpyHostToDevice), "upload rope table");
+    HIP_OR(hipStreamSynchronize(st), "model upload");
+    *out = m.release();
+    return AHIP_OK;
+}
+
+extern "C" int ahip_model_destroy(ahip_model* m) {
+    if (!m) return AHIP_OK;
+    hipSetDevice(m->ctx->device);
+    delete m;
+    return AHIP_OK;
+}
+
+extern "C" int ahip_model_weight_bytes(const ahip_model* m, int64_t* bytes) {
+    if (!m || !bytes) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
+    *bytes = m->weight_bytes;
+    return AHIP_OK;
+}
+
+// ------------------------------------------------------------------ session
+
+struct SessionSizes {
+    int64_t kv_per_layer, x, qkv, q16, ctx, ffn, partials, logits;
+    int64_t total;
+};
+
+static constexpr int kMaxSplits = 64;
+
+static SessionSizes session_sizes(const ahip_llama_config& c, int capacity, int max_batch, int kv_f16) {
+    SessionSizes s{};
+    const int64_t B = max_batch, QW = (int64_t)c.head_count * c.head_dim, KW = (int64_t)c.kv_head_count * c.head_dim;
+    s.kv_per_layer = (int64_t)capacity * KW * (kv_f16 ? 2 : 4);
+    s.x = B * c.hidden_size;
+    s.qkv = B * (QW + 2 * KW);
+    s.q16 = B * QW;
+    s.ctx = B * QW;
+    s.ffn = B * c.feed_forward_size;
+    s.partials = (int64_t)c.head_count * kMaxSplits * (c.head_dim + 2);
+    s.logits = c.vocab_size;
+    s.total = 2 * c.layer_count * s.kv_per_layer + 4 * (2 * s.x + s.qkv + s.ctx + s.ffn + s.partials + s.logits) +
+              2 * (s.x + s.q16 + s.ctx + s.ffn) + 4 * ((int64_t)capacity + 9 + capacity);
+    return s;
+}
+
+extern "C" int ahip_session_byte_count(const ahip_llama_config* config, int capacity, int max_batch, int kv_precision,
+                                       int64_t* bytes) {
+    if (!config || !bytes || capacity <= 0 || max_batch <= 0) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad argument");
+    *bytes = session_sizes(*config, capacity, max_batch, kv_precision == AHIP_KV_F16).total;
+    return AHIP_OK;
+}
+
+struct StageMark {
+    std::string label;
+    hipEvent_t start, end;
+    int dispatches;
+};
+
+struct ahip_session {
+    ahip_model* m = nullptr;
+    int capacity = 0, max_batch = 0, kv_f16 = 1, fast = 1;
+    hipStream_t stream = nullptr;
+    std::vector<std::unique_ptr<DevBuf>> kc, vc;
+    DevBuf x, xn, xh, qkv, qh, ctx, ctxh, ffn, ffnh, partials, logits, tokens, chain, emitted;
+    float* logits_host = nullptr;
+    int32_t* emitted_host = nullptr;
+    int32_t* tokens_host = nullptr;
+    int length = 0;
+    std::atomic<int> busy{0};
+    double last_gpu = 0, last_encode = 0;
+    bool profiling = false;
+    std::vector<hipEvent_t> event_pool;
+    size_t events_used = 0;
+    std::vector<StageMark> marks;
+    std::vector<ahip_stage> profile;
+    hipEvent_t ev_begin = nullptr, ev_end = nullptr;
+
+    ~ahip_session() {
+        if (stream) hipStreamSynchronize(stream);
+        for (auto e : event_pool) hipEventDestroy(e);
+        if (ev_begin) hipEventDestroy(ev_begin);
+        if (ev_end) hipEventDestroy(ev_end);
+        if (logits_host) hipHostFree(logits_host);
+        if (emitted_host) hipHostFree(emitted_host);
+        if (tokens_host) hipHostFree(tokens_host);
+        if (stream) hipStreamDestroy(stream);
+    }
+
+    hipEvent_t next_event() {
+        if (events_used == event_pool.size()) {
+            hipEvent_t e;
+            hipEventCreate(&e);
+            event_pool.push_back(e);
+        }
+        return event_pool[events_used++];
+    }
+    // Opens a labelled stage (EncoderProvider.stage, MetalLlamaModel.swift:431-447).
+    void stage(const char* label) {
+        if (!profiling) return;
+        if (!marks.empty() && marks.back().label == label) {
+            marks.back().dispatches++;
+            return;
+        }
+        hipEvent_t e = next_event();
+        hipEventRecord(e, stream);
+        if (!marks.empty()) marks.back().end = e;
+        marks.push_back({label, e, nullptr, 1});
+    }
+    void stage_end() {
+        if (!profiling || marks.empty() || marks.back().end) return;
+        hipEvent_t e = next_event();
+        hipEventRecord(e, stream);
+        marks.back().end = e;
+    }
+    void collect_profile() {
+        profile.clear();
+        if (!profiling) return;
+        std::map<std::string, size_t> index;
+        for (auto& mk : marks) {
+            float ms = 0;
+            if (mk.end) hipEventElapsedTime(&ms, mk.start, mk.end);
+            auto it = index.find(mk.label);
+            if (it == index.end()) {
+                ahip_stage s{};
+                std::snprintf(s.label, sizeof s.label, "%s", mk.label.c_str());
+                index[mk.label] = profile.size();
+                profile.push_back(s);
+                it = index.find(mk.label);
+            }
+            profile[it->second].seconds += ms * 1e-3;
+            profile[it->second].dispatches += mk.dispatches;
+        }
+    }
+    void begin_call() {
+        events_used = 0;
+        marks.clear();
+    }
+};
+
+extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, int kv_precision, int gemm_precision,
+                                   ahip_session** out) {
+    if (!m || !out) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
+    if (capacity <= 0 || max_batch <= 0) return fail(AHIP_ERR_INVALID_ARGUMENT, "capacity and maxBatch must be positive");
+    if (kv_precision != AHIP_KV_F16 && kv_precision != AHIP_KV_F32) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad kv precision");
+    if (gemm_precision != AHIP_GEMM_EXACT && gemm_precision != AHIP_GEMM_FAST) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad gemm precision");
+    const ahip_llama_config& c = m->c;
+    capacity = std::min(capacity, c.context_length);
+    max_batch = std::min(max_batch, capacity);
+    HIP_OR(hipSetDevice(m->ctx->device), "hipSetDevice");
+    auto s = std::make_unique<ahip_session>();
+    s->m = m;
+    s->capacity = capacity;
+    s->max_batch = max_batch;
+    s->kv_f16 = kv_precision == AHIP_KV_F16;
+    s->fast = gemm_precision == AHIP_GEMM_FAST;
+    HIP_OR(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate");
+    const SessionSizes z = session_sizes(c, capacity, max_batch, s->kv_f16);
+    for (int l = 0; l < c.layer_count; l++) {
+        s->kc.emplace_back(new DevBuf());
+        s->vc.emplace_back(new DevBuf());
+        if (int rc = s->kc.back()->alloc(z.kv_per_layer)) return rc;
+        if (int rc = s->vc.back()->alloc(z.kv_per_layer)) return rc;
+    }
+    struct A { DevBuf* b; int64_t n; };
+    for (A a : {A{&s->x, z.x * 4}, A{&s->xn, z.x * 4}, A{&s->xh, z.x * 2}, A{&s->qkv, z.qkv * 4}, A{&s->qh, z.q16 * 2},
+                A{&s->ctx, z.ctx * 4}, A{&s->ctxh, z.ctx * 2}, A{&s->ffn, z.ffn * 4}, A{&s->ffnh, z.ffn * 2},
+                A{&s->partials, z.partials * 4}, A{&s->logits, z.logits * 4}, A{&s->tokens, (int64_t)capacity * 4},
+                A{&s->chain, 64}, A{&s->emitted, ((int64_t)capacity + 8) * 4}})
+        if (int rc = a.b->alloc(a.n)) return rc;
+    if (hipHostMalloc((void**)&s->logits_host, (size_t)c.vocab_size * 4, hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc((void**)&s->emitted_host, ((size_t)capacity + 8) * 4, hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc((void**)&s->tokens_host, (size_t)capacity * 4, hipHostMallocDefault) != hipSuccess)
+        return fail(AHIP_ERR_ALLOC, "pinned host allocation failed");
+    HIP_OR(hipEventCreate(&s->ev_begin), "hipEventCreate");
+    HIP_OR(hipEventCreate(&s->ev_end), "hipEventCreate");
+    *out = s.release();
+    return AHIP_OK;
+}
+
+extern "C" int ahip_session_destroy(ahip_session* s) {
+    if (!s) return AHIP_OK;
+    hipSetDevice(s->m->ctx->device);
+    delete s;
+    return AHIP_OK;
+}
+
+// Single-flight guard (MetalLlamaModel.swift:235, :275).
+struct BusyGuard {
+    ahip_session* s;
+    bool ok;
+    explicit BusyGuard(ahip_session* s_) : s(s_) {
+        int expected = 0;
+        ok = s->busy.compare_exchange_strong(expected, 1);
+    }
+    ~BusyGuard() {
+        if (ok) s->busy.store(0);
+    }
+};
+
+#define LAUNCH(expr)                                                                                          \
+    do {                                                                                                      \
+        hipError_t e_ = (expr);                                                                               \
+        if (e_ != hipSuccess) return fail(AHIP_ERR_COMMAND_FAILED, std::string("kernel launch: ") + hipGetErrorString(e_)); \
+    } while (0)
+
+// Enqueues one chunk of `n` tokens at absolute position `pos` (encodeChunk,
+// MetalLlamaModel.swift:307-384).  Tokens are read from device memory.
+static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bool logits) {
+    ahip_model* m = s->m;
+    const ahip_llama_config& c = m->c;
+    const int H = c.hidden_size, QW = c.head_count * c.head_dim, KW = c.kv_head_count * c.head_dim,
+              F = c.feed_forward_size, hd = c.head_dim, LDQKV = QW + 2 * KW;
+    hipStream_t st = s->stream;
+    float* x = s->x.as<float>();
+    float* qkv = s->qkv.as<float>();
+    const float2* rope = m->rope.as<float2>();
+    s->stage("embed");
+    LAUNCH(launch_embed(dtok, n, m->embed.m, x, st));
+    const bool mfma = s->fast && n >= 16;
+    const bool flash = mfma && s->kv_f16 && (hd == 64 || hd == 128);
+    for (int li = 0; li < c.layer_count; li++) {
+        ahip_model::Layer& L = *m->layers[li];
+        void* kc = s->kc[li]->p;
+        void* vc = s->vc[li]->p;
+        if (n == 1) {
+            // Fused single-token path: 6 launches per layer (MetalLlamaModel.swift:344-356).
+            s->stage("qkv (fused norm)");
+            LAUNCH(launch_gemv(L.qkv.m, nullptr, x, L.attn_norm.as<float>(), c.rms_norm_eps, qkv, GEMV_STORE, st));
+            s->stage("rope + kv store");
+            LAUNCH(launch_rope_store(qkv, LDQKV, 1, c.head_count, c.kv_head_count, hd, pos, rope, c.rope_interleaved,
+                                     1, nullptr, kc, vc, s->kv_f16, s->capacity, st));
+            s->stage("attention");
+            const int splits = attention_splits(pos + 1, c.head_count, 1);
+            LAUNCH(launch_attention_generic(qkv, LDQKV, kc, vc, s->kv_f16, s->capacity, 1, c.head_count,
+                                            c.kv_head_count, hd, pos, splits, s->partials.as<float>(),
+                                            s->ctx.as<float>(), st));
+            s->stage("attn out projection (+residual)");
+            LAUNCH(launch_gemv(L.wo.m, nullptr, s->ctx.as<float>(), nullptr, 0.f, x, GEMV_ADD, st));
+            s->stage("ffn gate+up+silu (fused norm)");
+            LAUNCH(launch_gemv(L.gate.m, &L.up.m, x, L.ffn_norm.as<float>(), c.rms_norm_eps, s->ffn.as<float>(),
+                               GEMV_SWIGLU, st));
+            s->stage("ffn down (+residual)");
+            LAUNCH(launch_gemv(L.down.m, nullptr, s->ffn.as<float>(), nullptr, 0.f, x, GEMV_ADD, st));
+        } else if (mfma) {
+            f16* xh = s->xh.as<f16>();
+            s->stage("rmsnorm");
+            LAUNCH(launch_rmsnorm(x, L.attn_norm.as<float>(), nullptr, xh, n, H, c.rms_norm_eps, st));
+            s->stage("qkv projections");
+            LAUNCH(launch_gemm_mfma(xh, H, n, L.qkv.m, nullptr, qkv, nullptr, LDQKV, GEMM_STORE, st));
+            s->stage("rope + kv store");
+            LAUNCH(launch_rope_store(qkv, LDQKV, n, c.head_count, c.kv_head_count, hd, pos, rope, c.rope_interleaved,
+                                     flash ? 0 : 1, flash ? s->qh.as<f16>() : nullptr, kc, vc, s->kv_f16,
+                                     s->capacity, st));
+            s->stage("attention");
+            if (flash) {
+                LAUNCH(launch_flash_attention(s->qh.as<f16>(), QW, (const f16*)kc, (const f16*)vc, s->capacity, n,
+                                              c.head_count, c.kv_head_count, hd, pos, nullptr, s->ctxh.as<f16>(), st));
+            } else {
+                LAUNCH(launch_attention_generic(qkv, LDQKV, kc, vc, s->kv_f16, s->capacity, n, c.head_count,
+                                                c.kv_head_count, hd, pos, 1, nullptr, s->ctx.as<float>(), st));
+                LAUNCH(launch_f32_to_f16(s->ctx.as<float>(), s->ctxh.as<f16>(), (int64_t)n * QW, st));
+            }
+            s->stage("attn out projection (+residual)");
+            LAUNCH(launch_gemm_mfma(s->ctxh.as<f16>(), QW, n, L.wo.m, nullptr, x, nullptr, H, GEMM_ACC, st));
+            s->stage("rmsnorm");
+            LAUNCH(launch_rmsnorm(x, L.ffn_norm.as<float>(), nullptr, xh, n, H, c.rms_norm_eps, st));
+            s->stage("ffn gate+up+silu");
+            LAUNCH(launch_gemm_mfma(xh, H, n, L.gate.m, &L.up.m, nullptr, s->ffnh.as<f16>(), F, GEMM_SWIGLU, st));
+            s->stage("ffn down (+residual)");
+            LAUNCH(launch_gemm_mfma(s->ffnh.as<f16>(), F, n, L.down.m, nullptr, x, nullptr, H, GEMM_ACC, st));
+        } else {
+            float* xn = s->xn.as<float>();
+            s->stage("rmsnorm");
+            LAUNCH(launch_rmsnorm(x, L.attn_norm.as<float>(), xn, nullptr, n, H, c.rms_norm_eps, st));
+            s->stage("qkv projections");
+            LAUNCH(launch_gemm_f32(xn, H, n, L.qkv.m, nullptr, qkv, LDQKV, GEMM_STORE, st));
+            s->stage("rope + kv store");
+            LAUNCH(launch_rope_store(qkv, LDQKV, n, c.head_count, c.kv_head_count, hd, pos, rope, c.rope_interleaved,
+                                     1, nullptr, kc, vc, s->kv_f16, s->capacity, st));
+            s->stage("attention");
+            LAUNCH(launch_attention_generic(qkv, LDQKV, kc, vc, s->kv_f16, s->capacity, n, c.head_count,
+                                            c.kv_head_count, hd, pos, 1, nullptr, s->ctx.as<float>(), st));
+            s->stage("attn out projection (+residual)");
+            LAUNCH(launch_gemm_f32(s->ctx.as<float>(), QW, n, L.wo.m, nullptr, x, H, GEMM_ACC, st));
+            s->stage("rmsnorm");
+            LAUNCH(launch_rmsnorm(x, L.ffn_norm.as<float>(), xn, nullptr, n, H, c.rms_norm_eps, st));
+            s->stage("ffn gate+up+silu");
+            LAUNCH(launch_gemm_f32(xn, H, n, L.gate.m, &L.up.m, s->ffn.as<float>(), F, GEMM_SWIGLU, st));
+            s->stage("ffn down (+residual)");
+            LAUNCH(launch_gemm_f32(s->ffn.as<float>(), F, n, L.down.m, nullptr, x, H, GEMM_ACC, st));
+        }
+    }
+    if (logits) {
+        // Only the final position's logits: fused norm + GEMV (MetalLlamaModel.swift:373-383).
+        s->stage("final norm + logits");
+        LAUNCH(launch_gemv(m->out_matrix(), nullptr, x + (int64_t)(n - 1) * H, m->output_norm.as<float>(),
+                           c.rms_norm_eps, s->logits.as<float>(), GEMV_STORE, st));
+    }
+    return AHIP_OK;
+}
+
+static int validate_tokens(const ahip_session* s, const int32_t* tokens, int n) {
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= s->m->c.vocab_size)
+            return fail(AHIP_ERR_INVALID_ARGUMENT, "token id outside vocabulary of " + std::to_string(s->m->c.vocab_size));
+    return AHIP_OK;
+}
+
+extern "C" int ahip_session_forward(ahip_session* s, const int32_t* tokens, int n, const float** logits) {
+    if (!s || !logits) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
+    BusyGuard guard(s);
+    if (!guard.ok) return fail(AHIP_ERR_BUSY, "session is already executing a forward pass");
+    if (n <= 0 || !tokens) return fail(AHIP_ERR_INVALID_ARGUMENT, "forward called with no tokens");
+    if ((int64_t)s->length + n > s->capacity)
+        return fail(AHIP_ERR_INVALID_ARGUMENT, "context exhausted: " + std::to_string(s->length) + " cached + " +
+                                                   std::to_string(n) + " new > capacity " + std::to_string(s->capacity));
+    if (int rc = validate_tokens(s, tokens, n)) return rc;
+    HIP_OR(hipSetDevice(s->m->ctx->device), "hipSetDevice");
+    s->begin_call();
+    const auto t0 = std::chrono::steady_clock::now();
+    std::memcpy(s->tokens_host, tokens, (size_t)n * 4);
+    HIP_OR(hipEventRecord(s->ev_begin, s->stream), "hipEventRecord");
+    HIP_OR(hipMemcpyAsync(s->tokens.p, s->tokens_host, (size_t)n * 4, hipMemcpyHostToDevice, s->stream), "token upload");
+    for (int c0 = 0; c0 < n; c0 += s->max_batch) {
+        const int cn = std::min(s->max_batch, n - c0);
+        if (int rc = encode_chunk(s, s->tokens.as<int32_t>() + c0, cn, s->length + c0, c0 + cn == n)) {
+            hipStreamSynchronize(s->stream);
+            return rc;
+        }
+    }
+    s->stage_end();
+    HIP_OR(hipMemcpyAsync(s->logits_host, s->logits.p, (size_t)s->m->c.vocab_size * 4, hipMemcpyDeviceToHost, s->stream),
+           "logits download");
+    HIP_OR(hipEventRecord(s->ev_end, s->stream), "hipEventRecord");
+    s->last_encode = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    HIP_OR(hipStreamSynchronize(s->stream), "forward");
+    float ms = 0;
+    hipEventElapsedTime(&ms, s->ev_begin, s->ev_end);
+    s->last_gpu = ms * 1e-3;
+    s->collect_profile();
+    s->length += n;
+    *logits = s->logits_host;
+    return AHIP_OK;
+}
+
+extern "C" int ahip_session_decode(ahip_session* s, int32_t token, const float** logits) {
+    return ahip_session_forward(s, &token, 1, logits);
+}
+
+extern "C" int ahip_session_decode_greedy(ahip_session* s, int32_t start, int max_steps, int depth, ahip_emit_fn emit,
+                                          void* user, int* fed_out) {
+    if (!s || !emit || !fed_out) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
+    BusyGuard guard(s);
+    if (!guard.ok) return fail(AHIP_ERR_BUSY, "session is already executing a forward pass");
+    *fed_out = 0;
+    if (start < 0 || start >= s->m->c.vocab_size)
+        return fail(AHIP_ERR_INVALID_ARGUMENT, "token id outside vocabulary of " + std::to_string(s->m->c.vocab_size));
+    const int budget = std::min(max_steps, s->capacity - s->length);
+    if (budget <= 0) return AHIP_OK;
+    depth = std::max(1, std::min(depth, 8));
+    HIP_OR(hipSetDevice(s->m->ctx->device), "hipSetDevice");
+    s->begin_call();
+    hipStream_t st = s->stream;
+    s->tokens_host[0] = start;
+    HIP_OR(hipMemcpyAsync(s->chain.p, s->tokens_host, 4, hipMemcpyHostToDevice, st), "chain upload");
+    HIP_OR(hipEventRecord(s->ev_begin, st), "hipEventRecord");
+    std::vector<hipEvent_t> done(budget, nullptr);
+    int submitted = 0, fed = 0, rc = AHIP_OK;
+    auto submit = [&]() -> int {
+        const int i = submitted;
+        if (int r = encode_chunk(s, s->chain.as<int32_t>(), 1, s->length + i, true)) return r;
+        s->stage("sample");
+        LAUNCH(launch_argmax(s->logits.as<float>(), s->m->c.vocab_size, s->chain.as<int32_t>(),
+                             s->emitted.as<int32_t>(), i, st));
+        HIP_OR(hipMemcpyAsync(s->emitted_host + i, s->emitted.as<int32_t>() + i, 4, hipMemcpyDeviceToHost, st),
+               "token download");
+        done[i] = s->next_event();
+        HIP_OR(hipEventRecord(done[i], st), "hipEventRecord");
+        submitted++;
+        return AHIP_OK;
+    };
+    while (submitted < std::min(depth, budget) && rc == AHIP_OK) rc = submit();
+    while (rc == AHIP_OK && fed < submitted) {
+        hipError_t e = hipEventSynchronize(done[fed]);
+        if (e != hipSuccess) {
+            rc = fail(AHIP_ERR_COMMAND_FAILED, std::string("decode step: ") + hipGetErrorString(e));
+            break;
+        }
+        const int32_t token = s->emitted_host[fed];
+        fed++;
+        if (!emit(user, token)) break;
+        if (submitted < budget) rc = submit();
+    }
+    s->stage_end();
+    HIP_OR(hipEventRecord(s->ev_end, st), "hipEventRecord");
+    hipError_t e = hipStreamSynchronize(st);
+    if (e != hipSuccess && rc == AHIP_OK) rc = fail(AHIP_ERR_COMMAND_FAILED, std::string("drain: ") + hipGetErrorString(e));
+    float ms = 0;
+    hipEventElapsedTime(&ms, s->ev_begin, s->ev_end);
+    s->last_gpu = ms * 1e-3;
+    s->collect_profile();
+    s->length += fed;  // only tokens whose input was consumed (MetalLlamaModel.swift:265-267)
+    *fed_out = fed;
+    return rc;
+}
+
+extern "C" int ahip_session_reset(ahip_session* s) {
+    if (!s) return fail(AHIP_ERR_INVALID_ARGUMENT, "null session");
+    BusyGuard guard(s);
+    if (!guard.ok) return fail(AHIP_ERR_BUSY, "session is busy");
+    s->length = 0;
+    return AHIP_OK;
+}
+extern "C" int ahip_session_length(const ahip_session* s, int* v) {
+    if (!s || !v) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
+    *v = s->length;
+    return AHIP_OK;
+}
+extern "C" int ahip_session_capacity(const ahip_session* s, int* v) {
+    if (!s || !v) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
+    *v = s->capacity;
+    return AHIP_OK;
+}
+extern "C" int ahip_session_last_gpu_seconds(const ahip_session* s, double* v) {
+    if (!s || !v) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
+    *v = s->last_gpu;
+    return AHIP_OK;
+}
+extern "C" int ahip_session_last_encode_seconds(const ahip_session* s, double* v) {
+    if (!s || !v) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
+    *v = s->last_encode;
+    return AHIP_OK;
+}
+extern "C" int ahip_session_set_profiling(ahip_session* s, int enabled) {
+    if (!s) return fail(AHIP_ERR_INVALID_ARGUMENT, "null session");
+    s->profiling = enabled != 0;
+    return AHIP_OK;
+}
+extern "C" int ahip_session_profile(const ahip_session* s, ahip_stage* out, int cap, int* count) {
+    if (!s || !count || (cap > 0 && !out)) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
+    const int n = (int)s->profile.size();
+    for (int i = 0; i < n && i < cap; i++) out[i] = s->profile[i];
+    *count = n;
+    return AHIP_OK;
+}
+
+// ------------------------------------------------------------------ op-level API (MetalOps)
+
+namespace {
+
+// Runs `body` on the context stream and waits (MetalOps.run, MetalOps.swift:19-32).
+struct OpRun {
+    ahip_context* ctx;
+    explicit OpRun(ahip_context* c) : ctx(c) { hipSetDevice(c->device); }
+    int finish() {
+        HIP_OR(hipStreamSynchronize(ctx->stream), "op");
+        return AHIP_OK;
+    }
+};
+
+int upload(DevBuf& b, const void* host, size_t bytes, hipStream_t st) {
+    if (int rc = b.alloc(bytes)) return rc;
+    if (bytes) HIP_OR(hipMemcpyAsync(b.p, host, bytes, hipMemcpyHostToDevice, st), "upload");
+    return AHIP_OK;
+}
+
+int download(void* host, const DevBuf& b, size_t bytes, hipStream_t st) {
+    if (bytes) HIP_OR(hipMemcpyAsync(host, b.p, bytes, hipMemcpyDeviceToHost, st), "download");
+    HIP_OR(hipStreamSynchronize(st), "op");
+    return AHIP_OK;
+}
+
+int check_matrix(int dtype, int k) {
+    if (!valid_dtype(dtype)) return fail(AHIP_ERR_INVALID_ARGUMENT, "unknown dtype");
+    if (dtype == AHIP_F32) return fail(AHIP_ERR_UNSUPPORTED, "f32 weight matrices (use f16, q8_0 or q4_0)");
+    if (k <= 0 || k % 32 || k > 12288) return fail(AHIP_ERR_UNSUPPORTED, "K must be a positive multiple of 32 up to 12288");
+    return AHIP_OK;
+}
+
+template <typename F>
+int with_ctx(ahip_context* ctx, F f) {
+    if (!ctx) return fail(AHIP_ERR_INVALID_ARGUMENT, "null context");
+    HIP_OR(hipSetDevice(ctx->device), "hipSetDevice");
+    return f(ctx->stream);
+}
+
+}  // namespace
+
+static int op_binary(ahip_context* ctx, const float* a, const float* b, int64_t n, float* out, int which) {
+    if (n < 0 || (n && (!a || !out || (which != 2 && !b)))) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad buffers");
+    return with_ctx(ctx, [&](hipStream_t st) -> int {
+        DevBuf da, db, dout;
+        if (int rc = upload(da, a, n * 4, st)) return rc;
+        if (which != 2)
+            if (int rc = upload(db, b, n * 4, st)) return rc;
+        if (int rc = dout.alloc(n * 4)) return rc;
+        if (which == 0) LAUNCH(launch_add(da.as<float>(), db.as<float>(), dout.as<float>(), n, st));
+        else if (which == 1) LAUNCH(launch_mul(da.as<float>(), db.as<float>(), dout.as<float>(), n, st));
+        else if (which == 2) LAUNCH(launch_silu(da.as<float>(), dout.as<float>(), n, st));
+        else LAUNCH(launch_silu_mul(da.as<float>(), db.as<float>(), dout.as<float>(), n, st));
+        return download(out, dout, n * 4, st);
+    });
+}
+
+extern "C" int ahip_op_add(ahip_context* ctx, const float* a, const float* b, int64_t n, float* out) {
+    return op_binary(ctx, a, b, n, out, 0);
+}
+extern "C" int ahip_op_mul(ahip_context* ctx, const float* a, const float* b, int64_t n, float* out) {
+    return op_binary(ctx, a, b, n, out, 1);
+}
+extern "C" int ahip_op_silu(ahip_context* ctx, const float* x, int64_t n, float* out) {
+    return op_binary(ctx, x, nullptr, n, out, 2);
+}
+extern "C" int ahip_op_silu_mul(ahip_context* ctx, const float* g, const float* u, int64_t n, float* out) {
+    return op_binary(ctx, g, u, n, out, 3);
+}
+
+extern "C" int ahip_op_rmsnorm(ahip_context* ctx, const float* x, const float* w, int rows, int dim, float eps,
+                               float* out) {
+    if (rows < 0 || dim <= 0 || !(eps > 0) || (rows && (!x || !w || !out)))
+        return fail(AHIP_ERR_INVALID_ARGUMENT, "rmsNorm shapes");
+    return with_ctx(ctx, [&](hipStream_t st) -> int {
+        DevBuf dx, dw, dout;
+        if (int rc = upload(dx, x, (size_t)rows * dim * 4, st)) return rc;
+        if (int rc = upload(dw, w, (size_t)dim * 4, st)) return rc;
+        if (int rc = dout.alloc((size_t)rows * dim * 4)) return rc;
+        LAUNCH(launch_rmsnorm(dx.as<float>(), dw.as<float>(), dout.as<float>(), nullptr, rows, dim, eps, st));
+        return download(out, dout, (size_t)rows * dim * 4, st);
+    });
+}
+
+static int upload_weight(int dtype, const void* w, int n, int k, OwnedMatrix& om, hipStream_t st) {
+    return upload_matrix(dtype, {{w, n}}, k, om, st);
+}
+
+// Shared by linear / linear_add / gate_up_silu (MetalOps.swift:50-105):
+// m == 1 -> decode GEMV; fast and m >= 16 -> MFMA GEMM on f16 activations;
+// otherwise the float32 GEMM.
+static int op_project(ahip_context* ctx, const float* x, int m, int k, int dtype, const void* w, const void* wu,
+                      int n, int precision, float* y, int mode) {
+    if (m <= 0 || n <= 0 || !x || !w || !y || (mode == GEMM_SWIGLU && !wu))
+        return fail(AHIP_ERR_INVALID_ARGUMENT, "linear shapes");
+    if (precision != AHIP_GEMM_EXACT && precision != AHIP_GEMM_FAST) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad precision");
+    if (int rc = check_matrix(dtype, k)) return rc;
+    return with_ctx(ctx, [&](hipStream_t st) -> int {
+        OwnedMatrix W, U;
+        if (int rc = upload_weight(dtype, w, n, k, W, st)) return rc;
+        if (mode == GEMM_SWIGLU)
+            if (int rc = upload_weight(dtype, wu, n, k, U, st)) return rc;
+        DevBuf dx, dy;
+        if (int rc = upload(dx, x, (size_t)m * k * 4, st)) return rc;
+        if (mode == GEMM_ACC) {
+            if (int rc = upload(dy, y, (size_t)m * n * 4, st)) return rc;
+        } else if (int rc = dy.alloc((size_t)m * n * 4)) {
+            return rc;
+        }
+        const DevMatrix* up = mode == GEMM_SWIGLU ? &U.m : nullptr;
+        if (m == 1) {
+            const int gm = mode == GEMM_STORE ? GEMV_STORE : mode == GEMM_ACC ? GEMV_ADD : GEMV_SWIGLU;
+            LAUNCH(launch_gemv(W.m, up, dx.as<float>(), nullptr, 0.f, dy.as<float>(), gm, st));
+        } else if (precision == AHIP_GEMM_FAST && m >= 16) {
+            DevBuf xh, yh;
+            if (int rc = xh.alloc((size_t)m * k * 2)) return rc;
+            LAUNCH(launch_f32_to_f16(dx.as<float>(), xh.as<f16>(), (int64_t)m * k, st));
+            if (mode == GEMM_SWIGLU) {
+                if (int rc = yh.alloc((size_t)m * n * 2)) return rc;
+                LAUNCH(launch_gemm_mfma(xh.as<f16>(), k, m, W.m, up, nullptr, yh.as<f16>(), n, mode, st));
+                std::vector<uint16_t> h((size_t)m * n);
+                if (int rc = download(h.data(), yh, h.size() * 2, st)) return rc;
+                for (size_t i = 0; i < h.size(); i++) y[i] = f16_bits_to_f32(h[i]);
+                return AHIP_OK;
+            }
+            LAUNCH(launch_gemm_mfma(xh.as<f16>(), k, m, W.m, nullptr, dy.as<float>(), nullptr, n, mode, st));
+        } else {
+            LAUNCH(launch_gemm_f32(dx.as<float>(), k, m, W.m, up, dy.as<float>(), n, mode, st));
+        }
+        return download(y, dy, (size_t)m * n * 4, st);
+    });
+}
+
+extern "C" int ahip_op_linear(ahip_context* ctx, const float* x, int m, int k, int dtype, const void* w, int n,
+                              int precision, float* y) {
+    return op_project(ctx, x, m, k, dtype, w, nullptr, n, precision, y, GEMM_STORE);
+}
+extern "C" int ahip_op_linear_add(ahip_context* ctx, const float* x, int m, int k, int dtype, const void* w, int n,
+                                  int precision, float* residual) {
+    return op_project(ctx, x, m, k, dtype, w, nullptr, n, precision, residual, GEMM_ACC);
+}
+extern "C" int ahip_op_gate_up_silu(ahip_context* ctx, const float* x, int m, int k, int dtype, const void* wg,
+                                    const void* wu, int n, int precision, float* out) {
+    return op_project(ctx, x, m, k, dtype, wg, wu, n, precision, out, GEMM_SWIGLU);
+}
+
+extern "C" int ahip_op_rope(ahip_context* ctx, float* x, int tokens, int heads, int hd, int start, float theta,
+                            int interleaved) {
+    if (tokens < 0 || heads <= 0 || hd <= 0 || hd % 2 || start < 0 || !(theta > 0) || (tokens && !x))
+        return fail(AHIP_ERR_INVALID_ARGUMENT, "rope shape");
+    if (tokens == 0) return AHIP_OK;
+    return with_ctx(ctx, [&](hipStream_t st) -> int {
+        auto table = rope_table(start + tokens, hd, theta);
+        DevBuf dt, dx;
+        if (int rc = upload(dt, table.data(), table.size() * sizeof(float2), st)) return rc;
+        const size_t bytes = (size_t)tokens * heads * hd * 4;
+        if (int rc = upload(dx, x, bytes, st)) return rc;
+        LAUNCH(launch_rope_store(dx.as<float>(), heads * hd, tokens, heads, 0, hd, start, dt.as<float2>(),
+                                 interleaved ? 1 : 0, 1, nullptr, nullptr, nullptr, 1, 0, st));
+        return download(x, dx, bytes, st);
+    });
+}
+
+extern "C" int ahip_op_attention(ahip_context* ctx, const float* q, int tokens, int heads, int hd, const float* keys,
+                                 const float* values, int capacity, int kv_heads, int start, int kv_precision,
+                                 int precision, float* out) {
+    if (tokens <= 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || hd <= 0 || start < 0 ||
+        start + tokens > capacity || !q || !keys || !values || !out)
+        return fail(AHIP_ERR_INVALID_ARGUMENT, "attention shapes");
+    if (hd % 32 || hd > 256) return fail(AHIP_ERR_INVALID_ARGUMENT, "head dimension must be a multiple of 32 up to 256");
+    const bool f16kv = kv_precision == AHIP_KV_F16;
+    return with_ctx(ctx, [&](hipStream_t st) -> int {
+        // Cache rows [capacity][kv_heads][hd] -> [kv_heads][capacity][hd] in the cache format.
+        const size_t ne = (size_t)capacity * kv_heads * hd;
+        std::vector<uint8_t> kb(ne * (f16kv ? 2 : 4)), vb(ne * (f16kv ? 2 : 4));
+        for (int p = 0; p < capacity; p++)
+            for (int h = 0; h < kv_heads; h++)
+                for (int d = 0; d < hd; d++) {
+                    const size_t src = ((size_t)p * kv_heads + h) * hd + d, dst = ((size_t)h * capacity + p) * hd + d;
+                    if (f16kv) {
+                        ((uint16_t*)kb.data())[dst] = f32_to_f16_bits(keys[src]);
+                        ((uint16_t*)vb.data())[dst] = f32_to_f16_bits(values[src]);
+                    } else {
+                        ((float*)kb.data())[dst] = keys[src];
+                        ((float*)vb.data())[dst] = values[src];
+                    }
+                }
+        DevBuf dk, dv, dout, dq;
+        if (int rc = upload(dk, kb.data(), kb.size(), st)) return rc;
+        if (int rc = upload(dv, vb.data(), vb.size(), st)) return rc;
+        const size_t qn = (size_t)tokens * heads * hd;
+        if (int rc = dout.alloc(qn * 4)) return rc;
+        if (precision == AHIP_GEMM_FAST && f16kv && tokens >= 16 && (hd == 64 || hd == 128)) {
+            std::vector<uint16_t> qh(qn);
+            for (size_t i = 0; i < qn; i++) qh[i] = f32_to_f16_bits(q[i]);
+            if (int rc = upload(dq, qh.data(), qn * 2, st)) return rc;
+            LAUNCH(launch_flash_attention(dq.as<f16>(), heads * hd, dk.as<f16>(), dv.as<f16>(), capacity, tokens, heads,
+                                          kv_heads, hd, start, dout.as<float>(), nullptr, st));
+        } else {
+            if (int rc = upload(dq, q, qn * 4, st)) return rc;
+            const int splits = attention_splits(start + tokens, heads, tokens);
+            DevBuf part;
+            if (int rc = part.alloc(attention_partial_floats(heads, tokens, splits, hd) * 4)) return rc;
+            LAUNCH(launch_attention_generic(dq.as<float>(), heads * hd, dk.p, dv.p, f16kv, capacity, tokens, heads,
+                                            kv_heads, hd, start, splits, part.as<float>(), dout.as<float>(), st));
+        }
+        return download(out, dout, qn * 4, st);
+    });
+}
+
+extern "C" int ahip_op_embed(ahip_context* ctx, const int32_t* tokens, int count, int dtype, const void* table,
+                             int vocab, int dim, float* out) {
+    if (count < 0 || vocab <= 0 || dim <= 0 || !table || (count && (!tokens || !out)))
+        return fail(AHIP_ERR_INVALID_ARGUMENT, "embedding table");
+    if (!valid_dtype(dtype)) return fail(AHIP_ERR_INVALID_ARGUMENT, "unknown dtype");
+    if (dtype == AHIP_F32) return fail(AHIP_ERR_UNSUPPORTED, "f32 embedding tables");
+    if (dim % 32) return fail(AHIP_ERR_UNSUPPORTED, "embedding width must be a multiple of 32");
+    for (int i = 0; i < count; i++)
+        if (tokens[i] < 0 || tokens[i] >= vocab) return fail(AHIP_ERR_INVALID_ARGUMENT, "token id outside vocabulary");
+    if (count == 0) return AHIP_OK;
+    return with_ctx(ctx, [&](hipStream_t st) -> int {
+        OwnedMatrix T;
+        if (int rc = upload_weight(dtype, table, vocab, dim, T, st)) return rc;
+        DevBuf dt, dout;
+        if (int rc = upload(dt, tokens, (size_t)count * 4, st)) return rc;
+        if (int rc = dout.alloc((size_t)count * dim * 4)) return rc;
+        LAUNCH(launch_embed(dt.as<int32_t>(), count, T.m, dout.as<float>(), st));
+        return download(out, dout, (size_t)count * dim * 4, st);
+    });
+}
+
+extern "C" int ahip_op_dequantize(ahip_context* ctx, int dtype, const void* src, int64_t elements, float* out) {
+    if (!valid_dtype(dtype) || dtype == AHIP_F32) return fail(AHIP_ERR_INVALID_ARGUMENT, "dequantize: f16, q8_0 or q4_0");
+    if (elements < 0 || (elements && (!src || !out))) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad buffers");
+    if (elements % 32) return fail(AHIP_ERR_INVALID_ARGUMENT, "element count must be a multiple of 32");
+    if (elements == 0) return AHIP_OK;
+    if (elements / 32 > (int64_t)1 << 30) return fail(AHIP_ERR_UNSUPPORTED, "too many elements");
+    return with_ctx(ctx, [&](hipStream_t st) -> int {
+        OwnedMatrix M;
+        if (int rc = upload_weight(dtype, src, (int)(elements / 32), 32, M, st)) return rc;
+        DevBuf dout;
+        if (int rc = dout.alloc(elements * 4)) return rc;
+        LAUNCH(launch_dequant(M.m, dout.as<float>(), st));
+        return download(out, dout, elements * 4, st);
+    });
+}
+
+extern "C" int ahip_op_argmax(ahip_context* ctx, const float* logits, int n, int32_t* index) {
+    if (n <= 0 || !logits || !index) return fail(AHIP_ERR_INVALID_ARGUMENT, "empty logits");
+    return with_ctx(ctx, [&](hipStream_t st) -> int {
+        DevBuf dl, di;
+        if (int rc = upload(dl, logits, (size_t)n * 4, st)) return rc;
+        if (int rc = di.alloc(4)) return rc;
+        LAUNCH(launch_argmax(dl.as<float>(), n, di.as<int32_t>(), nullptr, 0, st));
+        return download(index, di, 4, st);
+    });
+}
+
+// ------------------------------------------------------------------ thin HIP shim
+
+extern "C" int ahip_malloc(ahip_context* ctx, int64_t bytes, void** dptr) {
+    if (!ctx || !dptr || bytes < 0) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad argument");
+    HIP_OR(hipSetDevice(ctx->device), "hipSetDevice");
+    if (hipMalloc(dptr, std::max<int64_t>(bytes, 256)) != hipSuccess)
+        return fail(AHIP_ERR_ALLOC, "failed to allocate a " + std::to_string(bytes) + "-byte device buffer");
+    return AHIP_OK;
+}
+extern "C" int ahip_free(ahip_context* ctx, void* dptr) {
+    if (!ctx) return fail(AHIP_ERR_INVALID_ARGUMENT, "null context");
+    if (dptr) HIP_OR(hipFree(dptr), "hipFree");
+    return AHIP_OK;
+}
+extern "C" int ahip_memcpy_htod(ahip_context* ctx, void* dst, const void* src, int64_t bytes) {
+    if (!ctx || bytes < 0) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad argument");
+    HIP_OR(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "memcpy");
+    HIP_OR(hipStreamSynchronize(ctx->stream), "memcpy");
+    return AHIP_OK;
+}
+extern "C" int ahip_memcpy_dtoh(ahip_context* ctx, void* dst, const void* src, int64_t bytes) {
+    if (!ctx || bytes < 0) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad argument");
+    HIP_OR(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "memcpy");
+    HIP_OR(hipStreamSynchronize(ctx->stream), "memcpy");
+    return AHIP_OK;
+}
+extern "C" int ahip_memset(ahip_context* ctx, void* dst, int value, int64_t bytes) {
+    if (!ctx || bytes < 0) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad argument");
+    HIP_OR(hipMemsetAsync(dst, value, bytes, ctx->stream), "memset");
+    HIP_OR(hipStreamSynchronize(ctx->stream), "memset");
+    return AHIP_OK;
+}
+extern "C" int ahip_synchronize(ahip_context* ctx) {
+    if (!ctx) return fail(AHIP_ERR_INVALID_ARGUMENT, "null context");
+    HIP_OR(hipStreamSynchronize(ctx->stream), "synchronize");
+    return AHIP_OK;
+}
+
+extern "C" int ahip_dev_pack_weight(ahip_context* ctx, int dtype, const void* host_w, int rows, int cols, void** handle) {
+    if (!ctx || !host_w || !handle || rows <= 0) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad argument");
+    if (int rc = check_matrix(dtype, cols)) return rc;
+    return with_ctx(ctx, [&](hipStream_t st) -> int {
+        auto om = std::make_unique<OwnedMatrix>();
+        if (int rc = upload_weight(dtype, host_w, rows, cols, *om, st)) return rc;
+        *handle = om.release();
+        return AHIP_OK;
+    });
+}
+extern "C" int ahip_dev_weight_free(ahip_context* ctx, void* handle) {
+    if (!ctx) return fail(AHIP_ERR_INVALID_ARGUMENT, "null context");
+    hipSetDevice(ctx->device);
+    delete (OwnedMatrix*)handle;
+    return AHIP_OK;
+}
+
+template <typename F>
+static int time_launches(ahip_context* ctx, int iters, double* avg, F launch) {
+    hipStream_t st = ctx->stream;
+    hipEvent_t a, b;
+    HIP_OR(hipEventCreate(&a), "hipEventCreate");
+    HIP_OR(hipEventCreate(&b), "hipEventCreate");
+    int rc = AHIP_OK;
+    hipEventRecord(a, st);
+    for (int i = 0; i < iters && rc == AHIP_OK; i++) {
+        hipError_t e = launch(st);
+        if (e != hipSuccess) rc = fail(AHIP_ERR_COMMAND_FAILED, std::string("kernel launch: ") + hipGetErrorString(e));
+    }
+    hipEventRecord(b, st);
+    hipError_t e = hipEventSynchronize(b);
+    if (e != hipSuccess && rc == AHIP_OK) rc = fail(AHIP_ERR_COMMAND_FAILED, hipGetErrorString(e));
+    float ms = 0;
+    hipEventElapsedTime(&ms, a, b);
+    if (avg) *avg = iters > 0 ? ms * 1e-3 / iters : 0.0;
+    hipEventDestroy(a);
+    hipEventDestroy(b);
+    return rc;
+}
+
+extern "C" int ahip_dev_gemv(ahip_context* ctx, void* weight, const float* dx, float* dy, int iters, double* avg) {
+    if (!ctx || !weight || !dx || !dy || iters < 0) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad argument");
+    const DevMatrix& w = ((OwnedMatrix*)weight)->m;
+    HIP_OR(hipSetDevice(ctx->device), "hipSetDevice");
+    return time_launches(ctx, iters, avg, [&](hipStream_t st) {
+        return launch_gemv(w, nullptr, dx, nullptr, 0.f, dy, GEMV_STORE, st);
+    });
+}
+
+extern "C" int ahip_dev_gemm(ahip_context* ctx, void* weight, const float* dx, int m, float* dy, int precision,
+                             int iters, double* avg) {
+    if (!ctx || !weight || !dx || !dy || m <= 0 || iters < 0) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad argument");
+    const DevMatrix& w = ((OwnedMatrix*)weight)->m;
+    HIP_OR(hipSetDevice(ctx->device), "hipSetDevice");
+    if (precision == AHIP_GEMM_FAST) {
+        DevBuf xh;
+        if (int rc = xh.alloc((size_t)m * w.cols * 2)) return rc;
+        LAUNCH(launch_f32_to_f16(dx, xh.as<f16>(), (int64_t)m * w.cols, ctx->stream));
+        return time_launches(ctx, iters, avg, [&](hipStream_t st) {
+            return launch_gemm_mfma(xh.as<f16>(), w.cols, m, w, nullptr, dy, nullptr, w.rows, GEMM_STORE, st);
+        });
+    }
+    return time_launches(ctx, iters, avg, [&](hipStream_t st) {
+        return launch_gemm_f32(dx, w.cols, m, w, nullptr, dy, w.rows, GEMM_STORE, st);
+    });
+}
+
+extern "C" int ahip_dev_attention(ahip_context* ctx, const void* dq, const void* dk, const void* dv, int tokens,
+                                  int heads, int kv_heads, int hd, int start, float* dout, int iters, double* avg) {
+    if (!ctx || !dq || !dk || !dv || !dout || tokens <= 0 || kv_heads <= 0 || heads % kv_heads || iters < 0)
+        return fail(AHIP_ERR_INVALID_ARGUMENT, "bad argument");
+    if (start != 0) return fail(AHIP_ERR_UNSUPPORTED, "device attention timing takes start = 0");
+    if (hd != 64 && hd != 128) return fail(AHIP_ERR_UNSUPPORTED, "flash attention needs head_dim 64 or 128");
+    HIP_OR(hipSetDevice(ctx->device), "hipSetDevice");
+    hipStream_t st = ctx->stream;
+    DevBuf kc, vc;
+    const size_t bytes = (size_t)tokens * kv_heads * hd * 2;
+    if (int rc = kc.alloc(bytes)) return rc;
+    if (int rc = vc.alloc(bytes)) return rc;
+    // [tokens][kv_heads][hd] -> [kv_heads][tokens][hd]
+    for (int h = 0; h < kv_heads; h++) {
+        HIP_OR(hipMemcpy2DAsync(kc.as<uint8_t>() + (size_t)h * tokens * hd * 2, hd * 2,
+                                (const uint8_t*)dk + (size_t)h * hd * 2, (size_t)kv_heads * hd * 2, hd * 2, tokens,
+                                hipMemcpyDeviceToDevice, st), "cache copy");
+        HIP_OR(hipMemcpy2DAsync(vc.as<uint8_t>() + (size_t)h * tokens * hd * 2, hd * 2,
+                                (const uint8_t*)dv + (size_t)h * hd * 2, (size_t)kv_heads * hd * 2, hd * 2, tokens,
+                                hipMemcpyDeviceToDevice, st), "cache copy");
+    }
+    return time_launches(ctx, iters, avg, [&](hipStream_t s2) {
+        return launch_flash_attention((const f16*)dq, heads * hd, kc.as<f16>(), vc.as<f16>(), tokens, tokens, heads,
+                                      kv_heads, hd, 0, dout, nullptr, s2);
+    });
+}

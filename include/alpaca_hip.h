@@ -1,0 +1,255 @@
+/*
+ * alpaca_hip.h -- C ABI of the MI355X (gfx950) backend for alpaca.swift.
+ *
+ * One shared library, libalpaca_hip.so, built from alpaca_amd/csrc/.  It holds
+ * the hand-written HIP kernels of the Llama decoder forward pass and the C++
+ * runtime that orders them (model upload, sessions with a resident KV cache,
+ * chunked prefill, fused decode, device-resident greedy chain, per-stage
+ * timing).  Every entry point takes plain pointers and sizes; nothing here
+ * names a PyTorch or Swift type.
+ *
+ * Each declaration cites the reference interface it replaces
+ * (torinriley/alpaca, file:line).  All functions return an ahip_status; on a
+ * non-zero status ahip_last_error() returns a thread-local message.
+ */
+#ifndef ALPACA_HIP_H
+#define ALPACA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes mirror MetalError (Sources/AlpacaMetal/Backend/MetalContext.swift:7-31). */
+typedef enum {
+    AHIP_OK = 0,
+    AHIP_ERR_NO_DEVICE = 1,        /* MetalError.noDevice */
+    AHIP_ERR_MODULE_LOAD = 2,      /* MetalError.shaderCompilation / shaderSourceMissing */
+    AHIP_ERR_MISSING_KERNEL = 3,   /* MetalError.missingFunction / pipelineCreation */
+    AHIP_ERR_ALLOC = 4,            /* MetalError.bufferAllocation */
+    AHIP_ERR_COMMAND_FAILED = 5,   /* MetalError.commandFailed */
+    AHIP_ERR_UNSUPPORTED = 6,      /* MetalError.unsupported */
+    AHIP_ERR_INVALID_ARGUMENT = 7, /* MetalError.invalidArgument */
+    AHIP_ERR_BUSY = 8              /* re-entrant call on a busy session (MetalLlamaModel.swift:235, :275) */
+} ahip_status;
+
+/* Element formats, Sources/AlpacaCore/Tensor/DType.swift:8-56.
+ * Q8_0: per 32 elements an f16 scale d then 32 int8 q (34 bytes).
+ * Q4_0: per 32 elements an f16 scale d then 16 bytes; byte j holds element j
+ * in its low nibble and element j+16 in its high nibble; value = d*(nib-8). */
+typedef enum { AHIP_F32 = 0, AHIP_F16 = 1, AHIP_Q8_0 = 2, AHIP_Q4_0 = 3 } ahip_dtype;
+
+/* KVPrecision, Sources/AlpacaMetal/Backend/KernelEncoder.swift:9-17. */
+typedef enum { AHIP_KV_F16 = 0, AHIP_KV_F32 = 1 } ahip_kv_precision;
+
+/* GEMMPrecision, KernelEncoder.swift:41-48: exact = float32 operands;
+ * fast = f16 operands on MFMA with float32 accumulation. */
+typedef enum { AHIP_GEMM_EXACT = 0, AHIP_GEMM_FAST = 1 } ahip_gemm_precision;
+
+/* LlamaConfig, Sources/AlpacaCore/Transformer/LlamaConfig.swift:8-20. */
+typedef struct {
+    int32_t vocab_size;
+    int32_t hidden_size;
+    int32_t layer_count;
+    int32_t head_count;
+    int32_t kv_head_count;
+    int32_t head_dim;
+    int32_t feed_forward_size;
+    int32_t context_length;
+    float rms_norm_eps;
+    float rope_theta;
+    int32_t rope_interleaved; /* 1: adjacent pairs (GGUF); 0: split halves (HF) */
+} ahip_llama_config;
+
+/* One weight tensor handed over at model creation, named as in GGUF
+ * (Sources/AlpacaModels/Llama/LlamaLoader.swift:43-67, LlamaWeights.swift:
+ * "token_embd", "output_norm", "output" (absent = tied), "blk.N.attn_norm",
+ * "blk.N.attn_q|attn_k|attn_v|attn_output", "blk.N.ffn_norm",
+ * "blk.N.ffn_gate|ffn_up|ffn_down").  `data` is host memory holding `bytes`
+ * bytes in `dtype`'s on-disk layout; it may be released after the call. */
+typedef struct {
+    const char* name;
+    int32_t dtype;
+    int64_t rows;
+    int64_t cols;
+    const void* data;
+    int64_t bytes;
+} ahip_tensor_desc;
+
+typedef struct ahip_context ahip_context;
+typedef struct ahip_model ahip_model;
+typedef struct ahip_session ahip_session;
+
+/* Per-stage GPU time of the last profiled call (EncoderProvider profiling,
+ * MetalLlamaModel.swift:387-484; lastProfile at :159-160). */
+typedef struct {
+    char label[48];
+    double seconds;
+    int32_t dispatches;
+} ahip_stage;
+
+/* ------------------------------------------------------------ errors, device */
+
+const char* ahip_last_error(void);
+/* Number of visible HIP devices (MetalContext.isAvailable). */
+int ahip_device_count(int* count);
+/* Library build string (arch and compile flags). */
+const char* ahip_version(void);
+
+/* MetalContext.init, MetalContext.swift:37-126: binds one device. */
+int ahip_context_create(int device, ahip_context** out);
+int ahip_context_destroy(ahip_context* ctx);
+
+/* ------------------------------------------------------------ model */
+
+/* MetalLlamaModel.init(context:config:weights:mappedRegion:keepAlive:
+ * prefillWeightCache:), MetalLlamaModel.swift:38-94.  Validates the config
+ * and every tensor shape (LlamaConfig.validate, LlamaWeights.validate), then
+ * copies all tensors to HBM once, repacking Q8_0/Q4_0 blocks into separate
+ * quant and scale streams.  `prefill_weight_cache` is accepted for interface
+ * parity; the MFMA GEMM dequantises blocks in LDS, so no f16 copy is kept. */
+int ahip_model_create(ahip_context* ctx, const ahip_llama_config* config, const ahip_tensor_desc* tensors,
+                      int count, int prefill_weight_cache, ahip_model** out);
+int ahip_model_destroy(ahip_model* model);
+/* Bytes of weights resident in HBM (MetalLlamaModel.copiedWeightBytes, :30-32). */
+int ahip_model_weight_bytes(const ahip_model* model, int64_t* bytes);
+
+/* MetalLlamaModel.sessionByteCount, MetalLlamaModel.swift:123-127. */
+int ahip_session_byte_count(const ahip_llama_config* config, int capacity, int max_batch, int kv_precision,
+                            int64_t* bytes);
+
+/* ------------------------------------------------------------ session */
+
+/* MetalLlamaModel.makeSession(capacity:maxBatch:kvPrecision:gemmPrecision:),
+ * MetalLlamaModel.swift:136-140 / MetalLlamaSession.init :181-217.  capacity
+ * is clamped to the model's context length.  Each session owns its KV cache,
+ * scratch, a pinned logits buffer and its own HIP stream. */
+int ahip_session_create(ahip_model* model, int capacity, int max_batch, int kv_precision, int gemm_precision,
+                        ahip_session** out);
+int ahip_session_destroy(ahip_session* s);
+
+/* MetalLlamaSession.forward(tokens:), MetalLlamaModel.swift:274-305 and
+ * InferenceSession.forward (Sources/Alpaca/LanguageModel.swift:317-328).
+ * Appends `n` tokens at positions length..length+n-1 (chunked by max_batch)
+ * and points *logits at the last position's vocab_size logits, valid until the
+ * next call on `s`.  Fails without advancing length on an empty input, a token
+ * outside the vocabulary or a context overflow. */
+int ahip_session_forward(ahip_session* s, const int32_t* tokens, int n, const float** logits);
+
+/* MetalLlamaSession.decode(token:), MetalLlamaModel.swift:221-226. */
+int ahip_session_decode(ahip_session* s, int32_t token, const float** logits);
+
+/* MetalLlamaSession.decodeGreedy(startToken:maxSteps:depth:emit:),
+ * MetalLlamaModel.swift:228-270.  Feeds `start` at position length, takes the
+ * arg-max on the GPU (lowest index wins ties, NaN never wins) and feeds it
+ * straight back; up to `depth` steps are queued ahead.  `emit` receives each
+ * produced token in order and returns 0 to stop; steps already queued are
+ * drained and discarded.  *fed = tokens consumed, by which length advances
+ * (also on failure). */
+typedef int (*ahip_emit_fn)(void* user, int32_t token);
+int ahip_session_decode_greedy(ahip_session* s, int32_t start, int max_steps, int depth, ahip_emit_fn emit,
+                               void* user, int* fed);
+
+/* MetalLlamaSession.reset / length / capacity / lastGPUSeconds /
+ * lastEncodeSeconds (MetalLlamaModel.swift:151-160, :219). */
+int ahip_session_reset(ahip_session* s);
+int ahip_session_length(const ahip_session* s, int* length);
+int ahip_session_capacity(const ahip_session* s, int* capacity);
+int ahip_session_last_gpu_seconds(const ahip_session* s, double* seconds);
+int ahip_session_last_encode_seconds(const ahip_session* s, double* seconds);
+
+/* profilingEnabled / lastProfile, MetalLlamaModel.swift:156-160: when on,
+ * every stage is bracketed by HIP events on the session stream. */
+int ahip_session_set_profiling(ahip_session* s, int enabled);
+int ahip_session_profile(const ahip_session* s, ahip_stage* out, int capacity, int* count);
+
+/* ------------------------------------------------------------ op-level API
+ * MetalOps, Sources/AlpacaMetal/Backend/MetalOps.swift:11-219: tensor in /
+ * tensor out.  Each call uploads its host operands, runs the same kernels the
+ * session uses, and copies the result back.  Weights are raw on-disk bytes. */
+
+int ahip_op_add(ahip_context* ctx, const float* a, const float* b, int64_t n, float* out);
+int ahip_op_mul(ahip_context* ctx, const float* a, const float* b, int64_t n, float* out);
+int ahip_op_silu(ahip_context* ctx, const float* x, int64_t n, float* out);
+int ahip_op_silu_mul(ahip_context* ctx, const float* gate, const float* up, int64_t n, float* out);
+int ahip_op_rmsnorm(ahip_context* ctx, const float* x, const float* weight, int rows, int dim, float eps,
+                    float* out);
+/* y[m,n] = x[m,k] * W[n,k]^T (MetalOps.linear, :50-67). */
+int ahip_op_linear(ahip_context* ctx, const float* x, int m, int k, int dtype, const void* w, int n,
+                   int gemm_precision, float* y);
+/* residual[m,n] += x * W^T in place (MetalOps.linearAdd, :69-84). */
+int ahip_op_linear_add(ahip_context* ctx, const float* x, int m, int k, int dtype, const void* w, int n,
+                       int gemm_precision, float* residual);
+/* silu(x*Wg^T) * (x*Wu^T) (MetalOps.gateUpSilu, :86-105). */
+int ahip_op_gate_up_silu(ahip_context* ctx, const float* x, int m, int k, int dtype, const void* wg,
+                         const void* wu, int n, int gemm_precision, float* out);
+/* RoPE in place on x[tokens, heads, hd] (MetalOps.rope, :107-114). */
+int ahip_op_rope(ahip_context* ctx, float* x, int tokens, int heads, int head_dim, int start, float theta,
+                 int interleaved);
+/* Causal GQA attention (MetalOps.attention, :116-148).  q [tokens, heads, hd];
+ * keys/values [capacity, kv_heads, hd] f32, stored into the cache format
+ * selected by kv_precision; out [tokens, heads, hd]. */
+int ahip_op_attention(ahip_context* ctx, const float* q, int tokens, int heads, int head_dim, const float* keys,
+                      const float* values, int capacity, int kv_heads, int start, int kv_precision,
+                      int gemm_precision, float* out);
+/* Embedding gather + dequant (MetalOps.embed, :150-160). */
+int ahip_op_embed(ahip_context* ctx, const int32_t* tokens, int count, int dtype, const void* table, int vocab,
+                  int dim, float* out);
+/* Block dequantisation of `elements` values (Quantization.swift:9-35 on GPU). */
+int ahip_op_dequantize(ahip_context* ctx, int dtype, const void* src, int64_t elements, float* out);
+/* GPU arg-max, lowest index on ties, NaN never wins (norm_embed.metal:93-121). */
+int ahip_op_argmax(ahip_context* ctx, const float* logits, int n, int32_t* index);
+
+/* Host block quantiser, Quantization.swift:39-73 (ggml quantize_row_*_ref):
+ * count must be a multiple of 32; writes count/32 blocks into out. */
+int ahip_quantize(int dtype, const float* values, int64_t count, void* out);
+
+/* Seeded synthetic inputs (SplitMix64, Sources/AlpacaCore/Runtime/
+ * Sampler.swift:30-40).  Element i of a stream uses the generator state after
+ * `offset + i` steps (normal: 2 steps per value pair):
+ *   uniform   u = (next() >> 11) * 2^-53 in [0,1)
+ *   normal    Box-Muller in double on pairs (u1, u2): r = sqrt(-2 ln(1-u1)),
+ *             z0 = r cos(2 pi u2), z1 = r sin(2 pi u2), scaled by std
+ *   integers  next() % range                                            */
+int ahip_synth_uniform(uint64_t seed, uint64_t offset, int64_t n, float lo, float hi, float* out);
+int ahip_synth_normal(uint64_t seed, uint64_t offset, int64_t n, float std, float* out);
+int ahip_synth_ints(uint64_t seed, uint64_t offset, int64_t n, uint64_t range, int64_t bias, int32_t* out);
+
+/* ------------------------------------------------------------ thin HIP shim
+ * The device-memory / stream / event surface the Swift C target wraps
+ * (north star: "a SwiftPM C target wrapping hipMalloc, ... streams and
+ * events").  Used by the bench harness to time kernels on device-resident
+ * inputs. */
+int ahip_malloc(ahip_context* ctx, int64_t bytes, void** dptr);
+int ahip_free(ahip_context* ctx, void* dptr);
+int ahip_memcpy_htod(ahip_context* ctx, void* dst, const void* src, int64_t bytes);
+int ahip_memcpy_dtoh(ahip_context* ctx, void* dst, const void* src, int64_t bytes);
+int ahip_memset(ahip_context* ctx, void* dst, int value, int64_t bytes);
+int ahip_synchronize(ahip_context* ctx);
+
+/* Device-resident kernel launches on the context stream, timed with HIP events
+ * recorded on that stream around `iters` back-to-back launches: *avg_seconds
+ * is the mean launch duration.  These run exactly the kernels the session
+ * uses, for the bench's roofline figures. */
+
+/* Decode GEMV: y[n] = W[n,k] x[k] with W in the repacked device layout made
+ * by ahip_dev_pack_weight. */
+int ahip_dev_pack_weight(ahip_context* ctx, int dtype, const void* host_w, int rows, int cols, void** handle);
+int ahip_dev_weight_free(ahip_context* ctx, void* handle);
+int ahip_dev_gemv(ahip_context* ctx, void* weight, const float* dx, float* dy, int iters, double* avg_seconds);
+/* Prefill GEMM: y[m,n] = x[m,k] W^T; x given as f32 on device, converted to
+ * f16 once before timing (fast path) or used as f32 (exact). */
+int ahip_dev_gemm(ahip_context* ctx, void* weight, const float* dx, int m, float* dy, int gemm_precision,
+                  int iters, double* avg_seconds);
+/* Causal GQA flash attention over device f16 q [t, heads, hd] and a cache
+ * filled from device f16 k/v [t, kv_heads, hd]; writes f32 out. */
+int ahip_dev_attention(ahip_context* ctx, const void* dq, const void* dk, const void* dv, int tokens, int heads,
+                       int kv_heads, int head_dim, int start, float* dout, int iters, double* avg_seconds);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ALPACA_HIP_H */

@@ -1,0 +1,197 @@
+"""HIP kernels vs the CPU oracle, through the C ABI (HIPOps = MetalOps mirror).
+
+Shapes and tolerances follow Tests/AlpacaMetalTests/KernelTests.swift.  Where
+this backend's arithmetic matches the CPU reference operation for operation
+(dequantisation, embedding, RoPE with the double-precision table, the exact
+float32 GEMM), the check is bit-for-bit.
+"""
+import numpy as np
+import pytest
+
+import oracle.oracle as orc
+from alpaca_amd.tensor import F16, Q4_0, Q8_0, encode
+from tests.helpers import assert_close, b64, fixture, metrics, splitmix_uniform
+
+pytestmark = pytest.mark.gpu
+
+FORMATS = [("f16", F16), ("q8_0", Q8_0), ("q4_0", Q4_0)]
+
+
+def rand(shape, seed, scale=1.0):
+    n = int(np.prod(shape))
+    return (splitmix_uniform(seed, n) * np.float32(scale)).reshape(shape)
+
+
+def test_elementwise(hip_ops):  # KernelTests.swift:37-43
+    a, b = rand((7, 37), 1, 3), rand((7, 37), 2, 3)
+    assert_close(hip_ops.add(a, b), orc.add(a, b), 1e-6, 1e-6, "add")
+    assert_close(hip_ops.mul(a, b), orc.mul(a, b), 1e-6, 1e-6, "mul")
+    assert_close(hip_ops.silu(a), orc.silu(a), 1e-6, 1e-5, "silu")
+    assert_close(hip_ops.silu_mul(a, b), orc.mul(orc.silu(a), b), 1e-5, 1e-5, "silu*mul")
+
+
+@pytest.mark.parametrize("dim", [32, 576, 1536, 2048])
+def test_rmsnorm(hip_ops, dim):  # KernelTests.swift:45-50
+    x, w = rand((5, dim), 3, 2), rand((dim,), 4)
+    assert_close(hip_ops.rms_norm(x, w, 1e-5), orc.rmsnorm(x, w, 1e-5), 1e-5, 1e-5, f"rmsnorm {dim}")
+
+
+@pytest.mark.parametrize("k,n", [(64, 10), (576, 193), (1536, 576)])
+@pytest.mark.parametrize("name,dt", FORMATS)
+def test_linear_all_formats_and_batch_sizes(hip_ops, k, n, name, dt):  # KernelTests.swift:52-66
+    w32 = rand((n, k), 5, 0.3)
+    w = encode(w32, dt)
+    for t in [1, 3, 8, 11, 16, 33, 70]:
+        x = rand((t, k), 6 + t)
+        cpu = orc.linear(x, dt, w.data, n)
+        gpu = hip_ops.linear(x, w, "exact")
+        assert_close(gpu, cpu, 2e-4, 1e-4, f"linear {name} K={k} N={n} T={t}")
+        if t > 1:
+            # exact GEMM: same per-block float32 order as CPUOps.dot -> identical bits
+            assert np.array_equal(gpu.view(np.uint32), cpu.view(np.uint32)), f"exact GEMM bits {name} T={t}"
+
+
+@pytest.mark.parametrize("k,n", [(64, 10), (576, 193), (1536, 576), (576, 1536)])
+@pytest.mark.parametrize("name,dt", FORMATS)
+def test_fast_gemm_within_analytic_bound(hip_ops, k, n, name, dt):  # KernelTests.swift:179-217
+    """f16 operands: |err| <= 2^-10 * sum_k |x_k w_k| + 1e-5 element-wise."""
+    w32 = rand((n, k), k * 31 + n, 0.3)
+    w = encode(w32, dt)
+    wd = orc.dequantize(dt, w.data, n * k).reshape(n, k).astype(np.float64)
+    worst = 0.0
+    for t in [16, 32, 33, 70, 130, 300]:
+        x = rand((t, k), 1000 + t)
+        gpu = hip_ops.linear(x, w, "fast").astype(np.float64)
+        cpu = orc.linear(x, dt, w.data, n).astype(np.float64)
+        bound = np.abs(x.astype(np.float64)) @ np.abs(wd).T / 1024 + 1e-5
+        err = np.abs(gpu - cpu)
+        worst = max(worst, float((err / bound).max()))
+        assert (err <= bound).all(), f"fast GEMM {name} K={k} N={n} T={t}: worst ratio {(err / bound).max()}"
+    print(f"[metrics] fast GEMM {name} K={k} N={n}: worst error / bound = {worst:.3f}")
+
+
+def test_fused_gate_up_silu(hip_ops):  # KernelTests.swift:219-244
+    k, n = 576, 200
+    for t in [1, 3, 16, 40, 100]:
+        x = rand((t, k), 77 + t)
+        g32, u32 = rand((n, k), 78, 0.3), rand((n, k), 79, 0.3)
+        for name, dt in FORMATS:
+            wg, wu = encode(g32, dt), encode(u32, dt)
+            cpu = orc.mul(orc.silu(orc.linear(x, dt, wg.data, n)), orc.linear(x, dt, wu.data, n))
+            for prec in ("exact", "fast"):
+                gpu = hip_ops.gate_up_silu(x, wg, wu, prec)
+                m = metrics(gpu, cpu)
+                print(f"[metrics] gate+up+silu T={t} {name} {prec}: {m}")
+                if prec == "exact" or t < 16:
+                    assert m["max_abs"] < 1e-3
+                else:
+                    assert m["max_rel_peak"] < 3e-3
+
+
+def test_fused_residual_projection(hip_ops):  # KernelTests.swift:246-267
+    k, n = 576, 576
+    for t in [1, 5, 8, 31, 40, 100]:
+        x, res = rand((t, k), 200 + t), rand((t, n), 300 + t, 5)
+        for name, dt in FORMATS:
+            w = encode(rand((n, k), 400, 0.3), dt)
+            cpu = orc.add(res, orc.linear(x, dt, w.data, n))
+            for prec in ("exact", "fast"):
+                gpu = hip_ops.linear_add(x, w, res, prec)
+                bound = 2e-4 if prec == "exact" or t < 16 else 2e-2
+                assert metrics(gpu, cpu)["max_abs"] < bound, f"linear+residual {name} {prec} T={t}"
+
+
+@pytest.mark.parametrize("start,theta", [(0, 10000.0), (7, 100000.0), (1500, 100000.0)])
+def test_rope_bit_exact(hip_ops, start, theta):  # KernelTests.swift:68-74
+    x = rand((4, 9, 64), 9)
+    for inter in (True, False):
+        gpu, cpu = hip_ops.rope(x, start, theta, inter), orc.rope(x, start, theta, inter)
+        assert np.array_equal(gpu.view(np.uint32), cpu.view(np.uint32)), f"rope start={start} interleaved={inter}"
+
+
+def _f16(a):
+    return a.astype(np.float16).astype(np.float32)
+
+
+@pytest.mark.parametrize("tokens,start,heads,kv,hd", [(1, 0, 4, 2, 64), (1, 100, 9, 3, 64), (5, 0, 9, 3, 64),
+                                                      (7, 20, 8, 2, 128), (3, 1, 6, 6, 32)])
+def test_attention_causal_gqa(hip_ops, tokens, start, heads, kv, hd):  # KernelTests.swift:76-88
+    cap = start + tokens + 3
+    q, k, v = rand((tokens, heads, hd), 11), rand((cap, kv, hd), 12), rand((cap, kv, hd), 13)
+    cpu16 = orc.attention(q, _f16(k), _f16(v), start)
+    assert_close(hip_ops.attention(q, k, v, start, "f16"), cpu16, 2e-5, 1e-4, f"attention f16-KV T={tokens}")
+    cpu32 = orc.attention(q, k, v, start)
+    assert_close(hip_ops.attention(q, k, v, start, "f32"), cpu32, 2e-6, 1e-5, f"attention f32-KV T={tokens}")
+
+
+SPLIT_CASES = [(0, 9, 3, 64), (1, 9, 3, 64), (7, 9, 3, 64), (255, 9, 3, 64), (256, 9, 3, 64), (257, 9, 3, 64),
+               (511, 9, 3, 64), (1000, 9, 3, 64), (2047, 9, 3, 64), (300, 8, 2, 128), (700, 8, 8, 64),
+               (90, 32, 4, 128), (500, 4, 1, 64), (4095, 15, 5, 64)]
+
+
+@pytest.mark.parametrize("start,heads,kv,hd", SPLIT_CASES)
+def test_split_decode_attention(hip_ops, start, heads, kv, hd):  # KernelTests.swift:123-144
+    cap = start + 1
+    q = rand((1, heads, hd), start * 7 + heads)
+    k = rand((cap, kv, hd), start * 7 + heads + 1)
+    v = rand((cap, kv, hd), start * 7 + heads + 2)
+    cpu = orc.attention(q, _f16(k), _f16(v), start)
+    gpu = hip_ops.attention(q, k, v, start, "f16")
+    m = metrics(gpu, cpu)
+    print(f"[metrics] split decode attention ctx={cap} H={heads}/{kv} hd={hd}: {m}")
+    assert m["max_abs"] < 2e-6
+
+
+TILED = [(8, 0, 9, 3, 64), (31, 0, 9, 3, 64), (32, 0, 9, 3, 64), (33, 0, 9, 3, 64), (100, 0, 9, 3, 64),
+         (64, 200, 9, 3, 64), (45, 7, 8, 2, 128), (128, 128, 4, 4, 128), (17, 3, 6, 3, 64), (200, 0, 8, 2, 64),
+         (16, 0, 9, 3, 64), (300, 40, 15, 5, 64)]
+
+
+@pytest.mark.parametrize("t,start,heads,kv,hd", TILED)
+def test_flash_attention(hip_ops, t, start, heads, kv, hd):  # KernelTests.swift:146-170
+    """f16 Q / P / V on MFMA: <= 1.5e-3 against float64-accurate CPU on the same f16 K/V."""
+    cap = start + t
+    q, k, v = rand((t, heads, hd), t * 131 + start), rand((cap, kv, hd), t * 131 + start + 1), \
+        rand((cap, kv, hd), t * 131 + start + 2)
+    cpu = orc.attention(q, _f16(k), _f16(v), start)
+    for prec in ("exact", "fast"):
+        gpu = hip_ops.attention(q, k, v, start, "f16", prec)
+        m = metrics(gpu, cpu)
+        print(f"[metrics] attention {prec} T={t} start={start} H={heads}/{kv} hd={hd}: {m}")
+        assert np.isfinite(gpu).all()
+        assert m["max_abs"] < 1.5e-3
+
+
+@pytest.mark.parametrize("name,dt", FORMATS)
+def test_embedding_all_formats(hip_ops, name, dt):  # KernelTests.swift:90-99
+    table = rand((50, 96), 21)
+    t = encode(table, dt)
+    tokens = [0, 49, 7, 7]
+    cpu = orc.embed(tokens, dt, t.data, 50, 96)
+    gpu = hip_ops.embed(tokens, t)
+    assert np.array_equal(gpu.view(np.uint32), cpu.view(np.uint32))
+    with pytest.raises(ValueError):
+        hip_ops.embed([50], t)
+
+
+@pytest.mark.parametrize("name", ["q8_0", "q4_0"])
+def test_dequantize_bit_exact_against_gguf(hip_ops, name):
+    c = fixture("ops")[name]
+    dt = Q8_0 if name == "q8_0" else Q4_0
+    from alpaca_amd.tensor import QTensor
+    t = QTensor(dt, c["n"], c["k"], b64(c["blocks"]))
+    gpu = hip_ops.dequantize(t).ravel()
+    assert np.array_equal(gpu.astype(np.float64), np.asarray(c["dequantized"], np.float64))
+    big = encode(rand((64, 4096), 33, 2.0), dt)
+    assert np.array_equal(hip_ops.dequantize(big).ravel(), orc.dequantize(dt, big.data, 64 * 4096))
+
+
+def test_argmax_rules(hip_ops):
+    assert hip_ops.argmax([1.0, 3.0, 3.0, 2.0]) == 1
+    assert hip_ops.argmax([np.nan, 1.0, np.nan, 5.0, 5.0]) == 3  # NaN never wins
+    assert hip_ops.argmax([np.nan, np.nan]) == 0
+    assert hip_ops.argmax([-np.inf, -np.inf, -1.0]) == 2
+    v = rand((49152,), 5)
+    v[31337] = 10.0
+    v[40000] = 10.0
+    assert hip_ops.argmax(v) == 31337 == orc.argmax(v)
