@@ -6,9 +6,11 @@
 // KernelEncoder.swift:192-280.  CPU semantics: CPUOps.linear / dot
 // (CPUOps.swift:77-139).
 //
-// gemm_mfma_kernel (fast): f16 activations, weights dequantised block by block
-// (32 weights share one f16 scale) into f16 tiles in LDS, v_mfma_f32_16x16x32_f16
-// with float32 accumulation.  256 threads = 2x2 waves; BK = 64 (two quant
+// gemm_mfma_kernel (fast): f16 activations; quantised weights staged in LDS as
+// their integer quants in f16 (exact) with the per-block f16 scale kept in
+// float32; one v_mfma_f32_16x16x32_f16 covers one 32-weight block and its
+// result is scaled by d before accumulation, so the only rounding on the
+// inputs is the activations' (float32 -> f16).  256 threads = 2x2 waves; BK = 64 (two quant
 // blocks) per LDS stage, double-buffered: the next stage's global loads are in
 // registers while the current stage is multiplied, one barrier per stage.
 // Epilogues: store f32, accumulate into the f32 residual, or SwiGLU
@@ -58,24 +60,27 @@ __device__ __forceinline__ void b_load(const DevMatrix& m, int n, int k, int K, 
     }
 }
 
-// Dequantise a unit to 16 halves: d*q rounded to f16 (tensor_gemm.metal:87-112).
+// Stores a unit as 16 halves.  Quantised formats store the integer quants
+// (q for Q8_0, nib-8 for Q4_0), which f16 holds exactly; the block scale d is
+// kept in float32 and applied to each block's MFMA result, so the weights
+// enter the product without rounding.  F16 weights are stored as they are.
 template <int FMT>
-__device__ __forceinline__ void b_store(const BUnit<FMT>& u, int k, f16* dst) {
+__device__ __forceinline__ void b_store(const BUnit<FMT>& u, int k, f16* dst, float* dscale) {
     f16x8 h0, h1;
     if (FMT == DT_Q8_0) {
         const int8_t* q = (const int8_t*)&u.q0;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            h0[j] = (f16)(u.d * (float)q[j]);
-            h1[j] = (f16)(u.d * (float)q[8 + j]);
+            h0[j] = (f16)(float)q[j];
+            h1[j] = (f16)(float)q[8 + j];
         }
     } else if (FMT == DT_Q4_0) {
         const uint8_t* q = (const uint8_t*)&u.q0;
         const int sh = (k & 16) ? 4 : 0;  // low nibbles: elements 0..15 of the block, high: 16..31
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            h0[j] = (f16)(u.d * (float)((int)((q[j] >> sh) & 15) - 8));
-            h1[j] = (f16)(u.d * (float)((int)((q[8 + j] >> sh) & 15) - 8));
+            h0[j] = (f16)(float)((int)((q[j] >> sh) & 15) - 8);
+            h1[j] = (f16)(float)((int)((q[8 + j] >> sh) & 15) - 8);
         }
     } else {
         h0 = *(const f16x8*)&u.q0;
@@ -83,18 +88,21 @@ __device__ __forceinline__ void b_store(const BUnit<FMT>& u, int k, f16* dst) {
     }
     *(f16x8*)dst = h0;
     *(f16x8*)(dst + 8) = h1;
+    if (FMT != DT_F16 && (k & 16) == 0) *dscale = u.d;
 }
 
 template <int FMT, int BM, int BN, int MODE>
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs p) {
+__global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmArgs p) {
     constexpr int NB = MODE == GEMM_SWIGLU ? 2 : 1;
     constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16;
     constexpr int SA = BM * (BK / 8) / 256;  // 16-byte A segments per thread
     constexpr int UB = BN * (BK / 16) / 256; // 16-weight B units per thread per matrix
     static_assert(SA >= 1 && UB >= 1, "tile too small for 256 threads");
 
+    constexpr bool kQuant = FMT != DT_F16;
     __shared__ __attribute__((aligned(16))) f16 As[2][BM][LDT];
     __shared__ __attribute__((aligned(16))) f16 Bs[2][NB][BN][LDT];
+    __shared__ float Ds[2][NB][BN][BK / 32];  // block scales of the stage
 
     const int K = p.w.cols, N = p.w.rows, M = p.M;
     const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
@@ -139,7 +147,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs p) {
 #pragma unroll
             for (int i = 0; i < UB; i++) {
                 const int unit = tid + 256 * i, r = unit >> 2, kk = (unit & 3) * 16;
-                b_store<FMT>(rb[mat][i], kt * BK + kk, &Bs[buf][mat][r][kk]);
+                b_store<FMT>(rb[mat][i], kt * BK + kk, &Bs[buf][mat][r][kk], &Ds[buf][mat][r][kk >> 5]);
             }
     };
 
@@ -167,10 +175,24 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs p) {
             for (int mat = 0; mat < NB; mat++)
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
-                    f16x8 bf = *(const f16x8*)&Bs[cur][mat][wn * WN + 16 * j + (lane & 15)][32 * kk + 8 * (lane >> 4)];
+                    const int br = wn * WN + 16 * j + (lane & 15);
+                    f16x8 bf = *(const f16x8*)&Bs[cur][mat][br][32 * kk + 8 * (lane >> 4)];
+                    if (kQuant) {
+                        // One 16x16x32 MFMA spans exactly one quant block: exact integer
+                        // products summed in float32, then scaled once by the block's d.
+                        const float d = Ds[cur][mat][br][kk];
 #pragma unroll
-                    for (int i = 0; i < TM; i++)
-                        acc[mat][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, acc[mat][i][j], 0, 0, 0);
+                        for (int i = 0; i < TM; i++) {
+                            const f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                            acc[mat][i][j] += d * t;
+                        }
+                        // keep one column tile of block results live at a time (register budget)
+                        __builtin_amdgcn_sched_barrier(0);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < TM; i++)
+                            acc[mat][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, acc[mat][i][j], 0, 0, 0);
+                    }
                 }
         }
         if (kt + 1 < nk) sstore(cur ^ 1, kt + 1);
@@ -206,17 +228,29 @@ hipError_t run_mfma(const GemmArgs& a, int mode, hipStream_t st) {
     dim3 grid((a.M + BM - 1) / BM, (a.w.rows + BN - 1) / BN);
     if (mode == GEMM_STORE) gemm_mfma_kernel<FMT, BM, BN, GEMM_STORE><<<grid, 256, 0, st>>>(a);
     else if (mode == GEMM_ACC) gemm_mfma_kernel<FMT, BM, BN, GEMM_ACC><<<grid, 256, 0, st>>>(a);
-    else gemm_mfma_kernel<FMT, BM, BN, GEMM_SWIGLU><<<grid, 256, 0, st>>>(a);
     return hipGetLastError();
 }
 
+template <int FMT, int BM, int BN>
+hipError_t run_mfma_swiglu(const GemmArgs& a, hipStream_t st) {
+    dim3 grid((a.M + BM - 1) / BM, (a.w.rows + BN - 1) / BN);
+    gemm_mfma_kernel<FMT, BM, BN, GEMM_SWIGLU><<<grid, 256, 0, st>>>(a);
+    return hipGetLastError();
+}
+
+// Tiles: 64x64 for short batches and for SwiGLU (two accumulator sets);
+// otherwise 128 tokens x 64 rows (quantised formats keep two waves per SIMD
+// there: the per-block scaling holds a second set of MFMA results in
+// registers), and 128x128 for F16 weights when the grid covers the chip twice.
 template <int FMT>
 hipError_t pick_tile(const GemmArgs& a, int mode, hipStream_t st) {
     const int M = a.M, N = a.w.rows;
+    if (mode == GEMM_SWIGLU) return run_mfma_swiglu<FMT, 64, 64>(a, st);
     if (M <= 64) return run_mfma<FMT, 64, 64>(a, mode, st);
-    if (mode == GEMM_SWIGLU) return run_mfma<FMT, 128, 64>(a, mode, st);
     const long big = (long)((M + 127) / 128) * ((N + 127) / 128);
-    if (big >= 512) return run_mfma<FMT, 128, 128>(a, mode, st);
+    if constexpr (FMT == DT_F16) {
+        if (big >= 512) return run_mfma<FMT, 128, 128>(a, mode, st);
+    }
     return run_mfma<FMT, 128, 64>(a, mode, st);
 }
 

@@ -346,6 +346,7 @@ static std::vector<float2> rope_table(int positions, int hd, float theta) {
 
 struct ahip_model {
     ahip_context* ctx = nullptr;
+    int device = 0;  // kept so destruction never touches a destroyed context
     ahip_llama_config c{};
     struct Layer {
         DevBuf attn_norm, ffn_norm;
@@ -416,6 +417,7 @@ extern "C" int ahip_model_create(ahip_context* ctx, const ahip_llama_config* con
     HIP_OR(hipSetDevice(ctx->device), "hipSetDevice");
     auto m = std::make_unique<ahip_model>();
     m->ctx = ctx;
+    m->device = ctx->device;
     m->c = c;
     hipStream_t st = ctx->stream;
     const ahip_tensor_desc *te, *tn, *to = nullptr;
@@ -473,7 +475,7 @@ extern "C" int ahip_model_create(ahip_context* ctx, const ahip_llama_config* con
 
 extern "C" int ahip_model_destroy(ahip_model* m) {
     if (!m) return AHIP_OK;
-    hipSetDevice(m->ctx->device);
+    hipSetDevice(m->device);
     delete m;
     return AHIP_OK;
 }
@@ -612,7 +614,7 @@ extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, i
     const ahip_llama_config& c = m->c;
     capacity = std::min(capacity, c.context_length);
     max_batch = std::min(max_batch, capacity);
-    HIP_OR(hipSetDevice(m->ctx->device), "hipSetDevice");
+    HIP_OR(hipSetDevice(m->device), "hipSetDevice");
     auto s = std::make_unique<ahip_session>();
     s->m = m;
     s->capacity = capacity;
@@ -645,7 +647,7 @@ extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, i
 
 extern "C" int ahip_session_destroy(ahip_session* s) {
     if (!s) return AHIP_OK;
-    hipSetDevice(s->m->ctx->device);
+    hipSetDevice(s->m->device);
     delete s;
     return AHIP_OK;
 }
@@ -781,7 +783,7 @@ extern "C" int ahip_session_forward(ahip_session* s, const int32_t* tokens, int 
         return fail(AHIP_ERR_INVALID_ARGUMENT, "context exhausted: " + std::to_string(s->length) + " cached + " +
                                                    std::to_string(n) + " new > capacity " + std::to_string(s->capacity));
     if (int rc = validate_tokens(s, tokens, n)) return rc;
-    HIP_OR(hipSetDevice(s->m->ctx->device), "hipSetDevice");
+    HIP_OR(hipSetDevice(s->m->device), "hipSetDevice");
     s->begin_call();
     const auto t0 = std::chrono::steady_clock::now();
     std::memcpy(s->tokens_host, tokens, (size_t)n * 4);
@@ -824,7 +826,7 @@ extern "C" int ahip_session_decode_greedy(ahip_session* s, int32_t start, int ma
     const int budget = std::min(max_steps, s->capacity - s->length);
     if (budget <= 0) return AHIP_OK;
     depth = std::max(1, std::min(depth, 8));
-    HIP_OR(hipSetDevice(s->m->ctx->device), "hipSetDevice");
+    HIP_OR(hipSetDevice(s->m->device), "hipSetDevice");
     s->begin_call();
     hipStream_t st = s->stream;
     s->tokens_host[0] = start;

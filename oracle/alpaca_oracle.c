@@ -496,6 +496,23 @@ void orc_kv_destroy(orc_kvcache* kv) {
 }
 int orc_kv_length(const orc_kvcache* kv) { return kv->length; }
 void orc_kv_reset(orc_kvcache* kv) { kv->length = 0; } /* KVCache.swift:71-73 */
+
+/* Benchmark helper (no reference counterpart): marks `length` rows valid and
+ * fills them with small deterministic values, so a decode step at a long
+ * context can be timed without first prefilling that context. */
+int orc_kv_fill(orc_kvcache* kv, int length, uint64_t seed) {
+    if (length < 0 || length > kv->capacity) return -1;
+    size_t n = (size_t)length * kv->kv_heads * kv->head_dim;
+    for (int l = 0; l < kv->layers; l++)
+        for (size_t i = 0; i < n; i++) {
+            uint64_t st = seed + (uint64_t)l * 0x100000000ull + i;
+            float u = (float)((orc_splitmix_next(&st) >> 40) * (1.0 / 16777216.0)) - 0.5f;
+            kv->keys[l][i] = u;
+            kv->values[l][i] = -u;
+        }
+    kv->length = length;
+    return 0;
+}
 const float* orc_kv_keys(const orc_kvcache* kv, int layer) { return kv->keys[layer]; }
 const float* orc_kv_values(const orc_kvcache* kv, int layer) { return kv->values[layer]; }
 

@@ -65,6 +65,7 @@ def lib():
             "orc_kv_destroy": (None, [vp]),
             "orc_kv_length": (C.c_int, [vp]),
             "orc_kv_reset": (None, [vp]),
+            "orc_kv_fill": (C.c_int, [vp, C.c_int, C.c_uint64]),
             "orc_kv_keys": (fp, [vp, C.c_int]),
             "orc_kv_values": (fp, [vp, C.c_int]),
             "orc_forward": (C.c_int, [vp, vp, ip, C.c_int, C.c_int, fp]),
@@ -319,6 +320,11 @@ class OracleKV:
 
     def reset(self) -> None:
         lib().orc_kv_reset(self.h)
+
+    def fill(self, length: int, seed: int = 0) -> None:
+        """Benchmark helper: `length` synthetic valid rows (no prefill needed)."""
+        if lib().orc_kv_fill(self.h, length, seed) != 0:
+            raise ValueError("fill length exceeds capacity")
 
     def keys(self, layer: int) -> np.ndarray:
         p = lib().orc_kv_keys(self.h, layer)
