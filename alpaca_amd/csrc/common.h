@@ -61,8 +61,10 @@ hipError_t launch_rmsnorm(const float* x, const float* w, float* out_f32, f16* o
                           float eps, hipStream_t st);
 hipError_t launch_embed(const int32_t* tokens, int count, const DevMatrix& table, float* out, hipStream_t st);
 hipError_t launch_dequant(const DevMatrix& m, float* out, hipStream_t st);
+// Greedy arg-max.  Writes the token to *chain_token and emitted[slot] (slot =
+// *pos_dev when pos_dev is set, which is then advanced by one).
 hipError_t launch_argmax(const float* logits, int n, int32_t* chain_token, int32_t* emitted, int slot,
-                         hipStream_t st);
+                         int* pos_dev, hipStream_t st);
 // RoPE with a host-built (cos, sin) table [positions][hd/2]; q rotated in
 // place (q_f32) and/or written as f16 (q_f16); k rotated and v copied into the
 // caches at rows start..start+tokens-1.  k/v may be null (q-only RoPE).
@@ -71,7 +73,31 @@ hipError_t launch_rope_store(float* qkv, int ld, int tokens, int heads, int kv_h
                              void* vcache, int kv_f16, int capacity, hipStream_t st);
 
 // decode GEMV (kernels_gemv.hip)
-enum { GEMV_STORE = 0, GEMV_ADD = 1, GEMV_SWIGLU = 2 };
+enum { GEMV_STORE = 0, GEMV_ADD = 1, GEMV_SWIGLU = 2, GEMV_QKV_ROPE = 3 };
+// Input row: x, RMS-normalised x (norm != null), or the merge of split-K
+// decode-attention partials [heads][splits][hd+2] (partials != null; with
+// pos_dev set, only the splits covering positions 0..*pos_dev are read).
+struct GemvInput {
+    const float* x = nullptr;
+    const float* norm = nullptr;
+    float eps = 0.f;
+    const float* partials = nullptr;
+    int heads = 0, splits = 0, hd = 0, split_len = 0;
+    const int* pos_dev = nullptr;
+};
+// QKV epilogue: rows [q | k | v] (q/k in adjacent RoPE pairs); q is rotated
+// into out[0..QW), k rotated and v copied into the caches at row pos (taken
+// from *pos_dev when set).
+struct GemvRope {
+    const float2* table = nullptr;
+    int heads = 0, kv_heads = 0, hd = 0, capacity = 0, pos = 0;
+    const int* pos_dev = nullptr;
+    void* kc = nullptr;
+    void* vc = nullptr;
+    int kv_f16 = 1;
+};
+hipError_t launch_gemv_ex(const DevMatrix& w, const DevMatrix* w_up, const GemvInput& in, const GemvRope* rope,
+                          float* out, int mode, hipStream_t st);
 hipError_t launch_gemv(const DevMatrix& w, const DevMatrix* w_up, const float* x, const float* norm, float eps,
                        float* out, int mode, hipStream_t st);
 
@@ -94,6 +120,19 @@ hipError_t launch_flash_attention(const f16* q, int ldq, const f16* kc, const f1
 // split into `splits` ranges merged by a second kernel when splits > 1.
 int attention_splits(int length, int heads, int tokens);
 size_t attention_partial_floats(int heads, int tokens, int splits, int hd);
+// Decode (one query token at position length-1): split-K over the context,
+// one workgroup per (KV head, split) for all query heads of the group; writes
+// per-split partials [heads][splits][hd+2] merged by launch_attention_merge or
+// by the Wo GEMV prologue.  Needs hd 64/128, heads/kv_heads <= 16.
+// Context length = *pos_dev + 1 when pos_dev is set (device-side position),
+// else `length`; `splits` workgroups of split_len positions (<= 256) each.
+bool attention_decode_supported(int heads, int kv_heads, int hd);
+int attention_decode_split_len(int capacity);
+int attention_decode_max_split_len();
+hipError_t launch_attention_decode(const float* q, const void* kc, const void* vc, int kv_f16, int capacity,
+                                   int heads, int kv_heads, int hd, int length, const int* pos_dev, int split_len,
+                                   int splits, float* partials, hipStream_t st);
+hipError_t launch_attention_merge(const float* partials, int heads, int hd, int splits, float* out, hipStream_t st);
 hipError_t launch_attention_generic(const float* q, int ldq, const void* kc, const void* vc, int kv_f16,
                                     int capacity, int tokens, int heads, int kv_heads, int hd, int start,
                                     int splits, float* partials, float* out, hipStream_t st);

@@ -247,6 +247,146 @@ __global__ void attn_merge_kernel(const float* partials, int H, int hd, int spli
     }
 }
 
+// ------------------------------------------------------------------ decode split-K
+// One workgroup per (KV head, split of the context) serves all G query heads
+// of that KV head, so every cached K/V row is read once per token.  Scores:
+// one thread per position (a 16-byte-vectorised K row each, coalesced across
+// the wave); probabilities go to LDS; P.V: hd/8 threads per V row with 16-byte
+// loads, partial sums reduced across rows with shuffles and LDS.  Writes the
+// split's (max, sum, unnormalised output) per query head; the Wo projection
+// merges the splits (attention_decode.metal:27-133 does split + merge
+// kernels).
+constexpr int kDecThreads = 256;
+constexpr int kMaxSplitLen = 256;
+constexpr int kMaxGroup = 16;
+
+template <int HD, int GM, typename KV>
+__global__ __launch_bounds__(kDecThreads) void attn_decode_split_kernel(const float* q, const KV* kc, const KV* vc,
+                                                                        int cap, int H, int KVH, int length,
+                                                                        const int* pos_dev, int split_len,
+                                                                        float scale_log2, float* partials) {
+    constexpr int VEC = 16 / sizeof(KV);    // elements per 16-byte load
+    constexpr int TPR = HD / 8;             // threads per V row (8 dims each)
+    constexpr int RPP = kDecThreads / TPR;  // V rows in flight per pass
+    __shared__ float qs[GM][HD];
+    __shared__ float es[GM][kMaxSplitLen];
+    __shared__ float red[GM][8];
+    __shared__ float ws[4][GM][HD];
+    const int G = H / KVH;
+    const int sp = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    if (pos_dev) length = *pos_dev + 1;
+    const int p0 = sp * split_len;
+    const int p1 = min(p0 + split_len, length);
+    const int n = p1 - p0;
+    for (int i = tid; i < G * HD; i += kDecThreads) qs[i / HD][i % HD] = q[(kvh * G + i / HD) * HD + i % HD] * scale_log2;
+    __syncthreads();
+
+    // scores in base-2 exponent units: one thread per position
+    float sc[GM];
+#pragma unroll
+    for (int g = 0; g < GM; g++) sc[g] = (tid < n && g < G) ? 0.f : -INFINITY;
+    if (tid < n) {
+        const KV* kr = kc + ((int64_t)kvh * cap + p0 + tid) * HD;
+#pragma unroll
+        for (int c = 0; c < HD / VEC; c++) {
+            const int4 raw = *(const int4*)(kr + c * VEC);
+            const KV* kv = (const KV*)&raw;
+#pragma unroll
+            for (int j = 0; j < VEC; j++) {
+                const float kf = (float)kv[j];
+#pragma unroll
+                for (int g = 0; g < GM; g++)
+                    if (g < G) sc[g] += qs[g][c * VEC + j] * kf;
+            }
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < GM; g++) {
+        const float m = wave_max(sc[g]);
+        if (lane == 0) red[g][wave] = m;
+    }
+    __syncthreads();
+    float mloc[GM];
+#pragma unroll
+    for (int g = 0; g < GM; g++) mloc[g] = fmaxf(fmaxf(red[g][0], red[g][1]), fmaxf(red[g][2], red[g][3]));
+#pragma unroll
+    for (int g = 0; g < GM; g++) {
+        const float e = (tid < n && g < G) ? exp2f(sc[g] - mloc[g]) : 0.f;
+        if (tid < kMaxSplitLen) es[g][tid] = e;
+        const float sum = wave_sum(e);
+        if (lane == 0) red[g][4 + wave] = sum;
+    }
+    __syncthreads();
+
+    // P.V: TPR threads per V row, RPP rows per pass
+    const int tr = tid % TPR, rowq = tid / TPR;
+    float acc[GM][8];
+#pragma unroll
+    for (int g = 0; g < GM; g++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[g][j] = 0.f;
+    for (int r = rowq; r < n; r += RPP) {
+        const KV* vr = vc + ((int64_t)kvh * cap + p0 + r) * HD + tr * 8;
+        float vf[8];
+        if constexpr (sizeof(KV) == 2) {
+            const int4 raw = *(const int4*)vr;
+            const KV* v = (const KV*)&raw;
+#pragma unroll
+            for (int j = 0; j < 8; j++) vf[j] = (float)v[j];
+        } else {
+            const int4 r0 = *(const int4*)vr, r1 = *(const int4*)(vr + 4);
+            const float* a = (const float*)&r0;
+            const float* b = (const float*)&r1;
+#pragma unroll
+            for (int j = 0; j < 4; j++) { vf[j] = a[j]; vf[4 + j] = b[j]; }
+        }
+#pragma unroll
+        for (int g = 0; g < GM; g++) {
+            const float e = es[g][r];
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[g][j] += e * vf[j];
+        }
+    }
+    // reduce the rows held by one wave (lane bits >= log2(TPR)), then the 4 waves
+#pragma unroll
+    for (int o = TPR; o < 64; o <<= 1)
+#pragma unroll
+        for (int g = 0; g < GM; g++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[g][j] += __shfl_xor(acc[g][j], o, 64);
+    if (lane < TPR)
+#pragma unroll
+        for (int g = 0; g < GM; g++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) ws[wave][g][tr * 8 + j] = acc[g][j];
+    __syncthreads();
+    for (int i = tid; i < G * HD; i += kDecThreads) {
+        const int g = i / HD, d = i % HD;
+        float* pp = partials + ((int64_t)(kvh * G + g) * gridDim.x + sp) * (HD + 2);
+        pp[2 + d] = ws[0][g][d] + ws[1][g][d] + ws[2][g][d] + ws[3][g][d];
+        if (d == 0) {
+            // the running max is kept in base-2 units; partials carry natural-log units
+            pp[0] = n > 0 ? fmaxf(fmaxf(red[g][0], red[g][1]), fmaxf(red[g][2], red[g][3])) * 0.69314718055994531f
+                          : -INFINITY;
+            pp[1] = red[g][4] + red[g][5] + red[g][6] + red[g][7];
+        }
+    }
+}
+
+template <int HD, typename KV>
+hipError_t decode_dispatch(int G, dim3 grid, hipStream_t st, const float* q, const void* kc, const void* vc, int cap,
+                           int H, int KVH, int length, const int* pos_dev, int split_len, float sl2, float* partials) {
+    const KV* k = (const KV*)kc;
+    const KV* v = (const KV*)vc;
+    if (G <= 1) attn_decode_split_kernel<HD, 1, KV><<<grid, kDecThreads, 0, st>>>(q, k, v, cap, H, KVH, length, pos_dev, split_len, sl2, partials);
+    else if (G <= 2) attn_decode_split_kernel<HD, 2, KV><<<grid, kDecThreads, 0, st>>>(q, k, v, cap, H, KVH, length, pos_dev, split_len, sl2, partials);
+    else if (G <= 4) attn_decode_split_kernel<HD, 4, KV><<<grid, kDecThreads, 0, st>>>(q, k, v, cap, H, KVH, length, pos_dev, split_len, sl2, partials);
+    else if (G <= 8) attn_decode_split_kernel<HD, 8, KV><<<grid, kDecThreads, 0, st>>>(q, k, v, cap, H, KVH, length, pos_dev, split_len, sl2, partials);
+    else attn_decode_split_kernel<HD, 16, KV><<<grid, kDecThreads, 0, st>>>(q, k, v, cap, H, KVH, length, pos_dev, split_len, sl2, partials);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_flash_attention(const f16* q, int ldq, const f16* kc, const f16* vc, int capacity, int tokens,
@@ -281,6 +421,39 @@ hipError_t launch_flash_attention(const f16* q, int ldq, const f16* kc, const f1
 
 // Splits for the generic kernel: decode spreads the context over >= 64-key
 // splits (up to 64 of them); batched queries already fill the chip.
+hipError_t launch_attention_decode(const float* q, const void* kc, const void* vc, int kv_f16, int capacity,
+                                   int heads, int kv_heads, int hd, int length, const int* pos_dev, int split_len,
+                                   int splits, float* partials, hipStream_t st) {
+    const int G = heads / kv_heads;
+    if (split_len > kMaxSplitLen || G > kMaxGroup || heads % kv_heads || (hd != 64 && hd != 128))
+        return hipErrorInvalidValue;
+    const float sl2 = 1.4426950408889634f / sqrtf((float)hd);
+    dim3 grid(splits, kv_heads);
+    if (hd == 64)
+        return kv_f16 ? decode_dispatch<64, f16>(G, grid, st, q, kc, vc, capacity, heads, kv_heads, length, pos_dev, split_len, sl2, partials)
+                      : decode_dispatch<64, float>(G, grid, st, q, kc, vc, capacity, heads, kv_heads, length, pos_dev, split_len, sl2, partials);
+    return kv_f16 ? decode_dispatch<128, f16>(G, grid, st, q, kc, vc, capacity, heads, kv_heads, length, pos_dev, split_len, sl2, partials)
+                  : decode_dispatch<128, float>(G, grid, st, q, kc, vc, capacity, heads, kv_heads, length, pos_dev, split_len, sl2, partials);
+}
+
+hipError_t launch_attention_merge(const float* partials, int heads, int hd, int splits, float* out, hipStream_t st) {
+    int bt = hd < 64 ? 64 : (hd > 256 ? 256 : (hd + 63) / 64 * 64);
+    attn_merge_kernel<<<heads, bt, 0, st>>>(partials, heads, hd, splits, out);
+    return hipGetLastError();
+}
+
+int attention_decode_split_len(int capacity) {
+    // 128 positions per split, widened so a context never needs more than 64 splits
+    int l = (capacity + 63) / 64;
+    l = (l + 31) / 32 * 32;
+    return l < 128 ? 128 : l;
+}
+int attention_decode_max_split_len() { return kMaxSplitLen; }
+
+bool attention_decode_supported(int heads, int kv_heads, int hd) {
+    return (hd == 64 || hd == 128) && heads % kv_heads == 0 && heads / kv_heads <= kMaxGroup;
+}
+
 int attention_splits(int length, int heads, int tokens) {
     (void)heads;
     if (tokens > 1) return 1;

@@ -9,11 +9,17 @@
 // lane reads whole 16-byte chunks with one global_load_dwordx4:
 //   Q8_0 chunk = 16 weights (half a block), Q4_0 chunk = 32 weights (one
 //   block), F16 chunk = 8 weights.
-// A group of LPR lanes owns one output row and strides over its chunks; each
-// lane issues up to 4 chunk loads before consuming any, to keep enough bytes
-// in flight per CU for HBM.  The (normalised) input row is staged once per
-// workgroup in LDS and read back as float4.  Partial sums are combined with
-// cross-lane shuffles; lane 0 of the group applies the epilogue.
+// A group of LPR lanes owns one output row and strides over its chunks.  The
+// first batch of up to 4 chunk loads per lane is issued before the input row
+// is staged, so the weight stream is in flight while the workgroup computes
+// the RMSNorm (or merges attention partials) into LDS.  Partial sums are
+// combined with cross-lane shuffles; lane 0 of the group applies the epilogue.
+//
+// Input stagers: x (optionally RMS-normalised with gain g), or the merge of
+// split-K decode-attention partials (max, sum, unnormalised output) per head,
+// which folds the attention merge into the Wo projection.
+// Epilogues: store, residual add, SwiGLU, or (QKV projection) RoPE on q and k
+// with k and v appended to the KV cache at position pos.
 #include "common.h"
 
 namespace {
@@ -21,12 +27,12 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kUnroll = 4;
+constexpr int kMaxRowsPerBlock = kWaves * 64 / 16;
 
 struct GemvArgs {
     DevMatrix w, u;
-    const float* x;
-    const float* norm;
-    float eps;
+    GemvInput in;
+    GemvRope rope;
     float* out;
 };
 
@@ -92,56 +98,165 @@ __device__ __forceinline__ float chunk_dot(const int4& q, float d, int c, const 
     }
 }
 
+// One row's dot product, with the first batch of loads already in registers.
 template <int FMT, int LPR>
-__device__ __forceinline__ float row_dot(const DevMatrix& m, int64_t row, int K, const float* xs, int li) {
-    const int nch = chunks_of<FMT>(K);
-    float acc = 0.f;
-    for (int c0 = li; c0 < nch; c0 += kUnroll * LPR) {
-        int4 q[kUnroll];
-        float d[kUnroll];
+struct RowStream {
+    int4 q[kUnroll];
+    float d[kUnroll];
+    __device__ __forceinline__ void prefetch(const DevMatrix& m, int64_t row, int K, int li) {
+        const int nch = chunks_of<FMT>(K);
 #pragma unroll
         for (int u = 0; u < kUnroll; u++) {
-            int c = c0 + u * LPR;
+            const int c = li + u * LPR;
             if (c < nch) load_chunk<FMT>(m, row, K, c, q[u], d[u]);
         }
+    }
+    __device__ __forceinline__ float finish(const DevMatrix& m, int64_t row, int K, int li, const float* xs) {
+        const int nch = chunks_of<FMT>(K);
+        float acc = 0.f;
 #pragma unroll
         for (int u = 0; u < kUnroll; u++) {
-            int c = c0 + u * LPR;
+            const int c = li + u * LPR;
             if (c < nch) acc += chunk_dot<FMT>(q[u], d[u], c, xs);
         }
+        for (int c0 = li + kUnroll * LPR; c0 < nch; c0 += kUnroll * LPR) {
+#pragma unroll
+            for (int u = 0; u < kUnroll; u++) {
+                const int c = c0 + u * LPR;
+                if (c < nch) load_chunk<FMT>(m, row, K, c, q[u], d[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < kUnroll; u++) {
+                const int c = c0 + u * LPR;
+                if (c < nch) acc += chunk_dot<FMT>(q[u], d[u], c, xs);
+            }
+        }
+        return acc;
     }
-    return acc;
+};
+
+enum { IN_X = 0, IN_NORM = 1, IN_MERGE = 2 };
+
+// Stages the input row (K floats) into LDS.
+template <int INP>
+__device__ __forceinline__ void stage_input(const GemvInput& in, int K, float* xs, float* red) {
+    if constexpr (INP == IN_MERGE) {
+        // Merge split-K attention partials: per head h, weights w_s = exp(m_s - M),
+        // x = sum_s w_s o_s / sum_s w_s l_s (attention_decode.metal:117-133).
+        __shared__ float mh[256];
+        __shared__ float wsp[4096];
+        const int H = in.heads, S = in.splits, hd = in.hd;
+        const int live = in.pos_dev ? min(S, (*in.pos_dev + in.split_len) / in.split_len) : S;
+        for (int h = threadIdx.x; h < H; h += kThreads) {
+            float m = -INFINITY;
+            for (int s = 0; s < live; s++) m = fmaxf(m, in.partials[((int64_t)h * S + s) * (hd + 2)]);
+            mh[h] = m;
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < H * live; i += kThreads) {
+            const int h = i / live, s = i - h * live;
+            const float ms = in.partials[((int64_t)h * S + s) * (hd + 2)];
+            wsp[h * live + s] = ms == -INFINITY ? 0.f : expf(ms - mh[h]);
+        }
+        __syncthreads();
+        for (int h = threadIdx.x; h < H; h += kThreads) {
+            float l = 0.f;
+            for (int s = 0; s < live; s++) l += wsp[h * live + s] * in.partials[((int64_t)h * S + s) * (hd + 2) + 1];
+            mh[h] = 1.0f / l;
+        }
+        __syncthreads();
+        for (int k = threadIdx.x; k < K; k += kThreads) {
+            const int h = k / hd, dd = k - h * hd;
+            const float* pp = in.partials + (int64_t)h * S * (hd + 2) + 2 + dd;
+            float acc = 0.f;
+            for (int s = 0; s < live; s++) acc += wsp[h * live + s] * pp[(int64_t)s * (hd + 2)];
+            xs[k] = acc * mh[h];
+        }
+    } else if constexpr (INP == IN_NORM) {
+        float ss = 0.f;
+        for (int i = threadIdx.x; i < K; i += kThreads) ss += in.x[i] * in.x[i];
+        ss = block_sum(ss, red);
+        const float scale = 1.0f / sqrtf(ss / (float)K + in.eps);
+        for (int i = threadIdx.x; i < K; i += kThreads) xs[i] = (in.x[i] * scale) * in.norm[i];
+    } else {
+        for (int i = threadIdx.x; i < K; i += kThreads) xs[i] = in.x[i];
+    }
+    __syncthreads();
 }
 
-template <int FMT, int LPR, int MODE, bool NORM>
+template <int FMT, int LPR, int MODE, int INP>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     extern __shared__ float xs[];
     __shared__ float red[16];
+    __shared__ float rowbuf[kMaxRowsPerBlock];
     const int K = a.w.cols;
-    float scale = 1.f;
-    if (NORM) {
-        float ss = 0.f;
-        for (int i = threadIdx.x; i < K; i += kThreads) ss += a.x[i] * a.x[i];
-        ss = block_sum(ss, red);
-        scale = 1.0f / sqrtf(ss / (float)K + a.eps);
-    }
-    for (int i = threadIdx.x; i < K; i += kThreads) xs[i] = NORM ? (a.x[i] * scale) * a.norm[i] : a.x[i];
-    __syncthreads();
-
     constexpr int kRowsPerWave = 64 / LPR;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int li = lane % LPR;
-    const int64_t row = ((int64_t)blockIdx.x * kWaves + wave) * kRowsPerWave + lane / LPR;
+    const int local = wave * kRowsPerWave + lane / LPR;
+    const int64_t row = (int64_t)blockIdx.x * kWaves * kRowsPerWave + local;
     const bool valid = row < a.w.rows;
+
+    RowStream<FMT, LPR> s0, s1;
+    if (valid) {
+        s0.prefetch(a.w, row, K, li);
+        if (MODE == GEMV_SWIGLU) s1.prefetch(a.u, row, K, li);
+    }
+    stage_input<INP>(a.in, K, xs, red);
     float acc = 0.f, acc2 = 0.f;
     if (valid) {
-        acc = row_dot<FMT, LPR>(a.w, row, K, xs, li);
-        if (MODE == GEMV_SWIGLU) acc2 = row_dot<FMT, LPR>(a.u, row, K, xs, li);
+        acc = s0.finish(a.w, row, K, li, xs);
+        if (MODE == GEMV_SWIGLU) acc2 = s1.finish(a.u, row, K, li, xs);
     }
 #pragma unroll
     for (int o = LPR / 2; o > 0; o >>= 1) {
         acc += __shfl_xor(acc, o, 64);
         if (MODE == GEMV_SWIGLU) acc2 += __shfl_xor(acc2, o, 64);
+    }
+    if (MODE == GEMV_QKV_ROPE) {
+        // Rows come in aligned (even, odd) pairs inside a block: RoPE pairs.
+        if (li == 0) rowbuf[local] = acc;
+        __syncthreads();
+        const GemvRope& r = a.rope;
+        const int pos = r.pos_dev ? *r.pos_dev : r.pos;
+        const int half = r.hd / 2;
+        const int pairs = kWaves * kRowsPerWave / 2;
+        for (int pi = threadIdx.x; pi < pairs; pi += kThreads) {
+            const int64_t r0 = (int64_t)blockIdx.x * kWaves * kRowsPerWave + 2 * pi;
+            if (r0 >= a.w.rows) break;
+            const float v0 = rowbuf[2 * pi], v1 = rowbuf[2 * pi + 1];
+            const int qw = r.heads * r.hd, kw = r.kv_heads * r.hd;
+            if (r0 < qw + kw) {
+                const int d = (int)(r0 % r.hd);
+                const float2 cs = r.table[(int64_t)pos * half + d / 2];
+                float ac = v0 * cs.x, bs = v1 * cs.y, as = v0 * cs.y, bc = v1 * cs.x;
+                const float ra = ac - bs, rb = as + bc;
+                if (r0 < qw) {
+                    a.out[r0] = ra;
+                    a.out[r0 + 1] = rb;
+                } else {
+                    const int64_t dst = ((int64_t)((r0 - qw) / r.hd) * r.capacity + pos) * r.hd + d;
+                    if (r.kv_f16) {
+                        ((f16*)r.kc)[dst] = (f16)ra;
+                        ((f16*)r.kc)[dst + 1] = (f16)rb;
+                    } else {
+                        ((float*)r.kc)[dst] = ra;
+                        ((float*)r.kc)[dst + 1] = rb;
+                    }
+                }
+            } else {
+                const int d = (int)((r0 - qw - kw) % r.hd);
+                const int64_t dst = ((int64_t)((r0 - qw - kw) / r.hd) * r.capacity + pos) * r.hd + d;
+                if (r.kv_f16) {
+                    ((f16*)r.vc)[dst] = (f16)v0;
+                    ((f16*)r.vc)[dst + 1] = (f16)v1;
+                } else {
+                    ((float*)r.vc)[dst] = v0;
+                    ((float*)r.vc)[dst + 1] = v1;
+                }
+            }
+        }
+        return;
     }
     if (valid && li == 0) {
         if (MODE == GEMV_STORE) a.out[row] = acc;
@@ -150,24 +265,29 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     }
 }
 
-template <int FMT, int MODE, bool NORM>
+template <int FMT, int MODE, int INP>
 hipError_t dispatch(int lpr, const GemvArgs& a, hipStream_t st) {
     const int rows_per_block = kWaves * (64 / lpr);
     const int grid = (a.w.rows + rows_per_block - 1) / rows_per_block;
     const size_t lds = (size_t)a.w.cols * sizeof(float);
     switch (lpr) {
-    case 16: gemv_kernel<FMT, 16, MODE, NORM><<<grid, kThreads, lds, st>>>(a); break;
-    case 32: gemv_kernel<FMT, 32, MODE, NORM><<<grid, kThreads, lds, st>>>(a); break;
-    default: gemv_kernel<FMT, 64, MODE, NORM><<<grid, kThreads, lds, st>>>(a); break;
+    case 16: gemv_kernel<FMT, 16, MODE, INP><<<grid, kThreads, lds, st>>>(a); break;
+    case 32: gemv_kernel<FMT, 32, MODE, INP><<<grid, kThreads, lds, st>>>(a); break;
+    default: gemv_kernel<FMT, 64, MODE, INP><<<grid, kThreads, lds, st>>>(a); break;
     }
     return hipGetLastError();
 }
 
+// The (epilogue, input) pairs the forward pass uses.
 template <int FMT>
-hipError_t dispatch_fmt(int lpr, int mode, bool norm, const GemvArgs& a, hipStream_t st) {
-    if (mode == GEMV_STORE) return norm ? dispatch<FMT, GEMV_STORE, true>(lpr, a, st) : dispatch<FMT, GEMV_STORE, false>(lpr, a, st);
-    if (mode == GEMV_ADD) return norm ? dispatch<FMT, GEMV_ADD, true>(lpr, a, st) : dispatch<FMT, GEMV_ADD, false>(lpr, a, st);
-    return norm ? dispatch<FMT, GEMV_SWIGLU, true>(lpr, a, st) : dispatch<FMT, GEMV_SWIGLU, false>(lpr, a, st);
+hipError_t dispatch_fmt(int lpr, int mode, int inp, const GemvArgs& a, hipStream_t st) {
+    if (mode == GEMV_STORE) return inp == IN_NORM ? dispatch<FMT, GEMV_STORE, IN_NORM>(lpr, a, st)
+                                                  : dispatch<FMT, GEMV_STORE, IN_X>(lpr, a, st);
+    if (mode == GEMV_ADD) return inp == IN_MERGE ? dispatch<FMT, GEMV_ADD, IN_MERGE>(lpr, a, st)
+                                                 : dispatch<FMT, GEMV_ADD, IN_X>(lpr, a, st);
+    if (mode == GEMV_SWIGLU) return inp == IN_NORM ? dispatch<FMT, GEMV_SWIGLU, IN_NORM>(lpr, a, st)
+                                                   : dispatch<FMT, GEMV_SWIGLU, IN_X>(lpr, a, st);
+    return dispatch<FMT, GEMV_QKV_ROPE, IN_NORM>(lpr, a, st);
 }
 
 }  // namespace
@@ -181,20 +301,32 @@ static int pick_lpr(int rows) {
     return 64;
 }
 
-hipError_t launch_gemv(const DevMatrix& w, const DevMatrix* w_up, const float* x, const float* norm, float eps,
-                       float* out, int mode, hipStream_t st) {
+hipError_t launch_gemv_ex(const DevMatrix& w, const DevMatrix* w_up, const GemvInput& in, const GemvRope* rope,
+                          float* out, int mode, hipStream_t st) {
+    const int inp = in.partials ? IN_MERGE : in.norm ? IN_NORM : IN_X;
+    if (inp == IN_MERGE && ((long)in.heads * in.splits > 4096 || in.heads > 256 || mode != GEMV_ADD))
+        return hipErrorInvalidValue;
+    if (mode == GEMV_QKV_ROPE && (!rope || inp != IN_NORM)) return hipErrorInvalidValue;
+    if (inp == IN_NORM && mode == GEMV_ADD) return hipErrorInvalidValue;
     GemvArgs a;
     a.w = w;
     a.u = w_up ? *w_up : w;
-    a.x = x;
-    a.norm = norm;
-    a.eps = eps;
+    a.in = in;
+    if (rope) a.rope = *rope;
     a.out = out;
     const int lpr = pick_lpr(w.rows);
-    const bool nrm = norm != nullptr;
     switch (w.dtype) {
-    case DT_Q8_0: return dispatch_fmt<DT_Q8_0>(lpr, mode, nrm, a, st);
-    case DT_Q4_0: return dispatch_fmt<DT_Q4_0>(lpr, mode, nrm, a, st);
-    default: return dispatch_fmt<DT_F16>(lpr, mode, nrm, a, st);
+    case DT_Q8_0: return dispatch_fmt<DT_Q8_0>(lpr, mode, inp, a, st);
+    case DT_Q4_0: return dispatch_fmt<DT_Q4_0>(lpr, mode, inp, a, st);
+    default: return dispatch_fmt<DT_F16>(lpr, mode, inp, a, st);
     }
+}
+
+hipError_t launch_gemv(const DevMatrix& w, const DevMatrix* w_up, const float* x, const float* norm, float eps,
+                       float* out, int mode, hipStream_t st) {
+    GemvInput in;
+    in.x = x;
+    in.norm = norm;
+    in.eps = eps;
+    return launch_gemv_ex(w, w_up, in, nullptr, out, mode, st);
 }

@@ -86,7 +86,7 @@ __global__ void dequant_kernel(DevMatrix m, float* out) {
 // (Sampler.argmax, Sampler.swift:100-108; all-NaN input yields 0).  Writes the
 // next input token and emitted[slot].  One block of 1024 threads.
 __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, int n, int32_t* chain, int32_t* emitted,
-                                                      int slot) {
+                                                      int slot, int* pos_dev) {
     __shared__ float sv[16];
     __shared__ int si[16];
     float v = -INFINITY;
@@ -111,7 +111,13 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, int n
             if (sv[i] > bv || (sv[i] == bv && si[i] < bi)) { bv = sv[i]; bi = si[i]; }
         int token = bi == INT_MAX ? 0 : bi;
         if (chain) chain[0] = token;
-        if (emitted) emitted[slot] = token;
+        if (pos_dev) {
+            const int p = *pos_dev;
+            if (emitted) emitted[p] = token;
+            *pos_dev = p + 1;
+        } else if (emitted) {
+            emitted[slot] = token;
+        }
     }
 }
 
@@ -197,8 +203,9 @@ hipError_t launch_dequant(const DevMatrix& m, float* out, hipStream_t st) {
     if (n > 0) dequant_kernel<<<grid_for(n), kBlock, 0, st>>>(m, out);
     return hipGetLastError();
 }
-hipError_t launch_argmax(const float* logits, int n, int32_t* chain, int32_t* emitted, int slot, hipStream_t st) {
-    argmax_kernel<<<1, 1024, 0, st>>>(logits, n, chain, emitted, slot);
+hipError_t launch_argmax(const float* logits, int n, int32_t* chain, int32_t* emitted, int slot, int* pos_dev,
+                         hipStream_t st) {
+    argmax_kernel<<<1, 1024, 0, st>>>(logits, n, chain, emitted, slot, pos_dev);
     return hipGetLastError();
 }
 hipError_t launch_rope_store(float* qkv, int ld, int tokens, int heads, int kv_heads, int hd, int start,

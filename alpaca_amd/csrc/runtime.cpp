@@ -295,6 +295,22 @@ static void repack_host(int dt, const uint8_t* raw, int64_t rows, int64_t cols, 
     }
 }
 
+// Rows of a [heads*hd, cols] projection reordered from split-half RoPE pairs
+// (i, i+hd/2) to adjacent pairs (2i, 2i+1).  q.k is unchanged when q and k
+// share the permutation, so attention results are identical while every
+// kernel can rotate adjacent pairs.
+static std::vector<uint8_t> interleave_rows(int dt, const void* raw, int64_t rows, int64_t cols, int hd) {
+    const int64_t rb = raw_bytes(dt, cols);
+    std::vector<uint8_t> out((size_t)(rows * rb));
+    const uint8_t* src = (const uint8_t*)raw;
+    for (int64_t r = 0; r < rows; r++) {
+        const int64_t h = r / hd, d = r % hd, half = hd / 2;
+        const int64_t from = h * hd + (d % 2 == 0 ? d / 2 : d / 2 + half);
+        std::memcpy(&out[(size_t)(r * rb)], src + from * rb, (size_t)rb);
+    }
+    return out;
+}
+
 // Uploads one or more matrices with equal dtype and cols stacked in row space.
 static int upload_matrix(int dt, const std::vector<std::pair<const void*, int64_t>>& parts, int64_t cols,
                          OwnedMatrix& out, hipStream_t st) {
@@ -457,7 +473,16 @@ extern "C" int ahip_model_create(ahip_context* ctx, const ahip_llama_config* con
         if (wg->dtype != wu->dtype) return fail(AHIP_ERR_UNSUPPORTED, p + "ffn_gate/up must share one format");
         if (int rc = upload_norm(an, L->attn_norm)) return rc;
         if (int rc = upload_norm(fn, L->ffn_norm)) return rc;
-        if (int rc = upload_matrix(wq->dtype, {{wq->data, QW}, {wk->data, KW}, {wv->data, KW}}, H, L->qkv, st)) return rc;
+        const void* qd = wq->data;
+        const void* kd = wk->data;
+        std::vector<uint8_t> qperm, kperm;
+        if (!c.rope_interleaved) {
+            qperm = interleave_rows(wq->dtype, wq->data, QW, H, c.head_dim);
+            kperm = interleave_rows(wk->dtype, wk->data, KW, H, c.head_dim);
+            qd = qperm.data();
+            kd = kperm.data();
+        }
+        if (int rc = upload_matrix(wq->dtype, {{qd, QW}, {kd, KW}, {wv->data, KW}}, H, L->qkv, st)) return rc;
         if (int rc = upload_matrix(wo->dtype, {{wo->data, H}}, QW, L->wo, st)) return rc;
         if (int rc = upload_matrix(wg->dtype, {{wg->data, F}}, H, L->gate, st)) return rc;
         if (int rc = upload_matrix(wu->dtype, {{wu->data, F}}, H, L->up, st)) return rc;
@@ -493,7 +518,7 @@ struct SessionSizes {
     int64_t total;
 };
 
-static constexpr int kMaxSplits = 64;
+static constexpr int kMaxSplits = 65;
 
 static SessionSizes session_sizes(const ahip_llama_config& c, int capacity, int max_batch, int kv_f16) {
     SessionSizes s{};
@@ -529,9 +554,14 @@ struct ahip_session {
     int capacity = 0, max_batch = 0, kv_f16 = 1, fast = 1;
     hipStream_t stream = nullptr;
     std::vector<std::unique_ptr<DevBuf>> kc, vc;
-    DevBuf x, xn, xh, qkv, qh, ctx, ctxh, ffn, ffnh, partials, logits, tokens, chain, emitted;
+    DevBuf x, xn, xh, qkv, qh, ctx, ctxh, ffn, ffnh, partials, logits, tokens, chain, dpos;
     float* logits_host = nullptr;
-    int32_t* emitted_host = nullptr;
+    int32_t* emitted_host = nullptr;   // pinned, mapped: the arg-max kernel writes tokens here
+    int32_t* emitted_mapped = nullptr; // device address of emitted_host
+    bool dec_split = false;            // split-K decode attention (else the generic kernel)
+    int dec_split_len = 0, dec_splits = 0;
+    hipGraphExec_t greedy_graph = nullptr;
+    bool graph_failed = false;
     int32_t* tokens_host = nullptr;
     int length = 0;
     std::atomic<int> busy{0};
@@ -548,6 +578,7 @@ struct ahip_session {
         for (auto e : event_pool) hipEventDestroy(e);
         if (ev_begin) hipEventDestroy(ev_begin);
         if (ev_end) hipEventDestroy(ev_end);
+        if (greedy_graph) hipGraphExecDestroy(greedy_graph);
         if (logits_host) hipHostFree(logits_host);
         if (emitted_host) hipHostFree(emitted_host);
         if (tokens_host) hipHostFree(tokens_host);
@@ -633,12 +664,19 @@ extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, i
     for (A a : {A{&s->x, z.x * 4}, A{&s->xn, z.x * 4}, A{&s->xh, z.x * 2}, A{&s->qkv, z.qkv * 4}, A{&s->qh, z.q16 * 2},
                 A{&s->ctx, z.ctx * 4}, A{&s->ctxh, z.ctx * 2}, A{&s->ffn, z.ffn * 4}, A{&s->ffnh, z.ffn * 2},
                 A{&s->partials, z.partials * 4}, A{&s->logits, z.logits * 4}, A{&s->tokens, (int64_t)capacity * 4},
-                A{&s->chain, 64}, A{&s->emitted, ((int64_t)capacity + 8) * 4}})
+                A{&s->chain, 64}, A{&s->dpos, 64}})
         if (int rc = a.b->alloc(a.n)) return rc;
     if (hipHostMalloc((void**)&s->logits_host, (size_t)c.vocab_size * 4, hipHostMallocDefault) != hipSuccess ||
-        hipHostMalloc((void**)&s->emitted_host, ((size_t)capacity + 8) * 4, hipHostMallocDefault) != hipSuccess ||
-        hipHostMalloc((void**)&s->tokens_host, (size_t)capacity * 4, hipHostMallocDefault) != hipSuccess)
+        hipHostMalloc((void**)&s->emitted_host, ((size_t)capacity + 8) * 4, hipHostMallocMapped) != hipSuccess ||
+        hipHostMalloc((void**)&s->tokens_host, ((size_t)capacity + 8) * 4, hipHostMallocDefault) != hipSuccess)
         return fail(AHIP_ERR_ALLOC, "pinned host allocation failed");
+    HIP_OR(hipHostGetDevicePointer((void**)&s->emitted_mapped, s->emitted_host, 0), "hipHostGetDevicePointer");
+    s->dec_split = attention_decode_supported(c.head_count, c.kv_head_count, c.head_dim) &&
+                   attention_decode_split_len(capacity) <= attention_decode_max_split_len();
+    if (s->dec_split) {
+        s->dec_split_len = attention_decode_split_len(capacity);
+        s->dec_splits = (capacity + s->dec_split_len - 1) / s->dec_split_len;
+    }
     HIP_OR(hipEventCreate(&s->ev_begin), "hipEventCreate");
     HIP_OR(hipEventCreate(&s->ev_end), "hipEventCreate");
     *out = s.release();
@@ -671,9 +709,73 @@ struct BusyGuard {
         if (e_ != hipSuccess) return fail(AHIP_ERR_COMMAND_FAILED, std::string("kernel launch: ") + hipGetErrorString(e_)); \
     } while (0)
 
+// One decoder layer for a single token (the fused decode path,
+// MetalLlamaModel.swift:344-356): 5 launches -- QKV GEMV with RMSNorm prologue
+// and RoPE + KV-store epilogue; split-K attention; Wo GEMV merging the splits
+// and adding the residual; gate/up GEMV with RMSNorm prologue and SwiGLU
+// epilogue; down GEMV adding the residual.  The position is `pos`, or *pos_dev
+// when pos_dev is set (the greedy chain advances it on the device).
+static int encode_decode_layer(ahip_session* s, int li, int pos, const int* pos_dev) {
+    ahip_model* m = s->m;
+    const ahip_llama_config& c = m->c;
+    const int hd = c.head_dim, LDQKV = (c.head_count + 2 * c.kv_head_count) * hd;
+    hipStream_t st = s->stream;
+    ahip_model::Layer& L = *m->layers[li];
+    float* x = s->x.as<float>();
+    float* qkv = s->qkv.as<float>();
+    void* kc = s->kc[li]->p;
+    void* vc = s->vc[li]->p;
+    s->stage("qkv (fused norm)");
+    GemvInput in;
+    in.x = x;
+    in.norm = L.attn_norm.as<float>();
+    in.eps = c.rms_norm_eps;
+    GemvRope rope;
+    rope.table = m->rope.as<float2>();
+    rope.heads = c.head_count;
+    rope.kv_heads = c.kv_head_count;
+    rope.hd = hd;
+    rope.capacity = s->capacity;
+    rope.pos = pos;
+    rope.pos_dev = pos_dev;
+    rope.kc = kc;
+    rope.vc = vc;
+    rope.kv_f16 = s->kv_f16;
+    LAUNCH(launch_gemv_ex(L.qkv.m, nullptr, in, &rope, qkv, GEMV_QKV_ROPE, st));
+    s->stage("attention");
+    GemvInput att;
+    if (s->dec_split) {
+        // eager calls launch only the splits the context covers; graph replays cover the capacity
+        const int splits = pos_dev ? s->dec_splits : (pos + s->dec_split_len) / s->dec_split_len;
+        LAUNCH(launch_attention_decode(qkv, kc, vc, s->kv_f16, s->capacity, c.head_count, c.kv_head_count, hd, pos + 1,
+                                       pos_dev, s->dec_split_len, splits, s->partials.as<float>(), st));
+        att.partials = s->partials.as<float>();
+        att.heads = c.head_count;
+        att.splits = splits;
+        att.hd = hd;
+        att.split_len = s->dec_split_len;
+        att.pos_dev = pos_dev;
+    } else {
+        if (pos_dev) return fail(AHIP_ERR_UNSUPPORTED, "device-positioned decode needs the split-K attention kernel");
+        const int splits = attention_splits(pos + 1, c.head_count, 1);
+        LAUNCH(launch_attention_generic(qkv, LDQKV, kc, vc, s->kv_f16, s->capacity, 1, c.head_count, c.kv_head_count,
+                                        hd, pos, splits, s->partials.as<float>(), s->ctx.as<float>(), st));
+        att.x = s->ctx.as<float>();
+    }
+    s->stage("attn out projection (+residual)");
+    LAUNCH(launch_gemv_ex(L.wo.m, nullptr, att, nullptr, x, GEMV_ADD, st));
+    s->stage("ffn gate+up+silu (fused norm)");
+    LAUNCH(launch_gemv(L.gate.m, &L.up.m, x, L.ffn_norm.as<float>(), c.rms_norm_eps, s->ffn.as<float>(), GEMV_SWIGLU,
+                       st));
+    s->stage("ffn down (+residual)");
+    LAUNCH(launch_gemv(L.down.m, nullptr, s->ffn.as<float>(), nullptr, 0.f, x, GEMV_ADD, st));
+    return AHIP_OK;
+}
+
 // Enqueues one chunk of `n` tokens at absolute position `pos` (encodeChunk,
 // MetalLlamaModel.swift:307-384).  Tokens are read from device memory.
-static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bool logits) {
+static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bool logits,
+                        const int* pos_dev = nullptr) {
     ahip_model* m = s->m;
     const ahip_llama_config& c = m->c;
     const int H = c.hidden_size, QW = c.head_count * c.head_dim, KW = c.kv_head_count * c.head_dim,
@@ -691,24 +793,7 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
         void* kc = s->kc[li]->p;
         void* vc = s->vc[li]->p;
         if (n == 1) {
-            // Fused single-token path: 6 launches per layer (MetalLlamaModel.swift:344-356).
-            s->stage("qkv (fused norm)");
-            LAUNCH(launch_gemv(L.qkv.m, nullptr, x, L.attn_norm.as<float>(), c.rms_norm_eps, qkv, GEMV_STORE, st));
-            s->stage("rope + kv store");
-            LAUNCH(launch_rope_store(qkv, LDQKV, 1, c.head_count, c.kv_head_count, hd, pos, rope, c.rope_interleaved,
-                                     1, nullptr, kc, vc, s->kv_f16, s->capacity, st));
-            s->stage("attention");
-            const int splits = attention_splits(pos + 1, c.head_count, 1);
-            LAUNCH(launch_attention_generic(qkv, LDQKV, kc, vc, s->kv_f16, s->capacity, 1, c.head_count,
-                                            c.kv_head_count, hd, pos, splits, s->partials.as<float>(),
-                                            s->ctx.as<float>(), st));
-            s->stage("attn out projection (+residual)");
-            LAUNCH(launch_gemv(L.wo.m, nullptr, s->ctx.as<float>(), nullptr, 0.f, x, GEMV_ADD, st));
-            s->stage("ffn gate+up+silu (fused norm)");
-            LAUNCH(launch_gemv(L.gate.m, &L.up.m, x, L.ffn_norm.as<float>(), c.rms_norm_eps, s->ffn.as<float>(),
-                               GEMV_SWIGLU, st));
-            s->stage("ffn down (+residual)");
-            LAUNCH(launch_gemv(L.down.m, nullptr, s->ffn.as<float>(), nullptr, 0.f, x, GEMV_ADD, st));
+            if (int rc = encode_decode_layer(s, li, pos, pos_dev)) return rc;
         } else if (mfma) {
             f16* xh = s->xh.as<f16>();
             s->stage("rmsnorm");
@@ -716,9 +801,8 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
             s->stage("qkv projections");
             LAUNCH(launch_gemm_mfma(xh, H, n, L.qkv.m, nullptr, qkv, nullptr, LDQKV, GEMM_STORE, st));
             s->stage("rope + kv store");
-            LAUNCH(launch_rope_store(qkv, LDQKV, n, c.head_count, c.kv_head_count, hd, pos, rope, c.rope_interleaved,
-                                     flash ? 0 : 1, flash ? s->qh.as<f16>() : nullptr, kc, vc, s->kv_f16,
-                                     s->capacity, st));
+            LAUNCH(launch_rope_store(qkv, LDQKV, n, c.head_count, c.kv_head_count, hd, pos, rope, 1, flash ? 0 : 1,
+                                     flash ? s->qh.as<f16>() : nullptr, kc, vc, s->kv_f16, s->capacity, st));
             s->stage("attention");
             if (flash) {
                 LAUNCH(launch_flash_attention(s->qh.as<f16>(), QW, (const f16*)kc, (const f16*)vc, s->capacity, n,
@@ -743,8 +827,8 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
             s->stage("qkv projections");
             LAUNCH(launch_gemm_f32(xn, H, n, L.qkv.m, nullptr, qkv, LDQKV, GEMM_STORE, st));
             s->stage("rope + kv store");
-            LAUNCH(launch_rope_store(qkv, LDQKV, n, c.head_count, c.kv_head_count, hd, pos, rope, c.rope_interleaved,
-                                     1, nullptr, kc, vc, s->kv_f16, s->capacity, st));
+            LAUNCH(launch_rope_store(qkv, LDQKV, n, c.head_count, c.kv_head_count, hd, pos, rope, 1, 1, nullptr, kc,
+                                     vc, s->kv_f16, s->capacity, st));
             s->stage("attention");
             LAUNCH(launch_attention_generic(qkv, LDQKV, kc, vc, s->kv_f16, s->capacity, n, c.head_count,
                                             c.kv_head_count, hd, pos, 1, nullptr, s->ctx.as<float>(), st));
@@ -815,6 +899,48 @@ extern "C" int ahip_session_decode(ahip_session* s, int32_t token, const float**
     return ahip_session_forward(s, &token, 1, logits);
 }
 
+// One greedy step with the position and input token on the device: forward of
+// the token in `chain` at position *dpos, logits, arg-max into `chain` and the
+// mapped emitted[] buffer, *dpos += 1.
+static int encode_greedy_step(ahip_session* s) {
+    const int* dpos = s->dpos.as<int>();
+    if (int rc = encode_chunk(s, s->chain.as<int32_t>(), 1, 0, true, dpos)) return rc;
+    s->stage("sample");
+    LAUNCH(launch_argmax(s->logits.as<float>(), s->m->c.vocab_size, s->chain.as<int32_t>(), s->emitted_mapped, 0,
+                         s->dpos.as<int>(), s->stream));
+    return AHIP_OK;
+}
+
+// Captures one greedy step into a HIP graph (kernel nodes only), replayed once
+// per token so the host issues one launch per token instead of ~150.
+static bool capture_greedy_graph(ahip_session* s) {
+    if (s->greedy_graph) return true;
+    if (s->graph_failed || !s->dec_split) return false;
+    hipGraph_t g = nullptr;
+    if (hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+        s->graph_failed = true;
+        return false;
+    }
+    const int rc = encode_greedy_step(s);
+    const hipError_t e = hipStreamEndCapture(s->stream, &g);
+    if (rc != AHIP_OK || e != hipSuccess || !g) {
+        if (g) hipGraphDestroy(g);
+        hipGetLastError();
+        s->graph_failed = true;
+        return false;
+    }
+    hipGraphExec_t ex = nullptr;
+    const hipError_t ie = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (ie != hipSuccess) {
+        hipGetLastError();
+        s->graph_failed = true;
+        return false;
+    }
+    s->greedy_graph = ex;
+    return true;
+}
+
 extern "C" int ahip_session_decode_greedy(ahip_session* s, int32_t start, int max_steps, int depth, ahip_emit_fn emit,
                                           void* user, int* fed_out) {
     if (!s || !emit || !fed_out) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
@@ -827,21 +953,31 @@ extern "C" int ahip_session_decode_greedy(ahip_session* s, int32_t start, int ma
     if (budget <= 0) return AHIP_OK;
     depth = std::max(1, std::min(depth, 8));
     HIP_OR(hipSetDevice(s->m->device), "hipSetDevice");
-    s->begin_call();
     hipStream_t st = s->stream;
+    // Eager launches when profiling (stage events between kernels) or when
+    // the split-K attention kernel does not apply; otherwise graph replays.
+    const bool use_graph = !s->profiling && capture_greedy_graph(s);
+    s->begin_call();
     s->tokens_host[0] = start;
+    s->tokens_host[1] = s->length;
     HIP_OR(hipMemcpyAsync(s->chain.p, s->tokens_host, 4, hipMemcpyHostToDevice, st), "chain upload");
+    HIP_OR(hipMemcpyAsync(s->dpos.p, s->tokens_host + 1, 4, hipMemcpyHostToDevice, st), "position upload");
     HIP_OR(hipEventRecord(s->ev_begin, st), "hipEventRecord");
     std::vector<hipEvent_t> done(budget, nullptr);
     int submitted = 0, fed = 0, rc = AHIP_OK;
     auto submit = [&]() -> int {
         const int i = submitted;
-        if (int r = encode_chunk(s, s->chain.as<int32_t>(), 1, s->length + i, true)) return r;
-        s->stage("sample");
-        LAUNCH(launch_argmax(s->logits.as<float>(), s->m->c.vocab_size, s->chain.as<int32_t>(),
-                             s->emitted.as<int32_t>(), i, st));
-        HIP_OR(hipMemcpyAsync(s->emitted_host + i, s->emitted.as<int32_t>() + i, 4, hipMemcpyDeviceToHost, st),
-               "token download");
+        if (use_graph) {
+            HIP_OR(hipGraphLaunch(s->greedy_graph, st), "hipGraphLaunch");
+        } else if (s->dec_split) {
+            if (int r = encode_greedy_step(s)) return r;
+        } else {
+            // generic attention needs host-side positions
+            if (int r = encode_chunk(s, s->chain.as<int32_t>(), 1, s->length + i, true)) return r;
+            s->stage("sample");
+            LAUNCH(launch_argmax(s->logits.as<float>(), s->m->c.vocab_size, s->chain.as<int32_t>(), s->emitted_mapped,
+                                 s->length + i, nullptr, st));
+        }
         done[i] = s->next_event();
         HIP_OR(hipEventRecord(done[i], st), "hipEventRecord");
         submitted++;
@@ -854,7 +990,7 @@ extern "C" int ahip_session_decode_greedy(ahip_session* s, int32_t start, int ma
             rc = fail(AHIP_ERR_COMMAND_FAILED, std::string("decode step: ") + hipGetErrorString(e));
             break;
         }
-        const int32_t token = s->emitted_host[fed];
+        const int32_t token = ((volatile int32_t*)s->emitted_host)[s->length + fed];
         fed++;
         if (!emit(user, token)) break;
         if (submitted < budget) rc = submit();
@@ -1111,6 +1247,15 @@ extern "C" int ahip_op_attention(ahip_context* ctx, const float* q, int tokens, 
             if (int rc = upload(dq, qh.data(), qn * 2, st)) return rc;
             LAUNCH(launch_flash_attention(dq.as<f16>(), heads * hd, dk.as<f16>(), dv.as<f16>(), capacity, tokens, heads,
                                           kv_heads, hd, start, dout.as<float>(), nullptr, st));
+        } else if (tokens == 1 && attention_decode_supported(heads, kv_heads, hd) &&
+                   attention_decode_split_len(capacity) <= attention_decode_max_split_len()) {
+            if (int rc = upload(dq, q, qn * 4, st)) return rc;
+            const int sl = attention_decode_split_len(capacity), splits = (start + sl) / sl;
+            DevBuf part;
+            if (int rc = part.alloc((size_t)heads * splits * (hd + 2) * 4)) return rc;
+            LAUNCH(launch_attention_decode(dq.as<float>(), dk.p, dv.p, f16kv, capacity, heads, kv_heads, hd, start + 1,
+                                           nullptr, sl, splits, part.as<float>(), st));
+            LAUNCH(launch_attention_merge(part.as<float>(), heads, hd, splits, dout.as<float>(), st));
         } else {
             if (int rc = upload(dq, q, qn * 4, st)) return rc;
             const int splits = attention_splits(start + tokens, heads, tokens);
@@ -1166,7 +1311,7 @@ extern "C" int ahip_op_argmax(ahip_context* ctx, const float* logits, int n, int
         DevBuf dl, di;
         if (int rc = upload(dl, logits, (size_t)n * 4, st)) return rc;
         if (int rc = di.alloc(4)) return rc;
-        LAUNCH(launch_argmax(dl.as<float>(), n, di.as<int32_t>(), nullptr, 0, st));
+        LAUNCH(launch_argmax(dl.as<float>(), n, di.as<int32_t>(), nullptr, 0, nullptr, st));
         return download(index, di, 4, st);
     });
 }

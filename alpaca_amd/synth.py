@@ -51,7 +51,7 @@ C1 = ModelSpec("C1-135M-Q8_0", _cfg(49152, 576, 30, 9, 3, 1536, 8192), Q8_0, see
 C4 = ModelSpec("C4-360M-Q4_0", _cfg(49152, 960, 32, 15, 5, 2560, 4096), Q4_0, seed=3)
 C5 = ModelSpec("C5-1.7B-Q8_0", _cfg(49152, 2048, 24, 32, 32, 8192, 4608), Q8_0, seed=4)
 # Small variants with the same structure, for parity tests the oracle runs in seconds.
-TINY = ModelSpec("tiny-Q8_0", _cfg(1000, 256, 3, 4, 2, 512, 1024), Q8_0, seed=11)
+TINY = ModelSpec("tiny-Q8_0", _cfg(1000, 256, 3, 4, 2, 512, 1024), Q8_0, seed=11, std=0.1)
 SPECS = {s.name: s for s in (C1, C4, C5, TINY)}
 
 

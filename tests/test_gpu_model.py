@@ -5,10 +5,13 @@ across chunks and reset, greedy chain vs synchronous decoding, early stop,
 capacity) and TransformerTests.swift (tiny models), on synthetic weights and
 on the reference's tiny_llama.json fixture.
 
-Tolerances (north star): logits within 2e-3 absolute + 1e-3 relative of the
-oracle, greedy ids identical.  The exact configuration (float32 GEMMs, f32
-KV) is held to 1e-4.  With an f16 KV cache the oracle rounds its cache rows
-through f16 as well (KVCache.roundsToFloat16), as the reference does.
+Tolerances: the C1 north-star test holds logits within 2e-3 absolute + 1e-3
+relative of the oracle and greedy ids identical.  The exact configuration
+(float32 GEMMs, f32 KV) is held to 1e-4 everywhere.  Other fast-path cases
+(f16 MFMA operands) use the reference's own fast-path bound: max |error| /
+max |logit| <= 3e-3 (MetalRealModelTests.swift, NUMERICAL_VALIDATION.md
+"peak-relative 3e-3"), plus greedy agreement.  With an f16 KV cache the oracle
+rounds its cache rows through f16 as well (KVCache.roundsToFloat16).
 """
 import numpy as np
 import pytest
@@ -46,6 +49,18 @@ def gpu_model(ctx, spec):
     return HIPLlamaModel(ctx, spec.config, built(spec))
 
 
+def check(g, e, kv, prec, label):
+    if prec == "exact" and kv == "f32":
+        assert_close(g, e, 1e-4, 0.0, label)
+    elif prec == "exact":
+        assert_close(g, e, 2e-3, 1e-3, label)
+    else:
+        m = metrics(g, e)
+        print(f"[metrics] {label}: {m}")
+        assert m["max_rel_peak"] <= 3e-3, label
+    assert int(np.argmax(g)) == int(np.argmax(e)), label
+
+
 TINY_SPECS = [synth.TINY, synth.with_dtype(synth.TINY, Q4_0), synth.with_dtype(synth.TINY, F16)]
 
 
@@ -58,19 +73,56 @@ def test_tiny_prefill_and_decode_match_oracle(hip_ctx, spec, kv, prec):
     prompt = synth.prompt_tokens(spec, 40)
     s = model.make_session(capacity=128, max_batch=512, kv_precision=kv, gemm_precision=prec)
     okv = orc.OracleKV(oracle_cfg(c), 128, rounds_f16=(kv == "f16"))
-    tol = (1e-4, 0.0) if (prec == "exact" and kv == "f32") else (2e-3, 1e-3)
     g = s.forward(prompt)
     e = orc.forward(om, okv, prompt)
-    assert_close(g, e, *tol, f"{spec.name} {kv}/{prec} prefill")
-    assert int(np.argmax(g)) == orc.argmax(e)
+    check(g, e, kv, prec, f"{spec.name} {kv}/{prec} prefill")
     tok = orc.argmax(e)
     for step in range(6):
         g = s.decode(tok)
         e = orc.forward(om, okv, [tok])
-        assert_close(g, e, *tol, f"{spec.name} {kv}/{prec} decode {step}")
-        assert int(np.argmax(g)) == orc.argmax(e)
+        check(g, e, kv, prec, f"{spec.name} {kv}/{prec} decode {step}")
         tok = orc.argmax(e)
     assert s.length == 46
+
+
+@pytest.mark.parametrize("prec", ["exact", "fast"])
+def test_split_half_rope_layout_matches_oracle(hip_ctx, prec):
+    """Hugging Face split-half RoPE (ropeInterleaved = false): q/k rows are
+    re-paired at upload; logits must still match the oracle's split-half rotation."""
+    from dataclasses import replace
+    spec = replace(synth.TINY, config=replace(synth.TINY.config, rope_interleaved=False), name="tiny-hf")
+    c = spec.config
+    w = built(synth.TINY)
+    model = HIPLlamaModel(hip_ctx, c, w)
+    om = oracle_model(c, w)
+    prompt = synth.prompt_tokens(spec, 33)
+    kv = "f32" if prec == "exact" else "f16"
+    s = model.make_session(capacity=64, kv_precision=kv, gemm_precision=prec)
+    okv = orc.OracleKV(oracle_cfg(c), 64, rounds_f16=(kv == "f16"))
+    check(s.forward(prompt), orc.forward(om, okv, prompt), kv, prec, f"split-half prefill {prec}")
+    for t in (5, 17, 900):
+        check(s.decode(t), orc.forward(om, okv, [t]), kv, prec, f"split-half decode {prec}")
+
+
+def test_profiled_greedy_equals_graph_greedy(hip_ctx):
+    """The greedy chain replays a captured HIP graph; with profiling on it launches the
+    same kernels eagerly.  Both must emit the same tokens, and stages must be reported."""
+    spec = synth.TINY
+    model = gpu_model(hip_ctx, spec)
+    prompt = synth.prompt_tokens(spec, 50)
+    out = []
+    for prof in (False, True, False):
+        s = model.make_session(capacity=256)
+        s.profiling_enabled = prof
+        first = int(np.argmax(s.forward(prompt)))
+        got = []
+        s.decode_greedy(first, 60, lambda t: got.append(t) or True)
+        out.append(got)
+        if prof:
+            st = s.last_profile
+            assert st["attention"].dispatches == 60 * spec.config.layer_count
+            assert "sample" in st and st["qkv (fused norm)"].seconds > 0
+    assert out[0] == out[1] == out[2]
 
 
 def test_chunked_prefill_equals_single_pass_and_reset_is_deterministic(hip_ctx):
