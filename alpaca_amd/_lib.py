@@ -91,6 +91,7 @@ SIGNATURES = {
     "ahip_session_last_encode_seconds": (i, [vp, dp]),
     "ahip_session_set_profiling": (i, [vp, i]),
     "ahip_session_profile": (i, [vp, C.POINTER(StageC), i, C.POINTER(C.c_int)]),
+    "ahip_session_decode_timeline": (i, [vp, C.POINTER(C.c_uint64), i64, i64p, C.POINTER(C.c_int), dp]),
     "ahip_op_add": (i, [vp, fp, fp, i64, fp]),
     "ahip_op_mul": (i, [vp, fp, fp, i64, fp]),
     "ahip_op_silu": (i, [vp, fp, i64, fp]),

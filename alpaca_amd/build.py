@@ -17,7 +17,17 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libalpaca_hip.so")
-SOURCES = ["kernels_misc.hip", "kernels_gemv.hip", "kernels_gemm.hip", "kernels_attention.hip", "runtime.cpp"]
+# (source, object name, extra defines).  kernels_decode.hip is compiled once per
+# (weight format, head dim) variant of the persistent decode kernel, so the
+# large inlined kernels build in parallel, and once for its host side.
+DECODE_VARIANTS = [(fmt, hd) for fmt in ("q8", "q4", "f16") for hd in (64, 128)]
+DECODE_FMT_ENUM = {"q8": "DT_Q8_0", "q4": "DT_Q4_0", "f16": "DT_F16"}
+SOURCES = [("kernels_decode.hip", f"kernels_decode_{fmt}_hd{hd}",
+            [f"-DDECODE_FMT={DECODE_FMT_ENUM[fmt]}", f"-DDECODE_HD={hd}", f"-DDECODE_ENTRY=decode_kernel_{fmt}_hd{hd}"])
+           for fmt, hd in DECODE_VARIANTS]
+SOURCES += [(src, os.path.splitext(src)[0], []) for src in
+            ("kernels_decode.hip", "kernels_misc.hip", "kernels_gemv.hip", "kernels_gemm.hip",
+             "kernels_attention.hip", "runtime.cpp")]
 ARCH = "gfx950"
 # Packed FP32 instructions are disabled: hipcc -O3 otherwise emits v_pk_* forms.
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-function",
@@ -31,9 +41,10 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *FLAGS, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+def _compile(item) -> str:
+    src, name, defines = item
+    obj = os.path.join(BUILD, name + ".o")
+    cmd = [hipcc(), *FLAGS, *defines, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -9,6 +9,32 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// Address-space casts: pointers read from structs are generic to the
+// compiler, which then emits flat instructions (counted against both the
+// vector-memory and the LDS wait counters).  Loads through gptr() are
+// global_load instructions.
+#define AS_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ const AS_GLOBAL T* gptr(const T* p) {
+    return (const AS_GLOBAL T*)p;
+}
+template <typename T>
+__device__ __forceinline__ AS_GLOBAL T* gptr(T* p) {
+    return (AS_GLOBAL T*)p;
+}
+// 16- and 8-byte global loads into HIP's vector classes (through the native
+// vector types, which address-space-qualified loads accept).
+__device__ __forceinline__ int4 gload_i4(const void* p) {
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    const v4i v = *(const AS_GLOBAL v4i*)p;
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float2 gload_f2(const void* p) {
+    typedef float v2f __attribute__((ext_vector_type(2)));
+    const v2f v = *(const AS_GLOBAL v2f*)p;
+    return make_float2(v.x, v.y);
+}
+
 enum { DT_F32 = 0, DT_F16 = 1, DT_Q8_0 = 2, DT_Q4_0 = 3 };
 
 // A weight matrix [rows, cols] resident in HBM.  Quantised formats are split
@@ -24,16 +50,42 @@ struct DevMatrix {
     const f16* s = nullptr;
 };
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// Cross-lane moves.  DPP controls (gfx9) act inside 16-lane rows without the
+// LDS crossbar: quad_perm [1,0,3,2] = 0xB1 and [2,3,0,1] = 0x4E swap lanes
+// xor 1 and xor 2; row_half_mirror (0x141) pairs the two quads of each
+// 8-lane half, row_mirror (0x140) the two halves of a row; row_ror:8 (0x128)
+// is xor 8.  Xor 16 is a ds_swizzle in bit-mask mode (and 0x1F, xor 0x10)
+// and xor 32 a ds_bpermute.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float swizzle_xor16(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+// Reduction over aligned groups of N lanes (N a power of two up to 64); every
+// lane of a group gets the result.  All lanes combine in the same tree, so the
+// result is identical across the group.
+template <int N, typename Op>
+__device__ __forceinline__ float lane_reduce(float v, Op op) {
+    if (N >= 2) v = op(v, dpp_mov<0xB1>(v));
+    if (N >= 4) v = op(v, dpp_mov<0x4E>(v));
+    if (N >= 8) v = op(v, dpp_mov<0x141>(v));
+    if (N >= 16) v = op(v, dpp_mov<0x140>(v));
+    if (N >= 32) v = op(v, swizzle_xor16(v));
+    if (N >= 64) v = op(v, __shfl_xor(v, 32, 64));
     return v;
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
+struct AddOp {
+    __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+};
+struct MaxOp {
+    __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+template <int N>
+__device__ __forceinline__ float lane_sum(float v) { return lane_reduce<N>(v, AddOp()); }
+__device__ __forceinline__ float wave_sum(float v) { return lane_reduce<64>(v, AddOp()); }
+__device__ __forceinline__ float wave_max(float v) { return lane_reduce<64>(v, MaxOp()); }
 
 // Block-wide sum over blockDim.x (a multiple of 64, at most 1024) threads.
 __device__ __forceinline__ float block_sum(float v, float* red /* >= 16 floats of LDS */) {
@@ -110,6 +162,59 @@ hipError_t launch_gemm_mfma(const f16* x, int ldx, int m, const DevMatrix& w, co
 // exact: x f32; float32 FMA in the reference's per-block order.  SWIGLU writes y f32.
 hipError_t launch_gemm_f32(const float* x, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up, float* y,
                            int ldy, int mode, hipStream_t st);
+
+// persistent single-token decode (kernels_decode.hip)
+//
+// One cooperative launch computes one token: every decoder layer, the logits
+// and the greedy arg-max.  Phases hand data to each other through exchange
+// words (8 bytes: f32 value in the low half, the launch's tag in the high
+// half) written and polled with agent-scope atomics; see kernels_decode.hip.
+struct DecLayer {
+    DevMatrix qkv, wo, gate, up, down;
+    const float* attn_norm = nullptr;
+    const float* ffn_norm = nullptr;
+    void* kc = nullptr;  // f16 [kv_heads][capacity][head_dim]
+    void* vc = nullptr;
+};
+struct DecodeParams {
+    const DecLayer* layers = nullptr;  // device array [n_layers]
+    int n_layers = 0, hidden = 0, heads = 0, kv_heads = 0, hd = 0, ffn = 0, vocab = 0, capacity = 0;
+    float eps = 0.f;
+    const float2* rope = nullptr;  // (cos, sin) [positions][hd/2]
+    DevMatrix embed, out;
+    const float* out_norm = nullptr;
+    int32_t* chain = nullptr;      // device word: input token, replaced by the arg-max
+    int* pos = nullptr;            // device word: position of the input token, advanced by one
+    unsigned* epoch = nullptr;     // device word: tag of this launch's exchange words, advanced by one
+    int32_t* emitted = nullptr;    // mapped host [capacity] (arg-max at emitted[pos]) or null
+    int* status = nullptr;         // mapped host word, set non-zero if the launch aborted
+    unsigned* abort_word = nullptr;  // device word shared by all workgroups of a launch
+    unsigned long long* xbuf = nullptr;  // exchange words
+    float* logits = nullptr;       // device [vocab] or null
+    unsigned long long* trace = nullptr;  // [decode_trace_points][grid] wall-clock stamps, or null
+    long long timeout_ticks = 0;   // bound on every wait, in wall-clock ticks
+    int abort_at_layer = -1;       // failure-path tests: workgroup 0 aborts the launch at this layer
+    int target_items = 64;         // attention work items to aim for
+    int max_splits = 1;            // splits per head the partial buffer holds
+    int stage = 0;                 // floats of the LDS staging row
+    // exchange-word offsets within one layer's block, and the block size
+    int off_part = 0, off_ctx = 0, off_xa = 0, off_ffn = 0, off_xf = 0, layer_words = 0, off_cand = 0;
+    // rows per workgroup of each projection (even)
+    int rows_qkv = 0, rows_wo = 0, rows_ffn = 0, rows_down = 0, rows_out = 0;
+};
+// Phase-end stamps per launch: [0] start, 6 per layer (qkv, attention, merge,
+// wo, gate/up, down), then logits and the arg-max (workgroup 0 only).
+__host__ __device__ inline int decode_trace_points(int layers) { return 3 + 6 * layers; }
+// After those points, kDecodeAttnSubPoints stamps inside the attention item of
+// the last layer: entry, loads issued, q ready, current k/v ready, scores,
+// softmax, P.V, published.
+constexpr int kDecodeAttnSubPoints = 8;
+// Support, shared-memory size and launch of the persistent decode kernel.
+bool decode_kernel_supported(int fmt, int hd, int heads, int kv_heads);
+int decode_attention_max_splits(int capacity, int kv_heads, int target_items);
+size_t decode_lds_bytes(const DecodeParams& p, int grid);
+hipError_t decode_kernel_occupancy(int fmt, int hd, int heads, int kv_heads, size_t lds, int* blocks_per_cu);
+hipError_t launch_decode_step(int fmt, const DecodeParams& p, int grid, size_t lds, hipStream_t st);
 
 // attention (kernels_attention.hip).  Cache layout [kv_heads][capacity][hd].
 // q rows are [tokens][heads][hd] with row stride ldq (elements).

@@ -1,0 +1,929 @@
+// Persistent single-token decode for gfx950: one cooperative launch runs a
+// whole decode step of the Llama forward pass (every layer, the logits and the
+// greedy arg-max) for one token.
+//
+// Replaces the reference's fused decode dispatch chain (MetalLlamaModel.swift:
+// 344-356 and the greedy chain at :234-270: decodeQKV, ropeQKVStore, split-K
+// attention + merge, decodeProjection(wo, add), decodeGateUp,
+// decodeProjection(wDown, add), then norm + logits and argmax_logits).  The
+// CPU semantics are LlamaCPUModel.forward for one token
+// (LlamaCPUModel.swift:24-61).
+//
+// Why one launch: at these model sizes each projection streams 0.3-2 MB, a
+// fraction of a microsecond of HBM time, while a kernel boundary costs several
+// microseconds.  Here the phases of a layer hand results to each other inside
+// one launch:
+//
+//   P1 QKV      rows of the stacked [q|k|v] matrix with the RMSNorm prologue and
+//               the RoPE epilogue; k/v rows also go to the KV cache.
+//   P2 attn     split-K attention: item (KV head, split of the context) serves
+//               the G query heads of that KV head; writes (max, sum, output).
+//   P3 merge    one item per query head merges its splits into the context row.
+//   P4 Wo       rows of Wo plus the residual.
+//   P5 gate/up  rows of gate and up with the RMSNorm prologue, SwiGLU epilogue.
+//   P6 down     rows of down plus the residual.
+//   then P7 logits (final norm + output rows + a per-workgroup arg-max) and
+//   P8 the arg-max reduction in workgroup 0.
+//
+// Hand-off: every value a phase produces is written as an 8-byte exchange word,
+// (launch tag << 32) | f32 bits, with one agent-scope atomic store; a consumer
+// polls the words themselves with agent-scope atomic loads until every tag
+// equals this launch's tag.  The barrier and the data transfer are one memory
+// round trip, and a consumer waits only for the words it reads.  Each phase
+// has its own words per layer, so no word is written twice in a launch; the
+// tag (a per-session counter advanced by every launch) separates launches.
+//
+// Before waiting, a workgroup issues the loads of its weight rows (and, in P2,
+// of its cached K/V rows), so HBM latency overlaps the wait.  Rows written to
+// the KV cache in this launch are read by attention only through the exchange
+// words; cache rows of earlier positions come from earlier launches, whose
+// completion makes them visible.
+//
+// The launch parameters and the current layer's table sit in LDS, so every
+// phase reads them with ds_read rather than with dependent memory loads.
+// Every phase is inlined into the kernel (a call would save and restore the
+// callee-saved registers through scratch memory on each phase); to keep the
+// build parallel, this file is compiled once per (weight format, head dim)
+// with DECODE_FMT / DECODE_HD / DECODE_ENTRY set, each object holding the
+// kernels for its group sizes, and once without them for the host side.
+//
+// Every wait is bounded: past `timeout_ticks` of the wall clock, or when any
+// workgroup has raised the shared abort word, a workgroup raises the abort
+// word and the mapped status word and returns, so a launch always drains.  The
+// launch is cooperative, so all workgroups are resident at once.
+#include "common.h"
+#include "gemv_chunks.h"
+
+#include <limits.h>
+
+namespace {
+
+constexpr int kT = 256;  // threads per workgroup
+constexpr int kWaves = kT / 64;
+constexpr int kMaxSplitLen = 256;  // positions per attention item (one per thread)
+constexpr int kMinSplitLen = 64;
+constexpr int kRedFloats = 32;
+
+// Attention decomposition for a context of `len` positions: split length in
+// [64, 256] aiming at `target` items over all KV heads.
+__device__ __host__ inline int split_len_for(int len, int kv_heads, int target) {
+    int sl = (len * kv_heads + target - 1) / target;
+    sl = (sl + kMinSplitLen - 1) / kMinSplitLen * kMinSplitLen;
+    return sl < kMinSplitLen ? kMinSplitLen : (sl > kMaxSplitLen ? kMaxSplitLen : sl);
+}
+
+// Group-size bucket: the kernel variant sized for G query heads per KV head.
+__host__ __device__ inline int group_bucket(int g) { return g <= 1 ? 1 : g <= 2 ? 2 : g <= 4 ? 4 : g <= 8 ? 8 : 16; }
+
+}  // namespace
+
+#ifdef DECODE_FMT
+
+namespace {
+
+using gemv::RowStream;
+typedef unsigned long long u64;
+
+// ------------------------------------------------------------------ LDS
+// Launch parameters and the current layer's table (copied by every workgroup).
+__shared__ __attribute__((aligned(16))) unsigned char lds_params[sizeof(DecodeParams)];
+__shared__ __attribute__((aligned(16))) unsigned char lds_layer[sizeof(DecLayer)];
+__device__ __forceinline__ const DecodeParams& P() { return *reinterpret_cast<const DecodeParams*>(lds_params); }
+__device__ __forceinline__ const DecLayer& LY() { return *reinterpret_cast<const DecLayer*>(lds_layer); }
+
+// Dynamic LDS: [0, 32) reductions; xres [hidden], the residual row of the
+// current half-layer; xn [stage], the normalised or staged input row; then
+// scratch.
+extern __shared__ float dyn_lds[];
+struct Shared {
+    float* red;
+    float* xres;
+    float* xn;
+    float* scr;
+};
+__device__ __forceinline__ Shared lds_of() {
+    Shared l;
+    l.red = dyn_lds;
+    l.xres = dyn_lds + kRedFloats;
+    l.xn = l.xres + P().hidden;
+    l.scr = l.xn + P().stage;
+    return l;
+}
+
+// ------------------------------------------------------------------ exchange words
+__device__ __forceinline__ u64 ld_word(const u64* p) {
+    return __hip_atomic_load(gptr(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void put_word(u64* p, float v, unsigned tag) {
+    __hip_atomic_store(gptr(p), ((u64)tag << 32) | (u64)__float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned ld_flag(const unsigned* p) {
+    return __hip_atomic_load(gptr(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct Ctl {
+    unsigned tag;
+    unsigned* abort_word;
+    int* status;
+    long long timeout;
+};
+
+__device__ __noinline__ void raise_abort(Ctl c) {
+    __hip_atomic_store(gptr(c.abort_word), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (c.status) *(volatile int*)c.status = 1;
+}
+
+// Waits until the n words at src carry this launch's tag and copies their
+// values to dst (LDS).  Called by every thread of the workgroup; returns false
+// (for every thread) when the launch is aborting.  All of a thread's pending
+// words are re-polled together, so a wait costs one round trip once the data
+// is there.  Indices past n are clamped to word n-1 for loading (never stored).
+__device__ __forceinline__ bool wait_words(const u64* src, int n, float* dst, const Ctl& c) {
+    constexpr int B = 8;
+    int bad = 0;
+    for (int base = 0; base < n && !bad; base += B * kT) {
+        u64 w[B];
+        unsigned pend = 0;
+#pragma unroll
+        for (int k = 0; k < B; k++) {
+            const int i = base + threadIdx.x + k * kT;
+            w[k] = ld_word(src + (i < n ? i : n - 1));
+            if (i < n) pend |= 1u << k;
+        }
+        long long t0 = 0;
+        int it = 0;
+        while (true) {
+#pragma unroll
+            for (int k = 0; k < B; k++)
+                if (((pend >> k) & 1u) && (unsigned)(w[k] >> 32) == c.tag) {
+                    dst[base + threadIdx.x + k * kT] = __uint_as_float((unsigned)w[k]);
+                    pend &= ~(1u << k);
+                }
+            if (!pend) break;
+            if ((it++ & 31) == 0) {
+                const long long now = wall_clock64();
+                if (t0 == 0) t0 = now;
+                if (now - t0 > c.timeout || ld_flag(c.abort_word)) {
+                    bad = 1;
+                    break;
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < B; k++) {
+                const int i = base + threadIdx.x + k * kT;
+                if ((pend >> k) & 1u) w[k] = ld_word(src + (i < n ? i : n - 1));
+            }
+        }
+    }
+    if (bad) raise_abort(c);
+    return !__syncthreads_or(bad);
+}
+
+// Block-wide sum over the 256 threads (result in every thread).
+__device__ __forceinline__ float block_sum4(float v, float* red) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// Element k of row r of a resident matrix, dequantised exactly (Quantization.swift:9-35).
+__device__ __forceinline__ float matrix_elem(const DevMatrix& m, int64_t r, int k) {
+    if (m.dtype == DT_F16) return (float)*gptr((const f16*)m.q + r * m.cols + k);
+    const int nb = m.cols / 32;
+    const float d = (float)*gptr(m.s + r * nb + k / 32);
+    if (m.dtype == DT_Q8_0) return d * (float)(int)*gptr((const int8_t*)m.q + r * m.cols + k);
+    const int j = k & 31;
+    const uint8_t b = *gptr(m.q + (r * nb + k / 32) * 16 + (j & 15));
+    return d * (float)((int)(j < 16 ? (b & 15) : (b >> 4)) - 8);
+}
+
+// x (LDS, n floats) -> out = (x * (1/sqrt(mean(x^2) + eps))) * w  (CPUOps.rmsNorm, CPUOps.swift:144-159).
+__device__ __forceinline__ void rmsnorm_lds(const float* x, const float* w, int n, float eps, float* out, float* red) {
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += kT) ss += x[i] * x[i];
+    ss = block_sum4(ss, red);
+    const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += kT) out[i] = (x[i] * scale) * *gptr(w + i);
+    __syncthreads();
+}
+
+// ------------------------------------------------------------------ GEMV rows
+// Rows [r0, r1) of one or two matrices (same shape) against xs in LDS, LPR
+// lanes per row, kWaves*64/LPR rows per pass.  The first pass's weights are
+// loaded by prefetch(); later passes are double-buffered (the next pass's
+// loads are in flight while the current pass is reduced).  Rows past r1 are
+// clamped to r1-1 for loading and never used.  epi(row, a0, a1) runs on the
+// row's first lane.
+template <int FMT, int LPR, bool TWO>
+struct Rows {
+    static constexpr int RPB = kWaves * (64 / LPR);
+    RowStream<FMT, LPR> a0, a1, b0, b1;
+    int li, local;
+    __device__ __forceinline__ Rows() {
+        const int lane = threadIdx.x & 63;
+        li = lane % LPR;
+        local = (threadIdx.x >> 6) * (64 / LPR) + lane / LPR;
+    }
+    __device__ __forceinline__ void load(RowStream<FMT, LPR>& s0, RowStream<FMT, LPR>& s1, const DevMatrix& w0,
+                                         const DevMatrix& w1, int base, int r1) {
+        const int r = min(base + local, r1 - 1);
+        s0.prefetch(w0, r, w0.cols, li);
+        if (TWO) s1.prefetch(w1, r, w0.cols, li);
+    }
+    __device__ __forceinline__ void prefetch(const DevMatrix& w0, const DevMatrix& w1, int r0, int r1) {
+        if (r0 < r1) load(a0, a1, w0, w1, r0, r1);
+    }
+    template <typename Epi>
+    __device__ __forceinline__ void pass(RowStream<FMT, LPR>& s0, RowStream<FMT, LPR>& s1, const DevMatrix& w0,
+                                         const DevMatrix& w1, int base, int r1, const float* xs, Epi& epi) {
+        const int r = base + local;
+        float v0 = 0.f, v1 = 0.f;
+        if (r < r1) {
+            v0 = s0.finish(w0, r, w0.cols, li, xs);
+            if (TWO) v1 = s1.finish(w1, r, w0.cols, li, xs);
+        }
+        v0 = lane_sum<LPR>(v0);
+        if (TWO) v1 = lane_sum<LPR>(v1);
+        if (r < r1 && li == 0) epi(r, v0, v1);
+    }
+    template <typename Epi>
+    __device__ __forceinline__ void run(const DevMatrix& w0, const DevMatrix& w1, int r0, int r1, const float* xs,
+                                        Epi epi) {
+        for (int base = r0; base < r1;) {
+            int nxt = base + RPB;
+            if (nxt < r1) load(b0, b1, w0, w1, nxt, r1);
+            pass(a0, a1, w0, w1, base, r1, xs, epi);
+            base = nxt;
+            if (base >= r1) break;
+            nxt = base + RPB;
+            if (nxt < r1) load(a0, a1, w0, w1, nxt, r1);
+            pass(b0, b1, w0, w1, base, r1, xs, epi);
+            base = nxt;
+        }
+    }
+};
+
+// The rows of a projection handled by this workgroup.
+__device__ __forceinline__ void my_rows(int rows_per_wg, int total, int& r0, int& r1) {
+    r0 = min(total, (int)blockIdx.x * rows_per_wg);
+    r1 = min(total, r0 + rows_per_wg);
+}
+
+// Runs `f.template go<LPR>()` with the lanes-per-row suited to a row count.
+template <typename F>
+__device__ __forceinline__ bool with_lpr(int rows, F& f) {
+    if (rows <= kWaves) return f.template go<64>();
+    if (rows <= 2 * kWaves) return f.template go<32>();
+    return f.template go<16>();
+}
+
+// ------------------------------------------------------------------ phases
+
+// P1: QKV rows with RMSNorm prologue and RoPE epilogue.  On return xres holds
+// the layer's input row (kept for the Wo residual).
+template <int FMT>
+struct PhaseQKV {
+    const u64* xin;  // previous layer's xf words, or null for layer 0
+    u64* out;        // this layer's qkv words
+    int pos, token;
+    Ctl c;
+    template <int LPR>
+    __device__ bool go() {
+        const DecodeParams& p = P();
+        const DecLayer& L = LY();
+        const Shared sh = lds_of();
+        const DevMatrix W = L.qkv;
+        int r0, r1;
+        my_rows(p.rows_qkv, W.rows, r0, r1);
+        Rows<FMT, LPR, false> rw;
+        rw.prefetch(W, W, r0, r1);
+        const int H = p.hidden;
+        if (xin) {
+            if (!wait_words(xin, H, sh.xres, c)) return false;
+        } else {
+            const DevMatrix E = p.embed;
+            for (int k = threadIdx.x; k < H; k += kT) sh.xres[k] = matrix_elem(E, token, k);
+            __syncthreads();
+        }
+        rmsnorm_lds(sh.xres, L.attn_norm, H, p.eps, sh.xn, sh.red);
+        float* rowbuf = sh.scr;
+        rw.run(W, W, r0, r1, sh.xn, [&](int r, float v, float) { rowbuf[r - r0] = v; });
+        __syncthreads();
+        // RoPE on (even, odd) row pairs of q and k (CPUOps.rope, CPUOps.swift:184-212), f16
+        // rounding of k/v as the cache stores them, cache append at row pos
+        // (KVCache.write, KVCache.swift:44-63) and publication of every row.
+        const int hd = p.hd, QW = p.heads * hd, KW = p.kv_heads * hd, half = hd / 2, cap = p.capacity;
+        const float2* rope = p.rope;
+        f16* kc = (f16*)L.kc;
+        f16* vc = (f16*)L.vc;
+        for (int i = threadIdx.x; 2 * i < r1 - r0; i += kT) {
+#pragma clang fp contract(off)
+            const int r = r0 + 2 * i;
+            float v0 = rowbuf[2 * i], v1 = rowbuf[2 * i + 1];
+            const int d = r % hd;
+            if (r < QW + KW) {
+                const float2 cs = gload_f2(rope + (int64_t)pos * half + d / 2);
+                const float ac = v0 * cs.x, bs = v1 * cs.y, as = v0 * cs.y, bc = v1 * cs.x;
+                v0 = ac - bs;
+                v1 = as + bc;
+            }
+            if (r >= QW) {
+                const bool isk = r < QW + KW;
+                const int h = (r - (isk ? QW : QW + KW)) / hd;
+                const f16 h0 = (f16)v0, h1 = (f16)v1;
+                f16* cache = (isk ? kc : vc) + ((int64_t)h * cap + pos) * hd + d;
+                *gptr(cache) = h0;
+                *gptr(cache + 1) = h1;
+                v0 = (float)h0;
+                v1 = (float)h1;
+            }
+            put_word(out + r, v0, c.tag);
+            put_word(out + r + 1, v1, c.tag);
+        }
+        return true;
+    }
+};
+
+// P2: split-K attention over the f16 cache.  Item (j, s): KV head j, context
+// positions [s*SL, min((s+1)*SL, len)).  Scores: TPP = HD/DPT threads per
+// position, each holding a DPT-wide slice of the G query rows in registers
+// and a DPT-wide slice of the K row (prefetched before the wait); the partial
+// dots are reduced across the TPP lanes.  P.V: HD/8 threads per V row.
+// Writes, per query head g of the group, the words
+// [max (base-2 units), sum, unnormalised output[HD]] of the split
+// (attention_decode.metal:27-116 computes the same triple).
+template <int HD, int GM>
+__device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int pos, Ctl c) {
+    constexpr int DPT = GM <= 4 ? 16 : 8;      // query/key dims per thread in the scores
+    constexpr int KV4 = DPT / 8;               // 16-byte K chunks per thread and position
+    constexpr int TPP = HD / DPT;              // threads per position
+    constexpr int PPP = kT / TPP;              // positions per score pass
+    constexpr int NKP = kMaxSplitLen / PPP;    // score passes
+    constexpr int TPR = HD / 8;                // threads per V row
+    constexpr int RPP = kT / TPR;              // V rows per pass
+    constexpr int NVP = kMaxSplitLen / RPP;    // V passes
+    const DecodeParams& p = P();
+    const DecLayer& L = LY();
+    float* scr = lds_of().scr;
+    const int heads = p.heads, kvh = p.kv_heads, G = heads / kvh, QW = heads * HD, KW = kvh * HD;
+    const int cap = p.capacity, max_splits = p.max_splits;
+    const int len = pos + 1;
+    const int SL = split_len_for(len, kvh, p.target_items);
+    const int S = (len + SL - 1) / SL, items = kvh * S;
+    const f16* kcache = (const f16*)L.kc;
+    const f16* vcache = (const f16*)L.vc;
+    float* qs = scr;                        // [GM][HD]
+    float* kcur = qs + GM * HD;             // [HD]
+    float* vcur = kcur + HD;                // [HD]
+    float* es = vcur + HD;                  // [GM][kMaxSplitLen]: scores, then probabilities
+    float* red = es + GM * kMaxSplitLen;    // [GM][8]
+    float* ws = red + GM * 8;               // [2*kWaves][GM][HD]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tr = tid % TPR, rq = tid / TPR;      // P.V layout
+    const int tq = tid % TPP, pq = tid / TPP;      // score layout
+    const float sl2 = 1.4426950408889634f / sqrtf((float)HD);
+    unsigned long long* sub_trace =
+        p.trace ? p.trace + (int64_t)decode_trace_points(p.n_layers) * gridDim.x : nullptr;
+    auto sub = [&](int k) {
+        if (sub_trace && tid == 0) *gptr(sub_trace + (int64_t)k * gridDim.x + blockIdx.x) = wall_clock64();
+    };
+    for (int it = blockIdx.x; it < items; it += gridDim.x) {
+        sub(0);
+        const int j = it / S, s = it - j * S;
+        const int p0 = s * SL, p1 = min(p0 + SL, len), n = p1 - p0;
+        const int nc = min(p1, pos) - p0;  // positions read from the cache
+        const bool has_cur = p1 == len;
+        const f16* kb = kcache + ((int64_t)j * cap + p0) * HD;
+        const f16* vb = vcache + ((int64_t)j * cap + p0) * HD;
+        // cache rows past nc are loaded from row 0 of the split (valid memory) and never used
+        int4 kr[NKP][KV4];
+#pragma unroll
+        for (int k = 0; k < NKP; k++) {
+            const int r = k * PPP + pq;
+#pragma unroll
+            for (int u = 0; u < KV4; u++) kr[k][u] = gload_i4(kb + (int64_t)(r < nc ? r : 0) * HD + tq * DPT + 8 * u);
+        }
+        int4 vr[NVP];
+#pragma unroll
+        for (int k = 0; k < NVP; k++) {
+            const int r = k * RPP + rq;
+            vr[k] = gload_i4(vb + (int64_t)(r < nc ? r : 0) * HD + tr * 8);
+        }
+        sub(1);
+        if (!wait_words(qkv + j * G * HD, G * HD, qs, c)) return false;
+        sub(2);
+        if (has_cur) {
+            if (!wait_words(qkv + QW + j * HD, HD, kcur, c)) return false;
+            if (!wait_words(qkv + QW + KW + j * HD, HD, vcur, c)) return false;
+        }
+        for (int i = G * HD + tid; i < GM * HD; i += kT) qs[i] = 0.f;  // rows past the group
+        __syncthreads();
+        sub(3);
+        // this thread's slice of the query rows, in base-2 exponent units
+        float qr[GM][DPT];
+#pragma unroll
+        for (int g = 0; g < GM; g++)
+#pragma unroll
+            for (int e = 0; e < DPT; e += 4) {
+                const float4 t = *(const float4*)&qs[g * HD + tq * DPT + e];
+                qr[g][e] = t.x * sl2;
+                qr[g][e + 1] = t.y * sl2;
+                qr[g][e + 2] = t.z * sl2;
+                qr[g][e + 3] = t.w * sl2;
+            }
+#pragma unroll
+        for (int k = 0; k < NKP; k++) {
+            if (k * PPP < n) {  // uniform across the workgroup
+                const int r = k * PPP + pq;
+                float kf[DPT];
+                if (r < nc) {
+#pragma unroll
+                    for (int u = 0; u < KV4; u++) {
+                        const f16* kh = (const f16*)&kr[k][u];
+#pragma unroll
+                        for (int e = 0; e < 8; e++) kf[8 * u + e] = (float)kh[e];
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < DPT; e++) kf[e] = kcur[tq * DPT + e];
+                }
+#pragma unroll
+                for (int g = 0; g < GM; g++) {
+                    float d = 0.f;
+#pragma unroll
+                    for (int e = 0; e < DPT; e++) d += qr[g][e] * kf[e];
+                    d = lane_sum<TPP>(d);
+                    if (tq == 0 && r < kMaxSplitLen) es[g * kMaxSplitLen + r] = d;
+                }
+            }
+        }
+        __syncthreads();
+        float sc[GM];
+#pragma unroll
+        for (int g = 0; g < GM; g++) sc[g] = (tid < n && g < G) ? es[g * kMaxSplitLen + tid] : -INFINITY;
+#pragma unroll
+        for (int g = 0; g < GM; g++) {
+            const float m = wave_max(sc[g]);
+            if (lane == 0) red[g * 8 + wave] = m;
+        }
+        __syncthreads();
+        sub(4);
+        float mloc[GM];
+#pragma unroll
+        for (int g = 0; g < GM; g++)
+            mloc[g] = fmaxf(fmaxf(red[g * 8 + 0], red[g * 8 + 1]), fmaxf(red[g * 8 + 2], red[g * 8 + 3]));
+#pragma unroll
+        for (int g = 0; g < GM; g++) {
+            const float e = (tid < n && g < G) ? exp2f(sc[g] - mloc[g]) : 0.f;
+            es[g * kMaxSplitLen + tid] = e;
+            const float sum = wave_sum(e);
+            if (lane == 0) red[g * 8 + 4 + wave] = sum;
+        }
+        __syncthreads();
+        sub(5);
+        float acc[GM][8];
+#pragma unroll
+        for (int g = 0; g < GM; g++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
+#pragma unroll
+        for (int k = 0; k < NVP; k++) {
+            const int r = k * RPP + rq;
+            if (k * RPP < n) {  // uniform across the workgroup
+                float vf[8];
+                if (r < nc) {
+                    const f16* vh = (const f16*)&vr[k];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) vf[e] = (float)vh[e];
+                } else if (r < n) {  // the current position
+#pragma unroll
+                    for (int e = 0; e < 8; e++) vf[e] = vcur[tr * 8 + e];
+                } else {  // past the split: probability 0, and no uninitialised value may enter
+#pragma unroll
+                    for (int e = 0; e < 8; e++) vf[e] = 0.f;
+                }
+#pragma unroll
+                for (int g = 0; g < GM; g++) {
+                    const float pe = es[g * kMaxSplitLen + (r < kMaxSplitLen ? r : 0)];  // zero past n
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[g][e] += pe * vf[e];
+                }
+            }
+        }
+        // sum the row groups: xor 8 (DPP) and xor 16 (swizzle) inside each 32-lane half,
+        // then the 8 half-wave partials through LDS
+#pragma unroll
+        for (int g = 0; g < GM; g++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                float v = acc[g][e];
+                if (TPR <= 8) v += dpp_mov<0x128>(v);
+                v += swizzle_xor16(v);
+                acc[g][e] = v;
+            }
+        if ((lane & (32 - TPR)) == 0) {
+            const int slot = wave * 2 + (lane >> 5);
+#pragma unroll
+            for (int g = 0; g < GM; g++)
+                if (g < G)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) ws[(slot * GM + g) * HD + tr * 8 + e] = acc[g][e];
+        }
+        __syncthreads();
+        sub(6);
+        for (int i = tid; i < G * (HD + 2); i += kT) {
+            const int g = i / (HD + 2), e = i - g * (HD + 2);
+            float v;
+            if (e == 0) {
+                v = fmaxf(fmaxf(red[g * 8 + 0], red[g * 8 + 1]), fmaxf(red[g * 8 + 2], red[g * 8 + 3]));
+            } else if (e == 1) {
+                v = (red[g * 8 + 4] + red[g * 8 + 5]) + (red[g * 8 + 6] + red[g * 8 + 7]);
+            } else {
+                const int d = e - 2;
+                v = 0.f;
+#pragma unroll
+                for (int slot = 0; slot < 2 * kWaves; slot++) v += ws[(slot * GM + g) * HD + d];
+            }
+            put_word(part + ((int64_t)(j * G + g) * max_splits + s) * (HD + 2) + e, v, c.tag);
+        }
+        __syncthreads();
+        sub(7);
+    }
+    return true;
+}
+
+// P3: query head h merges its splits: w_s = 2^(m_s - M), out = sum_s w_s o_s / sum_s w_s l_s
+// (attention_decode.metal:117-133 merges the same triples).
+template <int HD>
+__device__ __forceinline__ bool merge_phase(const u64* part, u64* ctx, int pos, Ctl c) {
+    const DecodeParams& p = P();
+    const Shared sh = lds_of();
+    float* scr = sh.scr;
+    float* red = sh.red;
+    const int len = pos + 1, heads = p.heads, max_splits = p.max_splits;
+    const int SL = split_len_for(len, p.kv_heads, p.target_items);
+    const int S = (len + SL - 1) / SL;
+    float* wsplit = scr + S * (HD + 2);
+    for (int h = blockIdx.x; h < heads; h += gridDim.x) {
+        if (!wait_words(part + (int64_t)h * max_splits * (HD + 2), S * (HD + 2), scr, c)) return false;
+        float m = -INFINITY;
+        for (int s = threadIdx.x; s < S; s += kT) m = fmaxf(m, scr[s * (HD + 2)]);
+        m = wave_max(m);
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+        __syncthreads();
+        const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        float l = 0.f;
+        for (int s = threadIdx.x; s < S; s += kT) {
+            const float w = exp2f(scr[s * (HD + 2)] - M);
+            wsplit[s] = w;
+            l += w * scr[s * (HD + 2) + 1];
+        }
+        l = block_sum4(l, red + 4);
+        const float inv = 1.0f / l;
+        for (int d = threadIdx.x; d < HD; d += kT) {
+            float o = 0.f;
+            for (int s = 0; s < S; s++) o += wsplit[s] * scr[s * (HD + 2) + 2 + d];
+            put_word(ctx + h * HD + d, o * inv, c.tag);
+        }
+        __syncthreads();
+    }
+    return true;
+}
+
+// P4 / P6: rows of a projection over a staged input row plus the residual.
+template <int FMT>
+struct PhaseResidual {
+    int which;      // 0: Wo, 1: down
+    const u64* in;  // input words (W.cols of them)
+    u64* out;       // output words (W.rows)
+    Ctl c;
+    template <int LPR>
+    __device__ bool go() {
+        const DecodeParams& p = P();
+        const Shared sh = lds_of();
+        const DevMatrix W = which ? LY().down : LY().wo;
+        int r0, r1;
+        my_rows(which ? p.rows_down : p.rows_wo, W.rows, r0, r1);
+        Rows<FMT, LPR, false> rw;
+        rw.prefetch(W, W, r0, r1);
+        if (!wait_words(in, W.cols, sh.xn, c)) return false;
+        const unsigned tag = c.tag;
+        const float* xres = sh.xres;
+        u64* o = out;
+        rw.run(W, W, r0, r1, sh.xn, [&](int r, float v, float) { put_word(o + r, xres[r] + v, tag); });
+        return true;
+    }
+};
+
+// P5: gate and up rows with RMSNorm prologue and SwiGLU epilogue.  On return
+// xres holds the row after attention (kept for the down residual).
+template <int FMT>
+struct PhaseGateUp {
+    const u64* in;  // xa words
+    u64* out;       // ffn words
+    Ctl c;
+    template <int LPR>
+    __device__ bool go() {
+        const DecodeParams& p = P();
+        const DecLayer& L = LY();
+        const Shared sh = lds_of();
+        const DevMatrix Wg = L.gate, Wu = L.up;
+        int r0, r1;
+        my_rows(p.rows_ffn, Wg.rows, r0, r1);
+        Rows<FMT, LPR, true> rw;
+        rw.prefetch(Wg, Wu, r0, r1);
+        if (!wait_words(in, p.hidden, sh.xres, c)) return false;
+        rmsnorm_lds(sh.xres, L.ffn_norm, p.hidden, p.eps, sh.xn, sh.red);
+        const unsigned tag = c.tag;
+        u64* o = out;
+        rw.run(Wg, Wu, r0, r1, sh.xn,
+               [&](int r, float g, float u) { put_word(o + r, (g / (1.0f + expf(-g))) * u, tag); });
+        return true;
+    }
+};
+
+// P7: final RMSNorm, output rows (logits) and this workgroup's arg-max, which
+// it publishes as two words (value, index bits).
+template <int FMT>
+struct PhaseLogits {
+    const u64* in;  // last layer's xf words
+    u64* cand;      // [2 * gridDim.x]
+    Ctl c;
+    template <int LPR>
+    __device__ bool go() {
+        const DecodeParams& p = P();
+        const Shared sh = lds_of();
+        const DevMatrix W = p.out;
+        int r0, r1;
+        my_rows(p.rows_out, W.rows, r0, r1);
+        Rows<FMT, LPR, false> rw;
+        rw.prefetch(W, W, r0, r1);
+        if (!wait_words(in, p.hidden, sh.xres, c)) return false;
+        rmsnorm_lds(sh.xres, p.out_norm, p.hidden, p.eps, sh.xn, sh.red);
+        float best = -INFINITY;
+        int bi = INT_MAX;
+        float* logits = p.logits;
+        rw.run(W, W, r0, r1, sh.xn, [&](int r, float v, float) {
+            if (logits) *gptr(logits + r) = v;
+            if (v > best) {  // rows ascend within a lane, so ties keep the lower index; NaN never wins
+                best = v;
+                bi = r;
+            }
+        });
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float v2 = __shfl_xor(best, o, 64);
+            const int i2 = __shfl_xor(bi, o, 64);
+            if (v2 > best || (v2 == best && i2 < bi)) {
+                best = v2;
+                bi = i2;
+            }
+        }
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) {
+            sh.scr[threadIdx.x >> 6] = best;
+            ((int*)sh.scr)[8 + (threadIdx.x >> 6)] = bi;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float bv = sh.scr[0];
+            int bx = ((int*)sh.scr)[8];
+            for (int w = 1; w < kWaves; w++) {
+                const float v2 = sh.scr[w];
+                const int i2 = ((int*)sh.scr)[8 + w];
+                if (v2 > bv || (v2 == bv && i2 < bx)) {
+                    bv = v2;
+                    bx = i2;
+                }
+            }
+            put_word(cand + 2 * blockIdx.x, bv, c.tag);
+            put_word(cand + 2 * blockIdx.x + 1, __int_as_float(bx), c.tag);
+        }
+        return true;
+    }
+};
+
+template <int FMT>
+__device__ __forceinline__ bool qkv_phase(const u64* xin, u64* out, int pos, int token, Ctl c) {
+    PhaseQKV<FMT> ph{xin, out, pos, token, c};
+    return with_lpr(P().rows_qkv, ph);
+}
+template <int FMT>
+__device__ __forceinline__ bool residual_phase(int which, const u64* in, u64* out, Ctl c) {
+    PhaseResidual<FMT> ph{which, in, out, c};
+    return with_lpr(which ? P().rows_down : P().rows_wo, ph);
+}
+template <int FMT>
+__device__ __forceinline__ bool gate_up_phase(const u64* in, u64* out, Ctl c) {
+    PhaseGateUp<FMT> ph{in, out, c};
+    return with_lpr(P().rows_ffn, ph);
+}
+template <int FMT>
+__device__ __forceinline__ bool logits_phase(const u64* in, u64* cand, Ctl c) {
+    PhaseLogits<FMT> ph{in, cand, c};
+    return with_lpr(P().rows_out, ph);
+}
+
+
+// Copies `bytes` (a multiple of 4) from global memory into LDS, then syncs.
+__device__ __forceinline__ void copy_to_lds(unsigned char* dst, const void* src, int bytes) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < bytes / 4; i += kT) ((unsigned*)dst)[i] = *gptr((const unsigned*)src + i);
+    __syncthreads();
+}
+
+template <int FMT, int HD, int GM>
+__global__ __launch_bounds__(kT) void decode_step_kernel(DecodeParams kp) {
+    for (int i = threadIdx.x; i < (int)(sizeof(DecodeParams) / 4); i += kT)
+        ((unsigned*)lds_params)[i] = ((const unsigned*)&kp)[i];
+    __syncthreads();
+    const Shared sh = lds_of();
+    float* red = sh.red;
+    Ctl c;
+    c.tag = *(volatile unsigned*)kp.epoch;
+    c.abort_word = kp.abort_word;
+    c.status = kp.status;
+    c.timeout = kp.timeout_ticks;
+    const int pos = *(volatile int*)kp.pos;
+    const int token = *(volatile int*)kp.chain;
+    const int n_layers = kp.n_layers, layer_words = kp.layer_words;
+    const int off_part = kp.off_part, off_ctx = kp.off_ctx, off_xa = kp.off_xa, off_ffn = kp.off_ffn,
+              off_xf = kp.off_xf;
+
+    // optional timeline: thread 0 stamps the wall clock when its workgroup ends a phase
+    unsigned long long* trace = kp.trace;
+    int point = 0;
+    auto stamp = [&]() {
+        if (trace && threadIdx.x == 0) *gptr(trace + (int64_t)point * gridDim.x + blockIdx.x) = wall_clock64();
+        point++;
+    };
+    stamp();
+    const u64* xprev = nullptr;
+    for (int l = 0; l < n_layers; l++) {
+        if (l == kp.abort_at_layer && blockIdx.x == 0) {
+            // Failure-path tests only: the other workgroups then wait for rows this workgroup
+            // never publishes and leave through the abort word.
+            if (threadIdx.x == 0) raise_abort(c);
+            return;
+        }
+        copy_to_lds(lds_layer, kp.layers + l, (int)sizeof(DecLayer));
+        u64* X = kp.xbuf + (int64_t)l * layer_words;
+        if (!qkv_phase<FMT>(xprev, X, pos, token, c)) return;
+        stamp();
+        if (!attention_phase<HD, GM>(X, X + off_part, pos, c)) return;
+        stamp();
+        if (!merge_phase<HD>(X + off_part, X + off_ctx, pos, c)) return;
+        stamp();
+        if (!residual_phase<FMT>(0, X + off_ctx, X + off_xa, c)) return;
+        stamp();
+        if (!gate_up_phase<FMT>(X + off_xa, X + off_ffn, c)) return;
+        stamp();
+        if (!residual_phase<FMT>(1, X + off_ffn, X + off_xf, c)) return;
+        stamp();
+        xprev = X + off_xf;
+    }
+    u64* cand = kp.xbuf + kp.off_cand;
+    bool ok;
+    switch (kp.out.dtype) {
+    case DT_Q8_0: ok = logits_phase<DT_Q8_0>(xprev, cand, c); break;
+    case DT_Q4_0: ok = logits_phase<DT_Q4_0>(xprev, cand, c); break;
+    default: ok = logits_phase<DT_F16>(xprev, cand, c); break;
+    }
+    if (!ok) return;
+    stamp();
+    if (blockIdx.x != 0) return;
+    // P8: arg-max over the workgroups' candidates (Sampler.argmax, Sampler.swift:100-108:
+    // lowest index on ties; NaN never wins; an all-NaN row yields token 0).
+    const int nc = gridDim.x;
+    if (!wait_words(cand, 2 * nc, sh.scr, c)) return;
+    float best = -INFINITY;
+    int bi = INT_MAX;
+    for (int w = threadIdx.x; w < nc; w += kT) {
+        const float v = sh.scr[2 * w];
+        const int i = __float_as_int(sh.scr[2 * w + 1]);
+        if (v > best || (v == best && i < bi)) {
+            best = v;
+            bi = i;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v2 = __shfl_xor(best, o, 64);
+        const int i2 = __shfl_xor(bi, o, 64);
+        if (v2 > best || (v2 == best && i2 < bi)) {
+            best = v2;
+            bi = i2;
+        }
+    }
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) {
+        red[threadIdx.x >> 6] = best;
+        ((int*)red)[8 + (threadIdx.x >> 6)] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float bv = red[0];
+        int bx = ((int*)red)[8];
+        for (int w = 1; w < kWaves; w++)
+            if (red[w] > bv || (red[w] == bv && ((int*)red)[8 + w] < bx)) {
+                bv = red[w];
+                bx = ((int*)red)[8 + w];
+            }
+        const int tok = bx == INT_MAX ? 0 : bx;
+        *gptr(kp.chain) = tok;
+        if (kp.emitted) *(volatile int32_t*)(kp.emitted + pos) = tok;
+        *gptr(kp.pos) = pos + 1;
+        *gptr(kp.epoch) = c.tag + 1;
+        if (trace) *gptr(trace + (int64_t)point * gridDim.x) = wall_clock64();
+    }
+}
+
+}  // namespace
+
+// The kernel of this variant for group-size bucket gm.
+const void* DECODE_ENTRY(int gm) {
+    switch (gm) {
+    case 1: return (const void*)decode_step_kernel<DECODE_FMT, DECODE_HD, 1>;
+    case 2: return (const void*)decode_step_kernel<DECODE_FMT, DECODE_HD, 2>;
+    case 4: return (const void*)decode_step_kernel<DECODE_FMT, DECODE_HD, 4>;
+    default: return DECODE_HD == 64 ? (const void*)decode_step_kernel<DECODE_FMT, DECODE_HD, 8> : nullptr;
+    }
+}
+
+#else  // host side
+
+// Kernels of the (format, head dim) variants, one object each.
+const void* decode_kernel_q8_hd64(int gm);
+const void* decode_kernel_q8_hd128(int gm);
+const void* decode_kernel_q4_hd64(int gm);
+const void* decode_kernel_q4_hd128(int gm);
+const void* decode_kernel_f16_hd64(int gm);
+const void* decode_kernel_f16_hd128(int gm);
+
+namespace {
+const void* kernel_for(int fmt, int hd, int heads, int kv_heads) {
+    const int gm = group_bucket(heads / kv_heads);
+    if (hd == 64) {
+        switch (fmt) {
+        case DT_Q8_0: return decode_kernel_q8_hd64(gm);
+        case DT_Q4_0: return decode_kernel_q4_hd64(gm);
+        default: return decode_kernel_f16_hd64(gm);
+        }
+    }
+    switch (fmt) {
+    case DT_Q8_0: return decode_kernel_q8_hd128(gm);
+    case DT_Q4_0: return decode_kernel_q4_hd128(gm);
+    default: return decode_kernel_f16_hd128(gm);
+    }
+}
+}  // namespace
+
+bool decode_kernel_supported(int fmt, int hd, int heads, int kv_heads) {
+    // query heads per KV head: up to 8 at head_dim 64, up to 4 at 128
+    return (fmt == DT_Q8_0 || fmt == DT_Q4_0 || fmt == DT_F16) && (hd == 64 || hd == 128) && kv_heads > 0 &&
+           heads % kv_heads == 0 && heads / kv_heads <= (hd == 64 ? 8 : 4);
+}
+
+int decode_attention_max_splits(int capacity, int kv_heads, int target_items) {
+    int m = 1;
+    for (int len = 1; len <= capacity; len++) {
+        const int sl = split_len_for(len, kv_heads, target_items);
+        const int s = (len + sl - 1) / sl;
+        if (s > m) m = s;
+    }
+    return m;
+}
+
+size_t decode_lds_bytes(const DecodeParams& p, int grid) {
+    const int G = p.heads / p.kv_heads, GM = group_bucket(G), HD = p.hd;
+    size_t scr = 0;
+    auto need = [&](size_t floats) { scr = floats > scr ? floats : scr; };
+    need((size_t)p.rows_qkv);                                                    // QKV row buffer
+    need((size_t)GM * HD + 2 * HD + (size_t)GM * kMaxSplitLen + GM * 8 + (size_t)2 * kWaves * GM * HD);  // attention
+    need((size_t)p.max_splits * (HD + 2) + p.max_splits);                         // merge
+    need(16);                                                                     // logits arg-max
+    need((size_t)2 * grid);                                                       // candidates
+    return ((size_t)kRedFloats + p.hidden + p.stage + scr) * sizeof(float);
+}
+
+hipError_t decode_kernel_occupancy(int fmt, int hd, int heads, int kv_heads, size_t lds, int* blocks_per_cu) {
+    const void* f = kernel_for(fmt, hd, heads, kv_heads);
+    if (!f) return hipErrorInvalidValue;
+    hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, f, kT, lds);
+}
+
+hipError_t launch_decode_step(int fmt, const DecodeParams& p, int grid, size_t lds, hipStream_t st) {
+    const void* f = kernel_for(fmt, p.hd, p.heads, p.kv_heads);
+    if (!f) return hipErrorInvalidValue;
+    DecodeParams a = p;
+    void* args[] = {&a};
+    return hipLaunchCooperativeKernel(f, dim3(grid), dim3(kT), args, (unsigned)lds, st);
+}
+
+#endif  // DECODE_FMT

@@ -21,8 +21,12 @@
 // Epilogues: store, residual add, SwiGLU, or (QKV projection) RoPE on q and k
 // with k and v appended to the KV cache at position pos.
 #include "common.h"
+#include "gemv_chunks.h"
 
 namespace {
+
+using gemv::RowStream;
+using gemv::chunks_of;
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
@@ -34,105 +38,6 @@ struct GemvArgs {
     GemvInput in;
     GemvRope rope;
     float* out;
-};
-
-template <int FMT>
-__device__ __forceinline__ int chunks_of(int K) {
-    return FMT == DT_Q8_0 ? K >> 4 : FMT == DT_Q4_0 ? K >> 5 : K >> 3;
-}
-
-template <int FMT>
-__device__ __forceinline__ void load_chunk(const DevMatrix& m, int64_t row, int K, int c, int4& q, float& d) {
-    if (FMT == DT_Q8_0) {
-        q = *(const int4*)(m.q + row * K + 16 * c);
-        d = (float)m.s[row * (K >> 5) + (c >> 1)];
-    } else if (FMT == DT_Q4_0) {
-        q = *(const int4*)(m.q + row * (K >> 1) + 16 * c);
-        d = (float)m.s[row * (K >> 5) + c];
-    } else {
-        q = *(const int4*)(m.q + (row * K + 8 * c) * 2);
-        d = 1.f;
-    }
-}
-
-template <int FMT>
-__device__ __forceinline__ float chunk_dot(const int4& q, float d, int c, const float* xs) {
-    const int32_t* w = (const int32_t*)&q;
-    float s = 0.f;
-    if (FMT == DT_Q8_0) {
-        const float4* xv = (const float4*)(xs + 16 * c);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float4 x = xv[i];
-            int32_t v = w[i];
-            s += (float)(int8_t)(v) * x.x;
-            s += (float)(int8_t)(v >> 8) * x.y;
-            s += (float)(int8_t)(v >> 16) * x.z;
-            s += (float)(int8_t)(v >> 24) * x.w;
-        }
-        return d * s;
-    } else if (FMT == DT_Q4_0) {
-        const float4* lo = (const float4*)(xs + 32 * c);
-        const float4* hi = (const float4*)(xs + 32 * c + 16);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float4 xl = lo[i], xh = hi[i];
-            uint32_t v = (uint32_t)w[i];
-            s += (float)((int)(v & 15u) - 8) * xl.x;
-            s += (float)((int)((v >> 4) & 15u) - 8) * xh.x;
-            s += (float)((int)((v >> 8) & 15u) - 8) * xl.y;
-            s += (float)((int)((v >> 12) & 15u) - 8) * xh.y;
-            s += (float)((int)((v >> 16) & 15u) - 8) * xl.z;
-            s += (float)((int)((v >> 20) & 15u) - 8) * xh.z;
-            s += (float)((int)((v >> 24) & 15u) - 8) * xl.w;
-            s += (float)((int)(v >> 28) - 8) * xh.w;
-        }
-        return d * s;
-    } else {
-        const f16* h = (const f16*)&q;
-        const float4* xv = (const float4*)(xs + 8 * c);
-        float4 x0 = xv[0], x1 = xv[1];
-        s = (float)h[0] * x0.x + (float)h[1] * x0.y + (float)h[2] * x0.z + (float)h[3] * x0.w;
-        s += (float)h[4] * x1.x + (float)h[5] * x1.y + (float)h[6] * x1.z + (float)h[7] * x1.w;
-        return s;
-    }
-}
-
-// One row's dot product, with the first batch of loads already in registers.
-template <int FMT, int LPR>
-struct RowStream {
-    int4 q[kUnroll];
-    float d[kUnroll];
-    __device__ __forceinline__ void prefetch(const DevMatrix& m, int64_t row, int K, int li) {
-        const int nch = chunks_of<FMT>(K);
-#pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
-            const int c = li + u * LPR;
-            if (c < nch) load_chunk<FMT>(m, row, K, c, q[u], d[u]);
-        }
-    }
-    __device__ __forceinline__ float finish(const DevMatrix& m, int64_t row, int K, int li, const float* xs) {
-        const int nch = chunks_of<FMT>(K);
-        float acc = 0.f;
-#pragma unroll
-        for (int u = 0; u < kUnroll; u++) {
-            const int c = li + u * LPR;
-            if (c < nch) acc += chunk_dot<FMT>(q[u], d[u], c, xs);
-        }
-        for (int c0 = li + kUnroll * LPR; c0 < nch; c0 += kUnroll * LPR) {
-#pragma unroll
-            for (int u = 0; u < kUnroll; u++) {
-                const int c = c0 + u * LPR;
-                if (c < nch) load_chunk<FMT>(m, row, K, c, q[u], d[u]);
-            }
-#pragma unroll
-            for (int u = 0; u < kUnroll; u++) {
-                const int c = c0 + u * LPR;
-                if (c < nch) acc += chunk_dot<FMT>(q[u], d[u], c, xs);
-            }
-        }
-        return acc;
-    }
 };
 
 enum { IN_X = 0, IN_NORM = 1, IN_MERGE = 2 };
@@ -208,11 +113,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         acc = s0.finish(a.w, row, K, li, xs);
         if (MODE == GEMV_SWIGLU) acc2 = s1.finish(a.u, row, K, li, xs);
     }
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) {
-        acc += __shfl_xor(acc, o, 64);
-        if (MODE == GEMV_SWIGLU) acc2 += __shfl_xor(acc2, o, 64);
-    }
+    acc = lane_sum<LPR>(acc);
+    if (MODE == GEMV_SWIGLU) acc2 = lane_sum<LPR>(acc2);
     if (MODE == GEMV_QKV_ROPE) {
         // Rows come in aligned (even, odd) pairs inside a block: RoPE pairs.
         if (li == 0) rowbuf[local] = acc;

@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <atomic>
 #include <chrono>
 #include <cmath>
@@ -36,6 +37,12 @@ static int fail(int code, const std::string& msg) {
     do {                                                                                                    \
         hipError_t e_ = (expr);                                                                             \
         if (e_ != hipSuccess) return fail(AHIP_ERR_COMMAND_FAILED, std::string(what) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+#define LAUNCH(expr)                                                                                          \
+    do {                                                                                                      \
+        hipError_t e_ = (expr);                                                                               \
+        if (e_ != hipSuccess) return fail(AHIP_ERR_COMMAND_FAILED, std::string("kernel launch: ") + hipGetErrorString(e_)); \
     } while (0)
 
 extern "C" const char* ahip_last_error(void) { return g_err.c_str(); }
@@ -562,6 +569,19 @@ struct ahip_session {
     int dec_split_len = 0, dec_splits = 0;
     hipGraphExec_t greedy_graph = nullptr;
     bool graph_failed = false;
+    // persistent single-token decode (kernels_decode.hip): one cooperative launch per token
+    bool pdec = false;
+    int pdec_fmt = 0, pdec_grid = 0;
+    size_t pdec_lds = 0;
+    DecodeParams pdec_params;
+    DevBuf pdec_layers, pdec_xbuf, pdec_ctl;  // ctl: [0] epoch, [1] abort word
+    int64_t pdec_xbuf_bytes = 0;
+    int* pdec_status = nullptr;              // mapped host word, set by an aborting launch
+    uint64_t pdec_launches = 0;
+    int pdec_clock_khz = 0;                  // wall-clock rate of the trace stamps
+    DevBuf pdec_trace;                       // phase-end stamps of the last launch (profiling)
+    std::vector<unsigned long long> pdec_trace_host;
+    std::map<std::string, std::pair<double, int>> pdec_stages;
     int32_t* tokens_host = nullptr;
     int length = 0;
     std::atomic<int> busy{0};
@@ -582,6 +602,7 @@ struct ahip_session {
         if (logits_host) hipHostFree(logits_host);
         if (emitted_host) hipHostFree(emitted_host);
         if (tokens_host) hipHostFree(tokens_host);
+        if (pdec_status) hipHostFree(pdec_status);
         if (stream) hipStreamDestroy(stream);
     }
 
@@ -636,6 +657,230 @@ struct ahip_session {
     }
 };
 
+
+// ------------------------------------------------------------------ persistent decode setup
+
+static int env_int(const char* name, int dflt) {
+    const char* v = std::getenv(name);
+    if (!v || !*v) return dflt;
+    return std::atoi(v);
+}
+
+// Clears the exchange words and restarts the launch tag at 1 (session
+// creation, tag wrap-around, and recovery after an aborted launch).
+static int pdec_reset_words(ahip_session* s) {
+    HIP_OR(hipMemsetAsync(s->pdec_xbuf.p, 0, (size_t)s->pdec_xbuf_bytes, s->stream), "clear exchange words");
+    const unsigned init[2] = {1u, 0u};
+    HIP_OR(hipMemcpyAsync(s->pdec_ctl.p, init, sizeof init, hipMemcpyHostToDevice, s->stream), "reset decode tag");
+    HIP_OR(hipStreamSynchronize(s->stream), "reset decode tag");
+    *(volatile int*)s->pdec_status = 0;
+    s->pdec_launches = 0;
+    return AHIP_OK;
+}
+
+// Chooses the persistent decode kernel when the model and device allow it:
+// f16 KV cache, one weight format for every layer matrix, head_dim 64/128,
+// cooperative launch support and enough LDS.  ALPACA_HIP_PERSISTENT_DECODE=0
+// turns it off; ALPACA_HIP_DECODE_WGS sets the workgroup count (default: one
+// per CU); ALPACA_HIP_DECODE_ITEMS the attention items aimed for;
+// ALPACA_HIP_DECODE_TIMEOUT_US the bound on each wait inside the kernel;
+// ALPACA_HIP_DECODE_ABORT_LAYER (failure-path tests) makes every launch abort
+// at that layer.
+static int setup_persistent_decode(ahip_session* s) {
+    ahip_model* m = s->m;
+    const ahip_llama_config& c = m->c;
+    if (!env_int("ALPACA_HIP_PERSISTENT_DECODE", 1) || !s->kv_f16) return AHIP_OK;
+    const int fmt = m->layers[0]->qkv.m.dtype;
+    for (auto& L : m->layers)
+        for (const OwnedMatrix* om : {&L->qkv, &L->wo, &L->gate, &L->up, &L->down})
+            if (om->m.dtype != fmt) return AHIP_OK;
+    if (!decode_kernel_supported(fmt, c.head_dim, c.head_count, c.kv_head_count)) return AHIP_OK;
+    int coop = 0, cus = 0, clock_khz = 0;
+    hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, m->device);
+    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->device);
+    hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeWallClockRate, m->device);
+    if (!coop || cus <= 0 || clock_khz <= 0) return AHIP_OK;
+
+    const int H = c.hidden_size, QW = c.head_count * c.head_dim, KW = c.kv_head_count * c.head_dim,
+              F = c.feed_forward_size, V = c.vocab_size, hd = c.head_dim;
+    DecodeParams p;
+    p.n_layers = c.layer_count;
+    p.hidden = H;
+    p.heads = c.head_count;
+    p.kv_heads = c.kv_head_count;
+    p.hd = hd;
+    p.ffn = F;
+    p.vocab = V;
+    p.capacity = s->capacity;
+    p.eps = c.rms_norm_eps;
+    p.rope = m->rope.as<float2>();
+    p.embed = m->embed.m;
+    p.out = m->out_matrix();
+    p.out_norm = m->output_norm.as<float>();
+    p.target_items = std::max(1, env_int("ALPACA_HIP_DECODE_ITEMS", 64));
+    p.max_splits = decode_attention_max_splits(s->capacity, c.kv_head_count, p.target_items);
+    p.stage = std::max(H, std::max(QW, F));
+    p.off_part = QW + 2 * KW;
+    p.off_ctx = p.off_part + c.head_count * p.max_splits * (hd + 2);
+    p.off_xa = p.off_ctx + QW;
+    p.off_ffn = p.off_xa + H;
+    p.off_xf = p.off_ffn + F;
+    p.layer_words = p.off_xf + H;
+    p.off_cand = c.layer_count * p.layer_words;
+
+    int grid = env_int("ALPACA_HIP_DECODE_WGS", cus);
+    grid = std::max(1, std::min(grid, 4096));
+    auto even_share = [&](int rows) { int r = (rows + grid - 1) / grid; return r + (r & 1); };
+    p.rows_qkv = even_share(QW + 2 * KW);
+    p.rows_wo = even_share(H);
+    p.rows_ffn = even_share(F);
+    p.rows_down = even_share(H);
+    p.rows_out = even_share(V);
+    size_t lds = decode_lds_bytes(p, grid);
+    int max_lds = 0;
+    hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, m->device);
+    if (lds > (size_t)max_lds) return AHIP_OK;
+    int per_cu = 0;
+    if (decode_kernel_occupancy(fmt, hd, c.head_count, c.kv_head_count, lds, &per_cu) != hipSuccess || per_cu < 1) {
+        hipGetLastError();
+        return AHIP_OK;
+    }
+    grid = std::min(grid, per_cu * cus);
+    // the row shares depend on the grid; recompute if the grid shrank
+    p.rows_qkv = even_share(QW + 2 * KW);
+    p.rows_wo = even_share(H);
+    p.rows_ffn = even_share(F);
+    p.rows_down = even_share(H);
+    p.rows_out = even_share(V);
+    lds = decode_lds_bytes(p, grid);
+
+    std::vector<DecLayer> table(c.layer_count);
+    for (int l = 0; l < c.layer_count; l++) {
+        const ahip_model::Layer& L = *m->layers[l];
+        table[l].qkv = L.qkv.m;
+        table[l].wo = L.wo.m;
+        table[l].gate = L.gate.m;
+        table[l].up = L.up.m;
+        table[l].down = L.down.m;
+        table[l].attn_norm = L.attn_norm.as<float>();
+        table[l].ffn_norm = L.ffn_norm.as<float>();
+        table[l].kc = s->kc[l]->p;
+        table[l].vc = s->vc[l]->p;
+    }
+    if (int rc = s->pdec_layers.alloc(table.size() * sizeof(DecLayer))) return rc;
+    HIP_OR(hipMemcpy(s->pdec_layers.p, table.data(), table.size() * sizeof(DecLayer), hipMemcpyHostToDevice),
+           "upload layer table");
+    s->pdec_xbuf_bytes = ((int64_t)p.off_cand + 2 * grid) * 8;
+    if (int rc = s->pdec_xbuf.alloc((size_t)s->pdec_xbuf_bytes)) return rc;
+    if (int rc = s->pdec_ctl.alloc(256)) return rc;
+    if (hipHostMalloc((void**)&s->pdec_status, 64, hipHostMallocMapped) != hipSuccess)
+        return fail(AHIP_ERR_ALLOC, "pinned host allocation failed");
+    int* status_dev = nullptr;
+    HIP_OR(hipHostGetDevicePointer((void**)&status_dev, s->pdec_status, 0), "hipHostGetDevicePointer");
+    p.layers = s->pdec_layers.as<DecLayer>();
+    p.chain = s->chain.as<int32_t>();
+    p.pos = s->dpos.as<int>();
+    p.epoch = s->pdec_ctl.as<unsigned>();
+    p.abort_word = s->pdec_ctl.as<unsigned>() + 1;
+    p.status = status_dev;
+    p.xbuf = s->pdec_xbuf.as<unsigned long long>();
+    p.emitted = nullptr;
+    p.logits = nullptr;
+    const long long timeout_us = env_int("ALPACA_HIP_DECODE_TIMEOUT_US", 2000000);
+    p.timeout_ticks = std::max(1LL, timeout_us * (long long)clock_khz / 1000);
+    p.abort_at_layer = env_int("ALPACA_HIP_DECODE_ABORT_LAYER", -1);  // failure-path tests
+    s->pdec_params = p;
+    s->pdec_clock_khz = clock_khz;
+    s->pdec_fmt = fmt;
+    s->pdec_grid = grid;
+    s->pdec_lds = lds;
+    if (int rc = pdec_reset_words(s)) return rc;
+    s->pdec = true;
+    return AHIP_OK;
+}
+
+// Enqueues one persistent decode launch: the token in `chain` at position
+// *dpos; the arg-max goes to `chain` (and emitted[pos] when `emitted`), the
+// logits to the session's logits buffer when `logits`.
+static int pdec_launch(ahip_session* s, bool logits, bool emitted) {
+    if (s->pdec_launches >= (1ull << 31)) {
+        HIP_OR(hipStreamSynchronize(s->stream), "decode tag wrap");
+        if (int rc = pdec_reset_words(s)) return rc;
+    }
+    DecodeParams p = s->pdec_params;
+    p.logits = logits ? s->logits.as<float>() : nullptr;
+    p.emitted = emitted ? s->emitted_mapped : nullptr;
+    if (s->profiling) {
+        const size_t n = (size_t)(decode_trace_points(p.n_layers) + kDecodeAttnSubPoints) * s->pdec_grid;
+        if (!s->pdec_trace.p)
+            if (int rc = s->pdec_trace.alloc(n * 8)) return rc;
+        HIP_OR(hipMemsetAsync(s->pdec_trace.p, 0, n * 8, s->stream), "clear trace");
+        p.trace = s->pdec_trace.as<unsigned long long>();
+    }
+    LAUNCH(launch_decode_step(s->pdec_fmt, p, s->pdec_grid, s->pdec_lds, s->stream));
+    s->pdec_launches++;
+    return AHIP_OK;
+}
+
+// Stage labels of the persistent kernel's phases (the multi-kernel path's labels).
+static const char* const kPhaseLabels[6] = {"qkv (fused norm)", "attention", "attention merge",
+                                            "attn out projection (+residual)", "ffn gate+up+silu (fused norm)",
+                                            "ffn down (+residual)"};
+
+// Profiling: after a launch has completed, turns its phase-end stamps into
+// per-stage times on the critical path (the last workgroup to end a phase ends
+// it) and adds them to the call's stages.
+static int pdec_collect_trace(ahip_session* s) {
+    const int L = s->m->c.layer_count, P = decode_trace_points(L), G = s->pdec_grid;
+    const size_t total = (size_t)(P + kDecodeAttnSubPoints) * G;
+    s->pdec_trace_host.resize(total);
+    HIP_OR(hipMemcpyAsync(s->pdec_trace_host.data(), s->pdec_trace.p, total * 8, hipMemcpyDeviceToHost,
+                          s->stream), "trace download");
+    HIP_OR(hipStreamSynchronize(s->stream), "trace download");
+    const unsigned long long* t = s->pdec_trace_host.data();
+    unsigned long long prev = ~0ull;
+    for (int g = 0; g < G; g++)
+        if (t[g]) prev = std::min(prev, t[g]);
+    const double tick = 1.0 / (1000.0 * s->pdec_clock_khz);
+    for (int k = 1; k < P; k++) {
+        unsigned long long end = 0;
+        const int n = k == P - 1 ? 1 : G;  // the arg-max runs in workgroup 0 only
+        for (int g = 0; g < n; g++) end = std::max(end, t[(size_t)k * G + g]);
+        const char* label = k == P - 1 ? "sample" : k == P - 2 ? "final norm + logits" : kPhaseLabels[(k - 1) % 6];
+        auto& st = s->pdec_stages[label];
+        st.first += end > prev ? (double)(end - prev) * tick : 0.0;
+        st.second += 1;
+        prev = std::max(prev, end);
+    }
+    return AHIP_OK;
+}
+
+// Writes the accumulated persistent-kernel stages into the session profile.
+static void pdec_publish_stages(ahip_session* s) {
+    s->profile.clear();
+    auto add = [&](const char* label) {
+        auto it = s->pdec_stages.find(label);
+        if (it == s->pdec_stages.end()) return;
+        ahip_stage st{};
+        std::snprintf(st.label, sizeof st.label, "%s", label);
+        st.seconds = it->second.first;
+        st.dispatches = it->second.second;
+        s->profile.push_back(st);
+    };
+    for (const char* l : kPhaseLabels) add(l);
+    add("final norm + logits");
+    add("sample");
+    s->pdec_stages.clear();
+}
+
+// After the launches of a call have completed: reports an aborted launch (a
+// bounded wait inside the kernel expired) and leaves the session usable.
+static int pdec_check(ahip_session* s) {
+    if (!s->pdec || *(volatile int*)s->pdec_status == 0) return AHIP_OK;
+    pdec_reset_words(s);
+    return fail(AHIP_ERR_COMMAND_FAILED, "persistent decode launch aborted: a workgroup timed out or aborted");
+}
+
 extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, int kv_precision, int gemm_precision,
                                    ahip_session** out) {
     if (!m || !out) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
@@ -677,6 +922,7 @@ extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, i
         s->dec_split_len = attention_decode_split_len(capacity);
         s->dec_splits = (capacity + s->dec_split_len - 1) / s->dec_split_len;
     }
+    if (int rc = setup_persistent_decode(s.get())) return rc;
     HIP_OR(hipEventCreate(&s->ev_begin), "hipEventCreate");
     HIP_OR(hipEventCreate(&s->ev_end), "hipEventCreate");
     *out = s.release();
@@ -703,11 +949,6 @@ struct BusyGuard {
     }
 };
 
-#define LAUNCH(expr)                                                                                          \
-    do {                                                                                                      \
-        hipError_t e_ = (expr);                                                                               \
-        if (e_ != hipSuccess) return fail(AHIP_ERR_COMMAND_FAILED, std::string("kernel launch: ") + hipGetErrorString(e_)); \
-    } while (0)
 
 // One decoder layer for a single token (the fused decode path,
 // MetalLlamaModel.swift:344-356): 5 launches -- QKV GEMV with RMSNorm prologue
@@ -872,12 +1113,25 @@ extern "C" int ahip_session_forward(ahip_session* s, const int32_t* tokens, int 
     const auto t0 = std::chrono::steady_clock::now();
     std::memcpy(s->tokens_host, tokens, (size_t)n * 4);
     HIP_OR(hipEventRecord(s->ev_begin, s->stream), "hipEventRecord");
-    HIP_OR(hipMemcpyAsync(s->tokens.p, s->tokens_host, (size_t)n * 4, hipMemcpyHostToDevice, s->stream), "token upload");
-    for (int c0 = 0; c0 < n; c0 += s->max_batch) {
-        const int cn = std::min(s->max_batch, n - c0);
-        if (int rc = encode_chunk(s, s->tokens.as<int32_t>() + c0, cn, s->length + c0, c0 + cn == n)) {
+    const bool persistent = n == 1 && s->pdec;
+    if (persistent) {
+        // one cooperative launch: token in `chain`, position in `dpos`
+        s->tokens_host[1] = s->length;
+        HIP_OR(hipMemcpyAsync(s->chain.p, s->tokens_host, 4, hipMemcpyHostToDevice, s->stream), "token upload");
+        HIP_OR(hipMemcpyAsync(s->dpos.p, s->tokens_host + 1, 4, hipMemcpyHostToDevice, s->stream), "position upload");
+        if (int rc = pdec_launch(s, true, false)) {
             hipStreamSynchronize(s->stream);
             return rc;
+        }
+    } else {
+        HIP_OR(hipMemcpyAsync(s->tokens.p, s->tokens_host, (size_t)n * 4, hipMemcpyHostToDevice, s->stream),
+               "token upload");
+        for (int c0 = 0; c0 < n; c0 += s->max_batch) {
+            const int cn = std::min(s->max_batch, n - c0);
+            if (int rc = encode_chunk(s, s->tokens.as<int32_t>() + c0, cn, s->length + c0, c0 + cn == n)) {
+                hipStreamSynchronize(s->stream);
+                return rc;
+            }
         }
     }
     s->stage_end();
@@ -886,10 +1140,17 @@ extern "C" int ahip_session_forward(ahip_session* s, const int32_t* tokens, int 
     HIP_OR(hipEventRecord(s->ev_end, s->stream), "hipEventRecord");
     s->last_encode = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
     HIP_OR(hipStreamSynchronize(s->stream), "forward");
+    if (persistent)
+        if (int rc = pdec_check(s)) return rc;
     float ms = 0;
     hipEventElapsedTime(&ms, s->ev_begin, s->ev_end);
     s->last_gpu = ms * 1e-3;
-    s->collect_profile();
+    if (persistent && s->profiling) {
+        if (int rc = pdec_collect_trace(s)) return rc;
+        pdec_publish_stages(s);
+    } else {
+        s->collect_profile();
+    }
     s->length += n;
     *logits = s->logits_host;
     return AHIP_OK;
@@ -952,11 +1213,13 @@ extern "C" int ahip_session_decode_greedy(ahip_session* s, int32_t start, int ma
     const int budget = std::min(max_steps, s->capacity - s->length);
     if (budget <= 0) return AHIP_OK;
     depth = std::max(1, std::min(depth, 8));
+    if (s->pdec && s->profiling) depth = 1;  // one launch in flight: each trace is read before the next launch
     HIP_OR(hipSetDevice(s->m->device), "hipSetDevice");
     hipStream_t st = s->stream;
     // Eager launches when profiling (stage events between kernels) or when
     // the split-K attention kernel does not apply; otherwise graph replays.
-    const bool use_graph = !s->profiling && capture_greedy_graph(s);
+    const bool use_pdec = s->pdec;
+    const bool use_graph = !use_pdec && !s->profiling && capture_greedy_graph(s);
     s->begin_call();
     s->tokens_host[0] = start;
     s->tokens_host[1] = s->length;
@@ -967,7 +1230,9 @@ extern "C" int ahip_session_decode_greedy(ahip_session* s, int32_t start, int ma
     int submitted = 0, fed = 0, rc = AHIP_OK;
     auto submit = [&]() -> int {
         const int i = submitted;
-        if (use_graph) {
+        if (use_pdec) {
+            if (int r = pdec_launch(s, false, true)) return r;
+        } else if (use_graph) {
             HIP_OR(hipGraphLaunch(s->greedy_graph, st), "hipGraphLaunch");
         } else if (s->dec_split) {
             if (int r = encode_greedy_step(s)) return r;
@@ -990,6 +1255,12 @@ extern "C" int ahip_session_decode_greedy(ahip_session* s, int32_t start, int ma
             rc = fail(AHIP_ERR_COMMAND_FAILED, std::string("decode step: ") + hipGetErrorString(e));
             break;
         }
+        if (use_pdec && *(volatile int*)s->pdec_status) {
+            rc = AHIP_ERR_COMMAND_FAILED;  // message set by pdec_check after the drain
+            break;
+        }
+        if (use_pdec && s->profiling)
+            if ((rc = pdec_collect_trace(s)) != AHIP_OK) break;
         const int32_t token = ((volatile int32_t*)s->emitted_host)[s->length + fed];
         fed++;
         if (!emit(user, token)) break;
@@ -999,10 +1270,13 @@ extern "C" int ahip_session_decode_greedy(ahip_session* s, int32_t start, int ma
     HIP_OR(hipEventRecord(s->ev_end, st), "hipEventRecord");
     hipError_t e = hipStreamSynchronize(st);
     if (e != hipSuccess && rc == AHIP_OK) rc = fail(AHIP_ERR_COMMAND_FAILED, std::string("drain: ") + hipGetErrorString(e));
+    if (use_pdec && e == hipSuccess)
+        if (int prc = pdec_check(s)) rc = prc;
     float ms = 0;
     hipEventElapsedTime(&ms, s->ev_begin, s->ev_end);
     s->last_gpu = ms * 1e-3;
-    s->collect_profile();
+    if (use_pdec && s->profiling) pdec_publish_stages(s);
+    else s->collect_profile();
     s->length += fed;  // only tokens whose input was consumed (MetalLlamaModel.swift:265-267)
     *fed_out = fed;
     return rc;
@@ -1040,6 +1314,18 @@ extern "C" int ahip_session_set_profiling(ahip_session* s, int enabled) {
     s->profiling = enabled != 0;
     return AHIP_OK;
 }
+extern "C" int ahip_session_decode_timeline(const ahip_session* s, uint64_t* out, int64_t cap, int64_t* count,
+                                            int* workgroups, double* tick_seconds) {
+    if (!s || !count || !workgroups || !tick_seconds || (cap > 0 && !out))
+        return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
+    const int64_t n = (int64_t)s->pdec_trace_host.size();
+    for (int64_t i = 0; i < n && i < cap; i++) out[i] = s->pdec_trace_host[(size_t)i];
+    *count = n;
+    *workgroups = s->pdec ? s->pdec_grid : 0;
+    *tick_seconds = s->pdec_clock_khz > 0 ? 1.0 / (1000.0 * s->pdec_clock_khz) : 0.0;
+    return AHIP_OK;
+}
+
 extern "C" int ahip_session_profile(const ahip_session* s, ahip_stage* out, int cap, int* count) {
     if (!s || !count || (cap > 0 && !out)) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
     const int n = (int)s->profile.size();

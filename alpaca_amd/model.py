@@ -226,6 +226,18 @@ class HIPLlamaSession:
         L.check(L.lib().ahip_session_profile(self.handle, arr, n.value, C.byref(n)))
         return {arr[k].label.decode(): StageTime(arr[k].seconds, arr[k].dispatches) for k in range(n.value)}
 
+    @property
+    def decode_timeline(self):
+        """Raw stamps of the last profiled single-token persistent launch:
+        (array [points, workgroups] of wall-clock ticks, seconds per tick)."""
+        n, wg, tick = C.c_int64(), C.c_int(), C.c_double()
+        L.check(L.lib().ahip_session_decode_timeline(self.handle, None, 0, C.byref(n), C.byref(wg), C.byref(tick)))
+        buf = (C.c_uint64 * max(n.value, 1))()
+        L.check(L.lib().ahip_session_decode_timeline(self.handle, buf, n.value, C.byref(n), C.byref(wg),
+                                                     C.byref(tick)))
+        arr = np.frombuffer(buf, dtype=np.uint64, count=n.value).copy()
+        return (arr.reshape(-1, wg.value) if wg.value else arr), tick.value
+
     def close(self) -> None:
         if getattr(self, "handle", None):
             L.lib().ahip_session_destroy(self.handle)

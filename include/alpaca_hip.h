@@ -164,6 +164,15 @@ int ahip_session_last_encode_seconds(const ahip_session* s, double* seconds);
  * every stage is bracketed by HIP events on the session stream. */
 int ahip_session_set_profiling(ahip_session* s, int enabled);
 int ahip_session_profile(const ahip_session* s, ahip_stage* out, int capacity, int* count);
+/* The wall-clock timeline behind the stages of the last profiled single-token
+ * launch of the persistent decode kernel (the GPU timestamps EncoderProvider
+ * takes at stage boundaries, MetalLlamaModel.swift:431-447): `count` stamps,
+ * laid out [point][workgroup] with `workgroups` columns.  Points: launch start,
+ * then six per layer (qkv, attention, merge, wo, gate/up, down), logits, and the
+ * arg-max (workgroup 0 only); then eight stamps inside the attention item of
+ * the last layer.  A zero stamp was not written.  Copies min(count, capacity). */
+int ahip_session_decode_timeline(const ahip_session* s, uint64_t* out, int64_t capacity, int64_t* count,
+                                 int* workgroups, double* tick_seconds);
 
 /* ------------------------------------------------------------ op-level API
  * MetalOps, Sources/AlpacaMetal/Backend/MetalOps.swift:11-219: tensor in /

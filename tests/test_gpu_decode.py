@@ -1,0 +1,166 @@
+"""The persistent single-token decode kernel (one cooperative launch per token).
+
+Sessions pick it for single-token forward calls and the greedy chain when the
+model allows it; ALPACA_HIP_PERSISTENT_DECODE=0 (read at session creation)
+selects the multi-kernel path instead.  These tests hold the persistent path
+to the multi-kernel path and to the CPU oracle
+(LlamaCPUModel.forward, LlamaCPUModel.swift:24-61) and check the greedy chain
+semantics of MetalLlamaSession.decodeGreedy (MetalLlamaModel.swift:228-270).
+
+Tolerances: against the oracle, the BASELINE bound (2e-3 absolute + 1e-3
+relative), after an exact-mode prefill (float32 GEMMs) so that the bound
+measures the decode step; between the two GPU paths, which compute the same float32
+products in a different summation order, 1e-4 of the logit peak.
+"""
+import os
+from contextlib import contextmanager
+from dataclasses import replace
+
+import numpy as np
+import pytest
+
+import oracle.oracle as orc
+from alpaca_amd import synth
+from alpaca_amd._lib import HIPError
+from alpaca_amd.model import HIPLlamaModel
+from alpaca_amd.tensor import F16, Q4_0
+from tests.helpers import assert_close, metrics
+from tests.test_gpu_model import built, oracle_cfg, oracle_model
+
+pytestmark = pytest.mark.gpu
+
+
+@contextmanager
+def env(**kv):
+    old = {k: os.environ.get(k) for k in kv}
+    os.environ.update({k: str(v) for k, v in kv.items()})
+    try:
+        yield
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+SPECS = [synth.TINY, synth.with_dtype(synth.TINY, Q4_0), synth.with_dtype(synth.TINY, F16),
+         replace(synth.TINY, config=replace(synth.TINY.config, head_count=8, kv_head_count=2), name="tiny-g4"),
+         replace(synth.TINY, config=replace(synth.TINY.config, head_count=4, kv_head_count=4), name="tiny-mha")]
+
+
+@pytest.mark.parametrize("spec", SPECS, ids=lambda s: s.name)
+def test_persistent_decode_matches_multi_kernel_and_oracle(hip_ctx, spec):
+    c = spec.config
+    w = built(spec)
+    model = HIPLlamaModel(hip_ctx, c, w)
+    om = oracle_model(c, w)
+    prompt = synth.prompt_tokens(spec, 37)
+    # exact prefill (float32 GEMMs) so the oracle comparison isolates the decode step
+    with env(ALPACA_HIP_PERSISTENT_DECODE=0):
+        ref = model.make_session(capacity=160, gemm_precision="exact")
+    fast = model.make_session(capacity=160, gemm_precision="exact")
+    okv = orc.OracleKV(oracle_cfg(c), 160, rounds_f16=True)
+    e = orc.forward(om, okv, prompt)
+    ref.forward(prompt)
+    fast.forward(prompt)
+    tok = orc.argmax(e)
+    for step in range(12):
+        g_ref = ref.decode(tok)
+        g = fast.decode(tok)
+        e = orc.forward(om, okv, [tok])
+        m = metrics(g, g_ref)
+        print(f"[metrics] {spec.name} step {step} persistent vs multi-kernel: {m}")
+        assert m["max_rel_peak"] <= 1e-4, step
+        assert_close(g, e, 2e-3, 1e-3, f"{spec.name} persistent decode step {step}")
+        assert int(np.argmax(g)) == int(np.argmax(e))
+        tok = orc.argmax(e)
+    assert fast.length == ref.length == 37 + 12
+
+
+def test_persistent_decode_across_attention_split_boundaries(hip_ctx):
+    """Contexts on both sides of every split length (64..256 positions per
+    split) and of the capacity: the split-K partials and their merge must
+    cover exactly positions 0..pos."""
+    spec = synth.TINY
+    c = spec.config
+    w = built(spec)
+    model = HIPLlamaModel(hip_ctx, c, w)
+    om = oracle_model(c, w)
+    cap = c.context_length  # 1024
+    prompt = synth.prompt_tokens(spec, cap)
+    s = model.make_session(capacity=cap, max_batch=512, gemm_precision="exact")
+    okv = orc.OracleKV(oracle_cfg(c), cap, rounds_f16=True)
+    for p in (1, 63, 64, 65, 127, 128, 129, 255, 256, 257, 511, 640, 1023, cap):
+        s.reset()
+        okv.reset()
+        if p > 1:
+            s.forward(prompt[: p - 1])
+            orc.forward(om, okv, prompt[: p - 1])
+        g = s.decode(int(prompt[p - 1]))
+        e = orc.forward(om, okv, [int(prompt[p - 1])])
+        assert_close(g, e, 2e-3, 1e-3, f"decode at context {p}")
+        assert s.length == p
+
+
+def test_persistent_greedy_chain_matches_stepwise_decode(hip_ctx):
+    """decodeGreedy through the persistent kernel emits the tokens that
+    step-by-step decode + host arg-max produce, stops early when emit returns
+    False (length = tokens fed) and stops at capacity."""
+    spec = synth.TINY
+    c = spec.config
+    model = HIPLlamaModel(hip_ctx, c, built(spec))
+    prompt = synth.prompt_tokens(spec, 30)
+    a = model.make_session(capacity=100)
+    first = int(np.argmax(a.forward(prompt)))
+    got = []
+    fed = a.decode_greedy(first, 50, lambda t: got.append(t) or True, depth=4)
+    assert fed == 50 and a.length == 80
+    b = model.make_session(capacity=100)
+    tok = int(np.argmax(b.forward(prompt)))
+    want = []
+    for _ in range(50):
+        tok = int(np.argmax(b.decode(tok)))
+        want.append(tok)
+    assert got == want
+    # early stop after 5 tokens: 5 fed
+    cs = model.make_session(capacity=100)
+    cs.forward(prompt)
+    seen = []
+    fed = cs.decode_greedy(first, 50, lambda t: seen.append(t) or len(seen) < 5, depth=3)
+    assert fed == 5 and cs.length == 35 and seen == want[:5]
+    # capacity: 100 - 30 = 70 steps at most
+    d = model.make_session(capacity=100)
+    d.forward(prompt)
+    fed = d.decode_greedy(first, 500, lambda t: True, depth=2)
+    assert fed == 70 and d.length == 100
+
+
+def test_persistent_decode_abort_is_reported_and_session_recovers(hip_ctx):
+    """A launch that aborts (a wait timed out, or a workgroup gave up) makes every
+    workgroup leave through the shared abort word.  Forced from the host
+    (ALPACA_HIP_DECODE_ABORT_LAYER: workgroup 0 raises the abort at layer 1 and
+    stops, so the others wait for rows it never publishes), the call fails
+    without advancing the session, the greedy chain reports it too, and the
+    exchange words are reset so that later launches succeed."""
+    spec = synth.TINY
+    c = spec.config
+    model = HIPLlamaModel(hip_ctx, c, built(spec))
+    prompt = synth.prompt_tokens(spec, 20)
+    with env(ALPACA_HIP_DECODE_ABORT_LAYER=1):
+        s = model.make_session(capacity=64)
+    s.forward(prompt)
+    for _ in range(2):
+        with pytest.raises(HIPError, match="aborted"):
+            s.decode(7)
+        assert s.length == 20
+    with pytest.raises(HIPError, match="aborted"):
+        s.decode_greedy(7, 5, lambda t: True)
+    assert s.length == 20
+    ok = model.make_session(capacity=64)
+    ok.forward(prompt)
+    with env(ALPACA_HIP_PERSISTENT_DECODE=0):
+        ref = model.make_session(capacity=64)
+    ref.forward(prompt)
+    m = metrics(ok.decode(7), ref.decode(7))
+    assert m["max_rel_peak"] <= 1e-4
