@@ -214,7 +214,11 @@ bool decode_kernel_supported(int fmt, int hd, int heads, int kv_heads);
 int decode_attention_max_splits(int capacity, int kv_heads, int target_items);
 size_t decode_lds_bytes(const DecodeParams& p, int grid);
 hipError_t decode_kernel_occupancy(int fmt, int hd, int heads, int kv_heads, size_t lds, int* blocks_per_cu);
-hipError_t launch_decode_step(int fmt, const DecodeParams& p, int grid, size_t lds, hipStream_t st);
+// cooperative = 0 launches the same grid as an ordinary kernel (for profilers
+// that cannot follow cooperative launches); residency is then not guaranteed
+// by the runtime, and a workgroup that never starts makes the others' bounded
+// waits expire, so the launch still ends, with an error.
+hipError_t launch_decode_step(int fmt, const DecodeParams& p, int grid, size_t lds, int cooperative, hipStream_t st);
 
 // attention (kernels_attention.hip).  Cache layout [kv_heads][capacity][hd].
 // q rows are [tokens][heads][hd] with row stride ldq (elements).

@@ -200,13 +200,35 @@ __device__ __forceinline__ float matrix_elem(const DevMatrix& m, int64_t r, int 
     return d * (float)((int)(j < 16 ? (b & 15) : (b >> 4)) - 8);
 }
 
+// The gain vector of an RMSNorm, loaded before the wait that precedes the
+// norm: the first kNormRegs*256 entries in registers, any rest from memory.
+constexpr int kNormRegs = 8;
+struct NormGain {
+    const float* w;
+    float r[kNormRegs];
+    __device__ __forceinline__ void load(const float* gain, int n) {
+        w = gain;
+#pragma unroll
+        for (int k = 0; k < kNormRegs; k++) {
+            const int i = threadIdx.x + k * kT;
+            r[k] = *gptr(gain + (i < n ? i : 0));
+        }
+    }
+};
+
 // x (LDS, n floats) -> out = (x * (1/sqrt(mean(x^2) + eps))) * w  (CPUOps.rmsNorm, CPUOps.swift:144-159).
-__device__ __forceinline__ void rmsnorm_lds(const float* x, const float* w, int n, float eps, float* out, float* red) {
+__device__ __forceinline__ void rmsnorm_lds(const float* x, const NormGain& g, int n, float eps, float* out,
+                                            float* red) {
     float ss = 0.f;
     for (int i = threadIdx.x; i < n; i += kT) ss += x[i] * x[i];
     ss = block_sum4(ss, red);
     const float scale = 1.0f / sqrtf(ss / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += kT) out[i] = (x[i] * scale) * *gptr(w + i);
+#pragma unroll
+    for (int k = 0; k < kNormRegs; k++) {
+        const int i = threadIdx.x + k * kT;
+        if (i < n) out[i] = (x[i] * scale) * g.r[k];
+    }
+    for (int i = threadIdx.x + kNormRegs * kT; i < n; i += kT) out[i] = (x[i] * scale) * *gptr(g.w + i);
     __syncthreads();
 }
 
@@ -249,6 +271,34 @@ struct Rows {
         if (TWO) v1 = lane_sum<LPR>(v1);
         if (r < r1 && li == 0) epi(r, v0, v1);
     }
+    // Pairs (even row, odd row) for LPR <= 32: the two rows of a pair are
+    // neighbouring lane groups of one wave, so their sums meet with one
+    // shuffle; epi2(even_row, even_sum, odd_sum) runs on the even row's first lane.
+    template <typename Epi2>
+    __device__ __forceinline__ void pass_pairs(RowStream<FMT, LPR>& s0, const DevMatrix& w0, int base, int r1,
+                                               const float* xs, Epi2& epi2) {
+        static_assert(LPR <= 32, "a row pair must sit in one wave");
+        const int r = base + local;
+        float v = 0.f;
+        if (r < r1) v = s0.finish(w0, r, w0.cols, li, xs);
+        v = lane_sum<LPR>(v);
+        const float partner = __shfl_xor(v, LPR, 64);
+        if (r < r1 && li == 0 && (local & 1) == 0) epi2(r, v, partner);
+    }
+    template <typename Epi2>
+    __device__ __forceinline__ void run_pairs(const DevMatrix& w0, int r0, int r1, const float* xs, Epi2 epi2) {
+        for (int base = r0; base < r1;) {
+            int nxt = base + RPB;
+            if (nxt < r1) load(b0, b1, w0, w0, nxt, r1);
+            pass_pairs(a0, w0, base, r1, xs, epi2);
+            base = nxt;
+            if (base >= r1) break;
+            nxt = base + RPB;
+            if (nxt < r1) load(a0, a1, w0, w0, nxt, r1);
+            pass_pairs(b0, w0, base, r1, xs, epi2);
+            base = nxt;
+        }
+    }
     template <typename Epi>
     __device__ __forceinline__ void run(const DevMatrix& w0, const DevMatrix& w1, int r0, int r1, const float* xs,
                                         Epi epi) {
@@ -283,24 +333,34 @@ __device__ __forceinline__ bool with_lpr(int rows, F& f) {
 // ------------------------------------------------------------------ phases
 
 // P1: QKV rows with RMSNorm prologue and RoPE epilogue.  On return xres holds
-// the layer's input row (kept for the Wo residual).
+// the layer's input row (kept for the Wo residual).  At most 32 lanes per
+// row, so each RoPE pair (rows 2i, 2i+1: q and k rows come in adjacent pairs)
+// is completed inside one wave.
 template <int FMT>
 struct PhaseQKV {
     const u64* xin;  // previous layer's xf words, or null for layer 0
     u64* out;        // this layer's qkv words
     int pos, token;
     Ctl c;
-    template <int LPR>
+    template <int LPR_>
     __device__ bool go() {
+        constexpr int LPR = LPR_ > 32 ? 32 : LPR_;
         const DecodeParams& p = P();
         const DecLayer& L = LY();
         const Shared sh = lds_of();
         const DevMatrix W = L.qkv;
+        const int hd = p.hd, QW = p.heads * hd, KW = p.kv_heads * hd, half = hd / 2, cap = p.capacity;
         int r0, r1;
         my_rows(p.rows_qkv, W.rows, r0, r1);
         Rows<FMT, LPR, false> rw;
         rw.prefetch(W, W, r0, r1);
         const int H = p.hidden;
+        NormGain gain;
+        gain.load(L.attn_norm, H);
+        // (cos, sin) of this lane's first pair (CPUOps.rope angle table, CPUOps.swift:196-201)
+        const float2* rope = p.rope;
+        const int rfirst = min(r0 + (rw.local & ~1), W.rows - 2);
+        const float2 cs0 = gload_f2(rope + (int64_t)pos * half + (rfirst % hd) / 2);
         if (xin) {
             if (!wait_words(xin, H, sh.xres, c)) return false;
         } else {
@@ -308,24 +368,18 @@ struct PhaseQKV {
             for (int k = threadIdx.x; k < H; k += kT) sh.xres[k] = matrix_elem(E, token, k);
             __syncthreads();
         }
-        rmsnorm_lds(sh.xres, L.attn_norm, H, p.eps, sh.xn, sh.red);
-        float* rowbuf = sh.scr;
-        rw.run(W, W, r0, r1, sh.xn, [&](int r, float v, float) { rowbuf[r - r0] = v; });
-        __syncthreads();
-        // RoPE on (even, odd) row pairs of q and k (CPUOps.rope, CPUOps.swift:184-212), f16
-        // rounding of k/v as the cache stores them, cache append at row pos
-        // (KVCache.write, KVCache.swift:44-63) and publication of every row.
-        const int hd = p.hd, QW = p.heads * hd, KW = p.kv_heads * hd, half = hd / 2, cap = p.capacity;
-        const float2* rope = p.rope;
+        rmsnorm_lds(sh.xres, gain, H, p.eps, sh.xn, sh.red);
+        // RoPE on the pair, f16 rounding of k/v as the cache stores them, cache
+        // append at row pos (KVCache.write, KVCache.swift:44-63), publication.
         f16* kc = (f16*)L.kc;
         f16* vc = (f16*)L.vc;
-        for (int i = threadIdx.x; 2 * i < r1 - r0; i += kT) {
+        const unsigned tag = c.tag;
+        u64* o = out;
+        rw.run_pairs(W, r0, r1, sh.xn, [&](int r, float v0, float v1) {
 #pragma clang fp contract(off)
-            const int r = r0 + 2 * i;
-            float v0 = rowbuf[2 * i], v1 = rowbuf[2 * i + 1];
             const int d = r % hd;
             if (r < QW + KW) {
-                const float2 cs = gload_f2(rope + (int64_t)pos * half + d / 2);
+                const float2 cs = r == rfirst ? cs0 : gload_f2(rope + (int64_t)pos * half + d / 2);
                 const float ac = v0 * cs.x, bs = v1 * cs.y, as = v0 * cs.y, bc = v1 * cs.x;
                 v0 = ac - bs;
                 v1 = as + bc;
@@ -340,9 +394,9 @@ struct PhaseQKV {
                 v0 = (float)h0;
                 v1 = (float)h1;
             }
-            put_word(out + r, v0, c.tag);
-            put_word(out + r + 1, v1, c.tag);
-        }
+            put_word(o + r, v0, tag);
+            put_word(o + r + 1, v1, tag);
+        });
         return true;
     }
 };
@@ -636,8 +690,10 @@ struct PhaseGateUp {
         my_rows(p.rows_ffn, Wg.rows, r0, r1);
         Rows<FMT, LPR, true> rw;
         rw.prefetch(Wg, Wu, r0, r1);
+        NormGain gain;
+        gain.load(L.ffn_norm, p.hidden);
         if (!wait_words(in, p.hidden, sh.xres, c)) return false;
-        rmsnorm_lds(sh.xres, L.ffn_norm, p.hidden, p.eps, sh.xn, sh.red);
+        rmsnorm_lds(sh.xres, gain, p.hidden, p.eps, sh.xn, sh.red);
         const unsigned tag = c.tag;
         u64* o = out;
         rw.run(Wg, Wu, r0, r1, sh.xn,
@@ -662,8 +718,10 @@ struct PhaseLogits {
         my_rows(p.rows_out, W.rows, r0, r1);
         Rows<FMT, LPR, false> rw;
         rw.prefetch(W, W, r0, r1);
+        NormGain gain;
+        gain.load(p.out_norm, p.hidden);
         if (!wait_words(in, p.hidden, sh.xres, c)) return false;
-        rmsnorm_lds(sh.xres, p.out_norm, p.hidden, p.eps, sh.xn, sh.red);
+        rmsnorm_lds(sh.xres, gain, p.hidden, p.eps, sh.xn, sh.red);
         float best = -INFINITY;
         int bi = INT_MAX;
         float* logits = p.logits;
@@ -918,12 +976,13 @@ hipError_t decode_kernel_occupancy(int fmt, int hd, int heads, int kv_heads, siz
     return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, f, kT, lds);
 }
 
-hipError_t launch_decode_step(int fmt, const DecodeParams& p, int grid, size_t lds, hipStream_t st) {
+hipError_t launch_decode_step(int fmt, const DecodeParams& p, int grid, size_t lds, int cooperative, hipStream_t st) {
     const void* f = kernel_for(fmt, p.hd, p.heads, p.kv_heads);
     if (!f) return hipErrorInvalidValue;
     DecodeParams a = p;
     void* args[] = {&a};
-    return hipLaunchCooperativeKernel(f, dim3(grid), dim3(kT), args, (unsigned)lds, st);
+    if (cooperative) return hipLaunchCooperativeKernel(f, dim3(grid), dim3(kT), args, (unsigned)lds, st);
+    return hipLaunchKernel(f, dim3(grid), dim3(kT), args, lds, st);
 }
 
 #endif  // DECODE_FMT

@@ -571,7 +571,7 @@ struct ahip_session {
     bool graph_failed = false;
     // persistent single-token decode (kernels_decode.hip): one cooperative launch per token
     bool pdec = false;
-    int pdec_fmt = 0, pdec_grid = 0;
+    int pdec_fmt = 0, pdec_grid = 0, pdec_coop = 1;
     size_t pdec_lds = 0;
     DecodeParams pdec_params;
     DevBuf pdec_layers, pdec_xbuf, pdec_ctl;  // ctl: [0] epoch, [1] abort word
@@ -685,7 +685,8 @@ static int pdec_reset_words(ahip_session* s) {
 // per CU); ALPACA_HIP_DECODE_ITEMS the attention items aimed for;
 // ALPACA_HIP_DECODE_TIMEOUT_US the bound on each wait inside the kernel;
 // ALPACA_HIP_DECODE_ABORT_LAYER (failure-path tests) makes every launch abort
-// at that layer.
+// at that layer; ALPACA_HIP_DECODE_COOPERATIVE=0 uses ordinary launches (for
+// profilers that cannot follow cooperative ones).
 static int setup_persistent_decode(ahip_session* s) {
     ahip_model* m = s->m;
     const ahip_llama_config& c = m->c;
@@ -791,6 +792,7 @@ static int setup_persistent_decode(ahip_session* s) {
     p.abort_at_layer = env_int("ALPACA_HIP_DECODE_ABORT_LAYER", -1);  // failure-path tests
     s->pdec_params = p;
     s->pdec_clock_khz = clock_khz;
+    s->pdec_coop = env_int("ALPACA_HIP_DECODE_COOPERATIVE", 1);
     s->pdec_fmt = fmt;
     s->pdec_grid = grid;
     s->pdec_lds = lds;
@@ -817,7 +819,7 @@ static int pdec_launch(ahip_session* s, bool logits, bool emitted) {
         HIP_OR(hipMemsetAsync(s->pdec_trace.p, 0, n * 8, s->stream), "clear trace");
         p.trace = s->pdec_trace.as<unsigned long long>();
     }
-    LAUNCH(launch_decode_step(s->pdec_fmt, p, s->pdec_grid, s->pdec_lds, s->stream));
+    LAUNCH(launch_decode_step(s->pdec_fmt, p, s->pdec_grid, s->pdec_lds, s->pdec_coop, s->stream));
     s->pdec_launches++;
     return AHIP_OK;
 }

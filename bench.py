@@ -2,21 +2,26 @@
 """Benchmark of the Llama forward hot path on one MI355X.
 
 Workload (BASELINE.json metric "prefill tok/s @4096, decode tok/s @2048 ctx
-(Q8_0)"): the 135M-shaped Q8_0 decoder (config C1: 30 layers, hidden 576,
-9/3 heads, head_dim 64, FFN 1536, vocab 49152, tied embeddings), random-init
-synthetic weights.
+(Q8_0); % of HBM/MFMA peak"): the 135M-shaped Q8_0 decoder (config C1: 30
+layers, hidden 576, 9/3 heads, head_dim 64, FFN 1536, vocab 49152, tied
+embeddings), random-init synthetic weights, all resident in HBM.
 
   * value: decode tok/s at context 2048.  A step is one greedy decode token
-    through the GPU-resident chain (MetalLlamaSession.decodeGreedy semantics):
-    the session is prefilled to 2048 - warmup positions, `warmup` untimed
-    steps bring it to 2048, then exactly `steps` steps are timed.
-  * prefill_tok_s: 4096-token prompt / wall time of forward (median of runs).
-  * roofline: the dominant decode kernel (by total time), from HIP events the
-    session records on its own stream around each stage in a profiled pass
-    over the same decode steps; achieved = algorithmic bytes per launch /
-    mean launch time, against 8 TB/s.
-  * roofline_prefill: the dominant prefill GEMM, algorithmic FLOPs per launch
-    / mean launch time, against 2.5 PFLOP/s dense fp16.
+    through the GPU-resident chain (MetalLlamaSession.decodeGreedy semantics,
+    MetalLlamaModel.swift:228-270): the session is prefilled to
+    2048 - warmup positions, `warmup` untimed steps bring it to 2048, then
+    exactly `steps` steps are timed by the wall clock around decode_greedy.
+    Each step is one launch of the persistent decode kernel.
+  * roofline (decode): that kernel.  Algorithmic bytes per launch = bytes one
+    token must move (every projection in Q8_0 at 34 B per 32 weights, the tied
+    output matrix, the norm gains, the f16 KV rows read at the mean timed
+    context and the row written), divided by the mean launch duration measured
+    with HIP events the session records on its own stream around the timed
+    steps; peak 8 TB/s.
+  * prefill_tok_s: 4096-token prompt / median wall time of forward.
+  * roofline_prefill: the dominant prefill GEMM (MFMA, f16 operands, f32
+    accumulate): algorithmic FLOPs per launch / mean launch time from the
+    session's per-stage HIP events; peak 2.5 PFLOP/s dense fp16.
   * cpu_baseline: the C oracle (restatement of AlpacaCore's CPU path) on the
     host cores: decode steps at context 2048 (the oracle's cache is filled
     with synthetic rows, since prefilling 2048 positions on the CPU would take
@@ -47,19 +52,23 @@ def q8_bytes(rows: int, cols: int) -> int:
     return rows * cols // 32 * 34
 
 
-def decode_stage_bytes(c, ctx_len: float) -> dict:
-    """Algorithmic HBM bytes per launch of each decode stage (one token)."""
-    H, QW, KW, F, V = c.hidden_size, c.query_width, c.kv_width, c.feed_forward_size, c.vocab_size
+def decode_token_bytes(c, ctx_len: float) -> float:
+    """Algorithmic HBM bytes of one decode token at context ctx_len."""
+    H, QW, KW, F, V, L = c.hidden_size, c.query_width, c.kv_width, c.feed_forward_size, c.vocab_size, c.layer_count
+    proj = L * (q8_bytes(QW + 2 * KW, H) + q8_bytes(H, QW) + 2 * q8_bytes(F, H) + q8_bytes(H, F))
+    return proj + q8_bytes(V, H) + (2 * L + 1) * H * 4 + 2 * L * ctx_len * KW * 2 + 2 * L * KW * 2
+
+
+def decode_phase_bytes(c, ctx_len: float) -> dict:
+    """Algorithmic bytes of each phase of one layer (weights or KV rows it must read)."""
+    H, QW, KW, F = c.hidden_size, c.query_width, c.kv_width, c.feed_forward_size
     return {
-        "qkv (fused norm)": q8_bytes(QW + 2 * KW, H) + 4 * (2 * H + QW + 2 * KW),
-        "rope + kv store": 4 * (QW + 2 * KW) * 2 + 2 * 2 * KW,
-        "attention": 2 * 2 * ctx_len * KW + 4 * (QW + 2 * KW) + 4 * QW,
-        "attn out projection (+residual)": q8_bytes(H, QW) + 4 * (QW + 2 * H),
-        "ffn gate+up+silu (fused norm)": 2 * q8_bytes(F, H) + 4 * (2 * H + F),
-        "ffn down (+residual)": q8_bytes(H, F) + 4 * (F + 2 * H),
-        "final norm + logits": q8_bytes(V, H) + 4 * (2 * H + V),
-        "embed": H // 32 * 34 + 4 * H,
-        "sample": 4 * V,
+        "qkv (fused norm)": q8_bytes(QW + 2 * KW, H) + 4 * H,
+        "attention": 2 * 2 * ctx_len * KW,
+        "attn out projection (+residual)": q8_bytes(H, QW),
+        "ffn gate+up+silu (fused norm)": 2 * q8_bytes(F, H) + 4 * H,
+        "ffn down (+residual)": q8_bytes(H, F),
+        "final norm + logits": q8_bytes(c.vocab_size, H) + 4 * H,
     }
 
 
@@ -74,15 +83,29 @@ def prefill_stage_flops(c, T: int) -> dict:
     }
 
 
-def stage_table(profile: dict, units: dict, scale: float, unit: str) -> dict:
+def stage_table(profile: dict, units: dict, scale: float, unit: str, per: int = 1) -> dict:
     out = {}
     for label, st in profile.items():
         avg = st.seconds / max(st.dispatches, 1)
-        row = {"total_ms": round(st.seconds * 1e3, 4), "launches": st.dispatches, "avg_us": round(avg * 1e6, 3)}
+        row = {"total_ms": round(st.seconds * 1e3 / per, 4), "count": st.dispatches // per,
+               "avg_us": round(avg * 1e6, 3)}
         if label in units and avg > 0:
             row[f"achieved_{unit}"] = round(units[label] / avg / scale, 2)
         out[label] = row
     return out
+
+
+def measured_traffic(root: str):
+    """HBM bytes per decode launch from the committed rocprofv3 counter summary
+    (FETCH_SIZE and WRITE_SIZE runs, scaled by a copy of known size), or None."""
+    import re
+    path = os.path.join(root, "profiles", "c1_decode_hbm_counters.md")
+    try:
+        with open(path) as f:
+            m = re.search(r"Traffic per launch[^:]*:\s*([0-9.]+)\s*MB", f.read())
+    except OSError:
+        return None
+    return None if not m else float(m.group(1)) * 1e6
 
 
 def cpu_baseline(weights, spec, budget_s: float = 12.0) -> dict:
@@ -115,12 +138,16 @@ def cpu_baseline(weights, spec, budget_s: float = 12.0) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--depth", type=int, default=3, help="greedy-chain steps queued ahead (reference default 3)")
     ap.add_argument("--prefill-runs", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the timed decode steps (for counter passes of the decode kernel)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only a device-to-device copy of 256 MiB, the reference the HBM byte counters are scaled by")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -130,6 +157,15 @@ def main() -> int:
     if args.steps < 1 or args.warmup < 0 or args.warmup >= DECODE_CTX:
         print("need steps >= 1 and 0 <= warmup < 2048", file=sys.stderr)
         return 2
+
+    if args.calibrate_copy:
+        import torch
+        a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+        log("copied 256 MiB device to device")
+        return 0
 
     import numpy as np
 
@@ -160,9 +196,28 @@ def main() -> int:
     t0 = time.perf_counter()
     fed = s.decode_greedy(first, args.steps, lambda t: timed.append(t) or True, depth=args.depth)
     el = time.perf_counter() - t0
+    gpu_s = s.last_gpu_seconds
     assert fed == args.steps
     decode_tok_s = args.steps / el
-    log(f"decode: {decode_tok_s:.1f} tok/s ({el / args.steps * 1e3:.3f} ms/token)")
+    avg_launch = gpu_s / args.steps
+    mean_ctx = DECODE_CTX + (args.steps - 1) / 2 + 1
+    tok_bytes = decode_token_bytes(c, mean_ctx)
+    achieved = tok_bytes / avg_launch / 1e9
+    roof = {"bound": "hbm", "kernel": "decode_step_kernel (persistent, one cooperative launch per token)",
+            "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 5),
+            "traffic": measured_traffic(os.path.dirname(os.path.abspath(__file__))),
+            "traffic_source": "profiles/c1_decode_hbm_counters.md (rocprofv3 FETCH_SIZE x2.00 + WRITE_SIZE x1.00)",
+            "bytes_per_launch": int(tok_bytes), "avg_launch_us": round(avg_launch * 1e6, 3),
+            "timing": "HIP events on the session stream around the timed steps, divided by the steps"}
+    log(f"decode: {decode_tok_s:.1f} tok/s ({el / args.steps * 1e3:.3f} ms/token wall, "
+        f"{avg_launch * 1e6:.1f} us/launch GPU, {achieved:.0f} GB/s algorithmic)")
+    if args.decode_only:
+        print(json.dumps({"decode_tok_s": round(decode_tok_s, 2), "roofline": roof}), flush=True)
+        s.close()
+        model.close()
+        ctx.close()
+        return 0
 
     # ---------------------------------------------------------------- prefill
     p = model.make_session(capacity=PREFILL_TOKENS, max_batch=PREFILL_TOKENS)
@@ -180,21 +235,15 @@ def main() -> int:
         f"GPU {np.median(gpus) * 1e3:.2f} ms)")
 
     # ---------------------------------------------------------------- stage profiles
-    roof, roof_p, stages_d, stages_p = None, None, {}, {}
+    roof_p, stages_d, stages_p = None, {}, {}
     if not args.no_profile:
+        prof_steps = min(args.steps, 32)
         s2 = model.make_session(capacity=cap, max_batch=PREFILL_TOKENS)
         t2 = int(np.argmax(s2.forward(prompt[:DECODE_CTX])))
         s2.profiling_enabled = True
-        s2.decode_greedy(t2, args.steps, lambda t: True, depth=args.depth)
-        prof = s2.last_profile
-        units = decode_stage_bytes(c, DECODE_CTX + args.steps / 2)
-        stages_d = stage_table(prof, units, 1e9, "GBs")
-        dom = max((k for k in prof if k in units), key=lambda k: prof[k].seconds)
-        avg = prof[dom].seconds / prof[dom].dispatches
-        achieved = units[dom] / avg / 1e9
-        roof = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "bytes_per_launch": int(units[dom]), "avg_launch_us": round(avg * 1e6, 3)}
+        s2.decode_greedy(t2, prof_steps, lambda t: True, depth=args.depth)
+        stages_d = stage_table(s2.last_profile, decode_phase_bytes(c, DECODE_CTX + prof_steps / 2), 1e9, "GBs",
+                               per=prof_steps)
         p.profiling_enabled = True
         p.forward(prompt)
         profp = p.last_profile
@@ -210,7 +259,7 @@ def main() -> int:
         gemm_s = sum(profp[k].seconds for k in profp if k in fl and k != "attention")
         gemm_f = sum(fl[k] * profp[k].dispatches for k in profp if k in fl and k != "attention")
         roof_p["all_prefill_gemms_frac"] = round(gemm_f / gemm_s / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
-        log(f"decode dominant stage: {dom} {achieved:.0f} GB/s; prefill dominant GEMM: {domp} {ach:.1f} TFLOP/s")
+        log(f"prefill dominant GEMM: {domp} {ach:.1f} TFLOP/s")
 
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
@@ -233,11 +282,17 @@ def main() -> int:
         "prefill_tok_s": round(prefill_tok_s, 1),
         "decode_ms_per_token": round(el / args.steps * 1e3, 4),
         "roofline": roof, "roofline_prefill": roof_p, "cpu_baseline": cpu,
-        "stages_decode": stages_d, "stages_prefill": stages_p,
+        "stages_decode_per_token": stages_d, "stages_prefill": stages_p,
         "reference_m5": {"prefill_tok_s_4096": 24069, "decode_tok_s_ctx2048": 456,
                          "note": "Apple M5, real SmolLM2-135M Q8_0 (BASELINE.md); context only"},
     }
     print(json.dumps(line), flush=True)
+    for h in (s, p):
+        h.close()
+    if not args.no_profile:
+        s2.close()
+    model.close()
+    ctx.close()
     return 0
 
 
