@@ -6,13 +6,16 @@
 // KernelEncoder.swift:192-280.  CPU semantics: CPUOps.linear / dot
 // (CPUOps.swift:77-139).
 //
-// gemm_mfma_kernel (fast): f16 activations; quantised weights staged in LDS as
-// their integer quants in f16 (exact) with the per-block f16 scale kept in
-// float32; one v_mfma_f32_16x16x32_f16 covers one 32-weight block and its
-// result is scaled by d before accumulation, so the only rounding on the
-// inputs is the activations' (float32 -> f16).  256 threads = 2x2 waves; BK = 64 (two quant
-// blocks) per LDS stage, double-buffered: the next stage's global loads are in
-// registers while the current stage is multiplied, one barrier per stage.
+// Fast path (f16 MFMA): f16 activations; quantised weights enter as their
+// integer quants in f16 (exact) with the per-block f16 scale kept in float32;
+// one v_mfma_f32_16x16x32_f16 covers one 32-weight block and its result is
+// scaled by d before accumulation, so the only rounding on the inputs is the
+// activations' (float32 -> f16).  (Rounding half(d*q) as the reference's
+// tensor-op path does moves C1 prefill logits past the 2e-3 bound against the
+// CPU reference; exact quants keep them at 1.6e-3.)
+//   dgemm_kernel: global -> LDS DMA, three stages in flight (the default).
+//   gemm_mfma_kernel: register-staged, double-buffered; shapes the DMA kernel
+//   does not take.
 // Epilogues: store f32, accumulate into the f32 residual, or SwiGLU
 // (silu(x Wg^T) * (x Wu^T) from two accumulator sets) written as f16.
 //
@@ -21,6 +24,9 @@
 // block sum is scaled once (acc += d * s), with FP contraction off, so each
 // output equals the CPU reference's float32 result.
 #include "common.h"
+
+#include <cstdlib>
+#include <cstring>
 
 namespace {
 
@@ -410,8 +416,10 @@ hipError_t run_f32(const GemmF32Args& a, int mode, hipStream_t st) {
 
 }  // namespace
 
-hipError_t launch_gemm_mfma(const f16* x, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up, float* y,
-                            f16* yh, int ldy, int mode, hipStream_t st) {
+// Register-staged kernel: shapes the LDS-DMA kernel does not take (K not a
+// multiple of 64, activation rows not 16-byte aligned).
+static hipError_t launch_gemm_mfma_staged(const f16* x, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up,
+                                         float* y, f16* yh, int ldy, int mode, hipStream_t st) {
     if (m <= 0) return hipSuccess;
     GemmArgs a;
     a.x = x;
@@ -444,5 +452,356 @@ hipError_t launch_gemm_f32(const float* x, int ldx, int m, const DevMatrix& w, c
     case DT_Q8_0: return run_f32<DT_Q8_0>(a, mode, st);
     case DT_Q4_0: return run_f32<DT_Q4_0>(a, mode, st);
     default: return run_f32<DT_F16>(a, mode, st);
+    }
+}
+
+// ------------------------------------------------------------------ LDS-DMA pipelined GEMM
+//
+// Same arithmetic as gemm_mfma_kernel (integer quants exact in f16, f16
+// activations, one v_mfma_f32_16x16x32_f16 per 32-weight block whose float32
+// result is scaled by the block's d and accumulated), built for latency: the
+// prefill projections are thin (K = 576..8192, a few hundred tiles on 256
+// CUs), so each workgroup keeps several K stages of loads in flight.  Stages
+// are 64 wide in K (two quant blocks) and move global -> LDS with
+// global_load_lds_dwordx4 (no VGPR staging, no LDS store instructions): stage
+// kt+2 is in flight while stage kt is multiplied; three LDS buffers, one
+// barrier per stage.  The DMA writes 64 lanes x 16 bytes contiguously, so the
+// LDS layout is fixed per instruction and the lane -> global-address map does
+// the swizzling:
+//   A / F16 weights: rows of 128 B (8 chunks of 16 B), chunk c of row r at
+//     slot c ^ swz_a(r), swz_a(r) = (r & 7) ^ ((r >> 1) & 4), which puts the
+//     16 rows one MFMA fragment read touches in 16 distinct 16-byte bank groups;
+//   Q8_0 quants: rows of 64 B (4 chunks), slot c ^ ((r >> 2) & 3);
+//   Q4_0 nibbles: rows of 32 B (2 blocks), slot c ^ ((r >> 3) & 1);
+//   scales: the stage's 2 f16 per row, 4-byte DMA.
+// Quants become f16 per MFMA fragment after the LDS read (8 bytes -> 8 halves
+// with a byte permute and a packed-f16 subtract: 0x64xx is 1024 + xx, so
+// (1024 + q + 128) - 1152 = q exactly).  Tiles are taken in an XCD-major
+// order so that tiles sharing A rows run on one XCD and share its L2.
+namespace {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+__device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// 4 signed bytes -> 2 dwords holding the 4 quants as f16 pairs (exact).
+__device__ __forceinline__ void int8x4_to_f16(uint32_t w, uint32_t& o0, uint32_t& o1) {
+    const uint32_t u = w ^ 0x80808080u;  // q + 128 in each byte
+    const h2 bias = {(f16)1152.0f, (f16)1152.0f};
+    o0 = as_u32(as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias);
+    o1 = as_u32(as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias);
+}
+// 4 nibbles (one per byte, already masked) -> nib - 8 as f16 pairs (exact).
+__device__ __forceinline__ void nib4_to_f16(uint32_t nib, uint32_t& o0, uint32_t& o1) {
+    const h2 bias = {(f16)1032.0f, (f16)1032.0f};
+    o0 = as_u32(as_h2(__builtin_amdgcn_perm(0x64646464u, nib, 0x04010400u)) - bias);
+    o1 = as_u32(as_h2(__builtin_amdgcn_perm(0x64646464u, nib, 0x04030402u)) - bias);
+}
+
+constexpr int DBK = 64;  // K per stage
+
+// global -> LDS DMA of 16 (or 4) bytes per lane: lane l writes LDS bytes
+// [lds + size*l, lds + size*(l+1)).  Issued through asm so that the only waits on
+// these loads are the explicit ones in wait_stage_barrier (the compiler's own
+// tracking of LDS DMA falls back to waiting for every outstanding load before
+// each LDS read, which would serialise the pipeline).  The asm sets m0, which
+// nothing else in these kernels uses; one wait state separates the m0 write from
+// the load that reads it (the compiler puts the same s_nop after its own m0
+// writes for LDS DMA).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ int swz_a(int r) { return (r & 7) ^ ((r >> 1) & 4); }
+__device__ __forceinline__ int swz_q8(int r) { return (r >> 2) & 3; }
+__device__ __forceinline__ int swz_q4(int r) { return (r >> 3) & 1; }
+
+// Wait until at most N of this wave's global loads are outstanding, and for
+// its LDS reads, then barrier.  The "memory" clobber keeps LDS accesses on
+// their side of the barrier.
+template <int N>
+__device__ __forceinline__ void wait_stage_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Byte layout of one stage buffer: A rows, then each matrix's weight rows,
+// then each matrix's scales.
+template <int FMT, int BM, int BN, int NB>
+struct DStage {
+    static constexpr int BROW = FMT == DT_Q8_0 ? 64 : FMT == DT_Q4_0 ? 32 : 128;  // weight bytes per row
+    static constexpr int SROW = FMT == DT_F16 ? 0 : 4;                             // scale bytes per row
+    static constexpr int B_OFF = BM * DBK * 2;
+    static constexpr int S_OFF = B_OFF + NB * BN * BROW;
+    static constexpr int BYTES = S_OFF + NB * BN * SROW + 16;
+};
+
+template <int FMT, int BM, int BN, int WM, int WN, int MODE>
+struct DGemm {
+    static constexpr int NB = MODE == GEMM_SWIGLU ? 2 : 1;
+    static constexpr int TM = WM / 16, TN = WN / 16;
+    static_assert((BM / WM) * (BN / WN) == 4, "four waves");
+    // DMA instructions per wave per stage
+    static constexpr int A_I = BM / 32;  // 8 rows of 128 B per instruction, 4 waves
+    static constexpr bool Q4_16 = (BN / 32) % 4 == 0;
+    static constexpr int B_I = FMT == DT_Q8_0 ? BN / 64 : FMT == DT_Q4_0 ? (Q4_16 ? BN / 128 : BN / 32) : BN / 32;
+    static constexpr int S_I = FMT == DT_F16 ? 0 : BN / 64;  // every wave loads all scale rows (identical bytes)
+    static constexpr int PER = A_I + NB * (B_I + S_I);
+    static_assert(BM % 32 == 0 && BN % 64 == 0, "tile shape");
+};
+
+template <int FMT, int BM, int BN, int WM, int WN, int MODE>
+__global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
+    using G = DGemm<FMT, BM, BN, WM, WN, MODE>;
+    using L = DStage<FMT, BM, BN, G::NB>;
+    constexpr int NB = G::NB, TM = G::TM, TN = G::TN, PER = G::PER;
+    __shared__ __attribute__((aligned(16))) uint8_t st0[L::BYTES], st1[L::BYTES], st2[L::BYTES];
+
+    const int K = p.w.cols, N = p.w.rows, M = p.M, nb = K >> 5;
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, tiles = tiles_m * tiles_n;
+    const int b = blockIdx.x, xcd = b % 8, q = tiles / 8, rem = tiles % 8;
+    const int t = xcd * q + min(xcd, rem) + b / 8;  // XCD-major tile order (bijective)
+    const int m0 = (t / tiles_n) * BM, n0 = (t % tiles_n) * BN;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / (BN / WN), wn = wave % (BN / WN);
+    const int nk = K / DBK;
+
+    auto issue = [&](uint32_t sg, int kt) {  // sg: LDS byte address of the stage buffer
+        const int k0 = kt * DBK;
+#pragma unroll
+        for (int i = 0; i < G::A_I; i++) {
+            const int r0 = (i * 4 + wave) * 8, r = r0 + (lane >> 3), c = (lane & 7) ^ swz_a(r);
+            dma16(p.x + (int64_t)min(m0 + r, M - 1) * p.ldx + k0 + c * 8, sg + r0 * DBK * 2);
+        }
+#pragma unroll
+        for (int mat = 0; mat < NB; mat++) {
+            const DevMatrix& w = mat ? p.u : p.w;
+            const uint32_t bq = sg + L::B_OFF + mat * BN * L::BROW;
+#pragma unroll
+            for (int i = 0; i < G::B_I; i++) {
+                if constexpr (FMT == DT_Q8_0) {
+                    const int r0 = (i * 4 + wave) * 16, r = r0 + (lane >> 2), c = (lane & 3) ^ swz_q8(r);
+                    dma16(w.q + (int64_t)min(n0 + r, N - 1) * K + k0 + c * 16, bq + r0 * 64);
+                } else if constexpr (FMT == DT_Q4_0) {
+                    if constexpr (G::Q4_16) {
+                        const int r0 = (i * 4 + wave) * 32, r = r0 + (lane >> 1), c = (lane & 1) ^ swz_q4(r);
+                        dma16(w.q + ((int64_t)min(n0 + r, N - 1) * nb + 2 * kt + c) * 16, bq + r0 * 32);
+                    } else {
+                        const int r0 = (i * 4 + wave) * 8, r = r0 + (lane >> 3), c = ((lane >> 2) & 1) ^ swz_q4(r);
+                        dma4(w.q + ((int64_t)min(n0 + r, N - 1) * nb + 2 * kt + c) * 16 + (lane & 3) * 4, bq + r0 * 32);
+                    }
+                } else {
+                    const int r0 = (i * 4 + wave) * 8, r = r0 + (lane >> 3), c = (lane & 7) ^ swz_a(r);
+                    dma16(w.q + ((int64_t)min(n0 + r, N - 1) * K + k0 + c * 8) * 2, bq + r0 * 128);
+                }
+            }
+            if constexpr (FMT != DT_F16) {
+#pragma unroll
+                for (int i = 0; i < G::S_I; i++) {
+                    const int r = i * 64 + lane;
+                    dma4(w.s + (int64_t)min(n0 + r, N - 1) * nb + 2 * kt, sg + L::S_OFF + mat * BN * 4 + i * 256);
+                }
+            }
+        }
+    };
+
+    f32x4 acc[NB][TM][TN];
+#pragma unroll
+    for (int mat = 0; mat < NB; mat++)
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[mat][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int jj = lane >> 4;  // which 8 of the fragment's 32 k values this lane holds
+    // Quantised weights, one 32-weight block (kk) of a stage: each MFMA result
+    // is scaled by the block's d before it is accumulated.  The MFMAs of column
+    // j+1 are issued before the scaling of column j, so the VALU work of one
+    // column runs under the MFMAs of the next instead of waiting on them.
+    auto compute_block_quant = [&](const uint8_t* sg, int kk, const f16x8 (&af)[TM]) {
+        f16x8 bf[NB * TN];
+        float d[NB * TN];
+#pragma unroll
+        for (int c = 0; c < NB * TN; c++) {
+            const int mat = c / TN, j = c % TN;
+            const int r = wn * WN + 16 * j + (lane & 15);
+            const uint8_t* bq = sg + L::B_OFF + mat * BN * L::BROW;
+            uint2 raw;
+            uint32_t o[4];
+            if constexpr (FMT == DT_Q8_0) {
+                const int u = 4 * kk + jj;
+                raw = *(const uint2*)(bq + r * 64 + ((u >> 1) ^ swz_q8(r)) * 16 + (u & 1) * 8);
+                int8x4_to_f16(raw.x, o[0], o[1]);
+                int8x4_to_f16(raw.y, o[2], o[3]);
+            } else {
+                raw = *(const uint2*)(bq + r * 32 + (kk ^ swz_q4(r)) * 16 + (jj & 1) * 8);
+                const int sh = (jj >> 1) * 4;
+                nib4_to_f16((raw.x >> sh) & 0x0F0F0F0Fu, o[0], o[1]);
+                nib4_to_f16((raw.y >> sh) & 0x0F0F0F0Fu, o[2], o[3]);
+            }
+            bf[c] = __builtin_bit_cast(f16x8, make_uint4(o[0], o[1], o[2], o[3]));
+            d[c] = (float)*(const f16*)(sg + L::S_OFF + mat * BN * 4 + r * 4 + kk * 2);
+        }
+        f32x4 prev[TM], cur[TM];
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < TM; i++) prev[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[0], zero, 0, 0, 0);
+#pragma unroll
+        for (int c = 1; c <= NB * TN; c++) {
+            if (c < NB * TN) {
+#pragma unroll
+                for (int i = 0; i < TM; i++) cur[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[c], zero, 0, 0, 0);
+            }
+            const int pc = c - 1, mat = pc / TN, j = pc % TN;
+#pragma unroll
+            for (int i = 0; i < TM; i++) acc[mat][i][j] += d[pc] * prev[i];
+#pragma unroll
+            for (int i = 0; i < TM; i++) prev[i] = cur[i];
+        }
+    };
+    auto compute = [&](const uint8_t* sg) {
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+            f16x8 af[TM];
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const int r = wm * WM + 16 * i + (lane & 15);
+                af[i] = *(const f16x8*)(sg + r * DBK * 2 + ((4 * kk + jj) ^ swz_a(r)) * 16);
+            }
+#pragma unroll
+            for (int mat = 0; mat < NB; mat++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const int r = wn * WN + 16 * j + (lane & 15);
+                    const uint8_t* bq = sg + L::B_OFF + mat * BN * L::BROW;
+                    if constexpr (FMT == DT_F16) {
+                        const f16x8 bf = *(const f16x8*)(bq + r * 128 + ((4 * kk + jj) ^ swz_a(r)) * 16);
+#pragma unroll
+                        for (int i = 0; i < TM; i++)
+                            acc[mat][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, acc[mat][i][j], 0, 0, 0);
+                    }
+                }
+            if constexpr (FMT != DT_F16) compute_block_quant(sg, kk, af);
+        }
+    };
+
+    // One step: wait for stage kt (stage kt+1 stays in flight), barrier, refill
+    // the buffer consumed by the previous step with stage kt+2, multiply stage
+    // kt.  Past the end the refill reloads the last stage into a buffer that is
+    // never read again, so every step has the same wait count.
+    auto step = [&](const uint8_t* cur, uint8_t* refill, int kt) {
+        wait_stage_barrier<PER>();
+        issue(lds_addr(refill), min(kt + 2, nk - 1));
+        compute(cur);
+    };
+    issue(lds_addr(st0), 0);
+    issue(lds_addr(st1), min(1, nk - 1));
+    for (int kt = 0; kt < nk; kt += 3) {
+        step(st0, st2, kt);
+        if (kt + 1 < nk) step(st1, st0, kt + 1);
+        if (kt + 2 < nk) step(st2, st1, kt + 2);
+    }
+    // No DMA may still be writing this workgroup's LDS when its waves end.
+    wait_stage_barrier<0>();
+
+    // C layout of the 16x16 MFMA: lane holds rows 4*(lane/16)+r, column lane%16.
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + wn * WN + 16 * j + (lane & 15);
+            if (n >= N) continue;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm * WM + 16 * i + 4 * (lane >> 4) + r;
+                if (m >= M) continue;
+                const int64_t o = (int64_t)m * p.ldy + n;
+                if (MODE == GEMM_STORE) {
+                    p.y[o] = acc[0][i][j][r];
+                } else if (MODE == GEMM_ACC) {
+                    p.y[o] += acc[0][i][j][r];
+                } else {
+                    const float g = acc[0][i][j][r], u = acc[NB - 1][i][j][r];
+                    p.yh[o] = (f16)((g / (1.0f + __expf(-g))) * u);
+                }
+            }
+        }
+}
+
+template <int FMT, int BM, int BN, int WM, int WN, int MODE>
+hipError_t run_dgemm(const GemmArgs& a, hipStream_t st) {
+    const int tiles = ((a.M + BM - 1) / BM) * ((a.w.rows + BN - 1) / BN);
+    dgemm_kernel<FMT, BM, BN, WM, WN, MODE><<<tiles, 256, 0, st>>>(a);
+    return hipGetLastError();
+}
+
+// ALPACA_HIP_GEMM_TILE=256 | 128x128 | 128x64 forces a tile family (tuning);
+// 256 means 256x128 (256x64 per matrix for SwiGLU).
+int forced_tile() {
+    static const int v = [] {
+        const char* e = std::getenv("ALPACA_HIP_GEMM_TILE");
+        if (!e) return 0;
+        if (!std::strcmp(e, "256")) return 1;
+        if (!std::strcmp(e, "128x128")) return 2;
+        if (!std::strcmp(e, "128x64")) return 3;
+        return 0;
+    }();
+    return v;
+}
+
+// Tile choice: the largest tile whose grid still gives every CU a workgroup.
+template <int FMT, int MODE>
+hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
+    const int M = a.M, N = a.w.rows;
+    auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+    constexpr int kCUs = 256;
+    const int f = forced_tile();
+    if constexpr (MODE == GEMM_SWIGLU) {
+        if (f == 1 || (f == 0 && tiles(256, 64) >= kCUs)) return run_dgemm<FMT, 256, 64, 128, 32, MODE>(a, st);
+        return run_dgemm<FMT, 128, 64, 64, 32, MODE>(a, st);
+    } else {
+        if (f == 1 || (f == 0 && tiles(256, 128) >= kCUs)) return run_dgemm<FMT, 256, 128, 128, 64, MODE>(a, st);
+        if (f == 2 || (f == 0 && tiles(128, 128) >= kCUs)) return run_dgemm<FMT, 128, 128, 64, 64, MODE>(a, st);
+        return run_dgemm<FMT, 128, 64, 64, 32, MODE>(a, st);
+    }
+}
+
+template <int FMT>
+hipError_t dgemm_mode(const GemmArgs& a, int mode, hipStream_t st) {
+    if (mode == GEMM_STORE) return pick_dgemm<FMT, GEMM_STORE>(a, st);
+    if (mode == GEMM_ACC) return pick_dgemm<FMT, GEMM_ACC>(a, st);
+    return pick_dgemm<FMT, GEMM_SWIGLU>(a, st);
+}
+
+}  // namespace
+
+hipError_t launch_gemm_mfma(const f16* x, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up, float* y,
+                            f16* yh, int ldy, int mode, hipStream_t st) {
+    if (m <= 0) return hipSuccess;
+    // The DMA kernel needs 64-wide K stages and 16-byte aligned activation rows.
+    if (w.cols % DBK || ldx % 8 || ((uintptr_t)x & 15))
+        return launch_gemm_mfma_staged(x, ldx, m, w, w_up, y, yh, ldy, mode, st);
+    GemmArgs a;
+    a.x = x;
+    a.ldx = ldx;
+    a.M = m;
+    a.w = w;
+    a.u = w_up ? *w_up : w;
+    a.y = y;
+    a.yh = yh;
+    a.ldy = ldy;
+    switch (w.dtype) {
+    case DT_Q8_0: return dgemm_mode<DT_Q8_0>(a, mode, st);
+    case DT_Q4_0: return dgemm_mode<DT_Q4_0>(a, mode, st);
+    default: return dgemm_mode<DT_F16>(a, mode, st);
     }
 }

@@ -70,6 +70,26 @@ def test_fast_gemm_within_analytic_bound(hip_ops, k, n, name, dt):  # KernelTest
     print(f"[metrics] fast GEMM {name} K={k} N={n}: worst error / bound = {worst:.3f}")
 
 
+@pytest.mark.parametrize("k,n", [(64, 10), (96, 40), (576, 193), (256, 300)])
+@pytest.mark.parametrize("name,dt", FORMATS)
+def test_fast_gemm_weights_enter_exactly(hip_ops, k, n, name, dt):
+    """The f16 MFMA GEMM takes the integer quants exactly (f16 holds them) and
+    scales each 32-weight block's float32 result by its d.
+
+    With the identity as activations every output is one weight times 1.0 plus
+    exact zeros, so Y = W^T must equal the float32 dequantisation bit for bit
+    (d * q is exact in float32): a wrong nibble order, block index, scale row or
+    LDS swizzle changes a value.  K = 96 takes the register-staged kernel, the
+    others the LDS-DMA one.
+    """
+    w = encode(rand((n, k), 17 * k + n, 0.3), dt)
+    deq = orc.dequantize(dt, w.data, n * k).reshape(n, k)
+    gpu = hip_ops.linear(np.eye(k, dtype=np.float32), w, "fast")
+    assert gpu.shape == (k, n)
+    bad = np.argwhere(gpu != deq.T)
+    assert bad.size == 0, f"{name} K={k} N={n}: {len(bad)} weights differ, first at (k, n) = {bad[0]}"
+
+
 def test_fused_gate_up_silu(hip_ops):  # KernelTests.swift:219-244
     k, n = 576, 200
     for t in [1, 3, 16, 40, 100]:
