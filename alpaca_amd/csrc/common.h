@@ -48,7 +48,16 @@ struct DevMatrix {
     int rows = 0, cols = 0;
     const uint8_t* q = nullptr;
     const f16* s = nullptr;
+    // Quantised matrices with cols % 64 == 0 also hold their scales stage-major
+    // for the prefill GEMM: s2[kt * stage_scale_pitch(rows) + n] packs the two
+    // f16 scales of row n for K columns [64 kt, 64 kt + 64).
+    const uint32_t* s2 = nullptr;
 };
+__host__ __device__ inline int stage_scale_pitch(int rows) { return (rows + 63) & ~63; }
+// u32 elements of the s2 buffer, including 128 elements of slack that a tile
+// hanging over the last rows of the last stage may read.
+inline int64_t stage_scale_elems(int rows, int cols) { return (int64_t)(cols / 64) * stage_scale_pitch(rows) + 128; }
+hipError_t launch_stage_scales(const f16* s, uint32_t* s2, int rows, int cols, hipStream_t st);
 
 // Cross-lane moves.  DPP controls (gfx9) act inside 16-lane rows without the
 // LDS crossbar: quad_perm [1,0,3,2] = 0xB1 and [2,3,0,1] = 0x4E swap lanes

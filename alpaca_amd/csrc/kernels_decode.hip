@@ -86,15 +86,18 @@ typedef unsigned long long u64;
 
 // ------------------------------------------------------------------ LDS
 // Launch parameters and the current layer's table (copied by every workgroup).
-__shared__ __attribute__((aligned(16))) unsigned char lds_params[sizeof(DecodeParams)];
-__shared__ __attribute__((aligned(16))) unsigned char lds_layer[sizeof(DecLayer)];
+// Sizes rounded to 16 bytes: the dynamic LDS placed after these arrays is read
+// with 128-bit accesses, which lose their alignment (and most of their speed)
+// otherwise.
+__shared__ __attribute__((aligned(16))) unsigned char lds_params[(sizeof(DecodeParams) + 15) & ~size_t(15)];
+__shared__ __attribute__((aligned(16))) unsigned char lds_layer[(sizeof(DecLayer) + 15) & ~size_t(15)];
 __device__ __forceinline__ const DecodeParams& P() { return *reinterpret_cast<const DecodeParams*>(lds_params); }
 __device__ __forceinline__ const DecLayer& LY() { return *reinterpret_cast<const DecLayer*>(lds_layer); }
 
 // Dynamic LDS: [0, 32) reductions; xres [hidden], the residual row of the
 // current half-layer; xn [stage], the normalised or staged input row; then
 // scratch.
-extern __shared__ float dyn_lds[];
+extern __shared__ __attribute__((aligned(16))) float dyn_lds[];
 struct Shared {
     float* red;
     float* xres;

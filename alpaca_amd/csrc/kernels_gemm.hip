@@ -473,7 +473,7 @@ hipError_t launch_gemm_f32(const float* x, int ldx, int m, const DevMatrix& w, c
 //     16 rows one MFMA fragment read touches in 16 distinct 16-byte bank groups;
 //   Q8_0 quants: rows of 64 B (4 chunks), slot c ^ ((r >> 2) & 3);
 //   Q4_0 nibbles: rows of 32 B (2 blocks), slot c ^ ((r >> 3) & 1);
-//   scales: the stage's 2 f16 per row, 4-byte DMA.
+//   scales: the stage's 2 f16 per row, from the stage-major copy (s2).
 // Quants become f16 per MFMA fragment after the LDS read (8 bytes -> 8 halves
 // with a byte permute and a packed-f16 subtract: 0x64xx is 1024 + xx, so
 // (1024 + q + 128) - 1152 = q exactly).  Tiles are taken in an XCD-major
@@ -553,7 +553,7 @@ struct DGemm {
     static constexpr int A_I = BM / 32;  // 8 rows of 128 B per instruction, 4 waves
     static constexpr bool Q4_16 = (BN / 32) % 4 == 0;
     static constexpr int B_I = FMT == DT_Q8_0 ? BN / 64 : FMT == DT_Q4_0 ? (Q4_16 ? BN / 128 : BN / 32) : BN / 32;
-    static constexpr int S_I = FMT == DT_F16 ? 0 : BN / 64;  // every wave loads all scale rows (identical bytes)
+    static constexpr int S_I = FMT == DT_F16 ? 0 : 1;  // a quarter of the tile's scale pairs per wave
     static constexpr int PER = A_I + NB * (B_I + S_I);
     static_assert(BM % 32 == 0 && BN % 64 == 0, "tile shape");
 };
@@ -565,7 +565,7 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
     constexpr int NB = G::NB, TM = G::TM, TN = G::TN, PER = G::PER;
     __shared__ __attribute__((aligned(16))) uint8_t st0[L::BYTES], st1[L::BYTES], st2[L::BYTES];
 
-    const int K = p.w.cols, N = p.w.rows, M = p.M, nb = K >> 5;
+    const int K = p.w.cols, N = p.w.rows, M = p.M, nb = K >> 5, spitch = stage_scale_pitch(N);
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, tiles = tiles_m * tiles_n;
     const int b = blockIdx.x, xcd = b % 8, q = tiles / 8, rem = tiles % 8;
     const int t = xcd * q + min(xcd, rem) + b / 8;  // XCD-major tile order (bijective)
@@ -605,11 +605,11 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
                 }
             }
             if constexpr (FMT != DT_F16) {
-#pragma unroll
-                for (int i = 0; i < G::S_I; i++) {
-                    const int r = i * 64 + lane;
-                    dma4(w.s + (int64_t)min(n0 + r, N - 1) * nb + 2 * kt, sg + L::S_OFF + mat * BN * 4 + i * 256);
-                }
+                // The tile's BN scale pairs are contiguous in s2: each wave moves a
+                // quarter of them, 16 bytes (4 rows) per active lane.
+                if (lane < BN / 16)
+                    dma16(w.s2 + (int64_t)kt * spitch + n0 + wave * (BN / 4) + lane * 4,
+                          sg + L::S_OFF + mat * BN * 4 + wave * BN);
             }
         }
     };
@@ -787,8 +787,10 @@ hipError_t dgemm_mode(const GemmArgs& a, int mode, hipStream_t st) {
 hipError_t launch_gemm_mfma(const f16* x, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up, float* y,
                             f16* yh, int ldy, int mode, hipStream_t st) {
     if (m <= 0) return hipSuccess;
-    // The DMA kernel needs 64-wide K stages and 16-byte aligned activation rows.
-    if (w.cols % DBK || ldx % 8 || ((uintptr_t)x & 15))
+    // The DMA kernel needs 64-wide K stages, 16-byte aligned activation rows and,
+    // for quantised weights, the stage-major scales.
+    const bool quant = w.dtype != DT_F16;
+    if (w.cols % DBK || ldx % 8 || ((uintptr_t)x & 15) || (quant && (!w.s2 || (w_up && !w_up->s2))))
         return launch_gemm_mfma_staged(x, ldx, m, w, w_up, y, yh, ldy, mode, st);
     GemmArgs a;
     a.x = x;
@@ -804,4 +806,21 @@ hipError_t launch_gemm_mfma(const f16* x, int ldx, int m, const DevMatrix& w, co
     case DT_Q4_0: return dgemm_mode<DT_Q4_0>(a, mode, st);
     default: return dgemm_mode<DT_F16>(a, mode, st);
     }
+}
+
+// Stage-major scale pairs for the prefill GEMM (layout in DevMatrix::s2).
+__global__ void stage_scales_kernel(const f16* __restrict__ s, uint32_t* __restrict__ s2, int rows, int cols) {
+    const int nst = cols / 64, nb = cols / 32, pitch = stage_scale_pitch(rows);
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)rows * nst) return;
+    const int n = (int)(i / nst), kt = (int)(i % nst);
+    const uint32_t* src = (const uint32_t*)(s + (int64_t)n * nb + 2 * kt);  // nb even: 4-byte aligned
+    s2[(int64_t)kt * pitch + n] = *src;
+}
+
+hipError_t launch_stage_scales(const f16* s, uint32_t* s2, int rows, int cols, hipStream_t st) {
+    const int64_t n = (int64_t)rows * (cols / 64);
+    if (n <= 0) return hipSuccess;
+    stage_scales_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(s, s2, rows, cols);
+    return hipGetLastError();
 }

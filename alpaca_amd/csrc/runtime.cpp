@@ -277,10 +277,16 @@ struct DevBuf {
     T* as() const { return (T*)p; }
 };
 
+static int env_int(const char* name, int dflt) {
+    const char* v = std::getenv(name);
+    if (!v || !*v) return dflt;
+    return std::atoi(v);
+}
+
 // A weight matrix uploaded in the split quant/scale layout of DevMatrix.
 struct OwnedMatrix {
     DevMatrix m;
-    DevBuf q, s;
+    DevBuf q, s, s2;
     int64_t bytes = 0;
 };
 
@@ -347,6 +353,15 @@ static int upload_matrix(int dt, const std::vector<std::pair<const void*, int64_
     out.m.q = out.q.as<uint8_t>();
     out.m.s = sbytes ? out.s.as<f16>() : nullptr;
     out.bytes = qbytes + sbytes;
+    if (sbytes && cols % 64 == 0) {
+        const int64_t s2bytes = stage_scale_elems((int)rows, (int)cols) * 4;
+        if (int rc = out.s2.alloc(s2bytes)) return rc;
+        HIP_OR(hipMemsetAsync(out.s2.p, 0, s2bytes, st), "stage scales");
+        LAUNCH(launch_stage_scales(out.m.s, out.s2.as<uint32_t>(), (int)rows, (int)cols, st));
+        HIP_OR(hipStreamSynchronize(st), "stage scales");
+        out.m.s2 = out.s2.as<uint32_t>();
+        out.bytes += s2bytes;
+    }
     return AHIP_OK;
 }
 
@@ -659,12 +674,6 @@ struct ahip_session {
 
 
 // ------------------------------------------------------------------ persistent decode setup
-
-static int env_int(const char* name, int dflt) {
-    const char* v = std::getenv(name);
-    if (!v || !*v) return dflt;
-    return std::atoi(v);
-}
 
 // Clears the exchange words and restarts the launch tag at 1 (session
 // creation, tag wrap-around, and recovery after an aborted launch).
