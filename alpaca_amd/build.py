@@ -26,11 +26,13 @@ SOURCES = [("kernels_decode.hip", f"kernels_decode_{fmt}_hd{hd}",
             [f"-DDECODE_FMT={DECODE_FMT_ENUM[fmt]}", f"-DDECODE_HD={hd}", f"-DDECODE_ENTRY=decode_kernel_{fmt}_hd{hd}"])
            for fmt, hd in DECODE_VARIANTS]
 SOURCES += [(src, os.path.splitext(src)[0], []) for src in
-            ("kernels_decode.hip", "kernels_misc.hip", "kernels_gemv.hip", "kernels_attention.hip", "runtime.cpp")]
-# The prefill GEMMs scale each MFMA result on the VALU; the VGPR form of the
-# MFMA writes those results where the VALU reads them (the AGPR form adds a
-# v_accvgpr_read per result register).
-SOURCES += [("kernels_gemm.hip", "kernels_gemm", ["-mllvm", "-amdgpu-mfma-vgpr-form=1"])]
+            ("kernels_decode.hip", "kernels_misc.hip", "kernels_gemv.hip", "runtime.cpp")]
+# The prefill GEMMs scale each MFMA result on the VALU, and flash attention
+# rescales its output accumulators every key block; the VGPR form of the MFMA
+# keeps those results where the VALU reads them (the AGPR form adds a
+# v_accvgpr_read / write per result register).
+SOURCES += [(src, os.path.splitext(src)[0], ["-mllvm", "-amdgpu-mfma-vgpr-form=1"])
+            for src in ("kernels_gemm.hip", "kernels_attention.hip")]
 ARCH = "gfx950"
 # Packed FP32 instructions are disabled: hipcc -O3 otherwise emits v_pk_* forms.
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-function",

@@ -43,6 +43,36 @@ enum { DT_F32 = 0, DT_F16 = 1, DT_Q8_0 = 2, DT_Q4_0 = 3 };
 //   Q4_0: q = uint8 [rows][cols/32][16]      s = f16 [rows][cols/32]
 //         (byte j of a block: low nibble = element j, high = element j+16)
 //   F16:  q = f16 [rows][cols],              s = null
+// ------------------------------------------------------------------ LDS DMA
+// global -> LDS DMA of 16 (or 4) bytes per lane: lane l writes LDS bytes
+// [lds + size*l, lds + size*(l+1)).  Issued through asm so that the only waits on
+// these loads are the explicit ones in wait_stage_barrier (the compiler's own
+// tracking of LDS DMA falls back to waiting for every outstanding load before
+// each LDS read, which would serialise the pipeline).  The asm sets m0, which
+// nothing else in these kernels uses; one wait state separates the m0 write from
+// the load that reads it (the compiler puts the same s_nop after its own m0
+// writes for LDS DMA).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// Wait until at most N of this wave's global loads are outstanding, and for
+// its LDS reads, then barrier.  The "memory" clobber keeps LDS accesses on
+// their side of the barrier.
+template <int N>
+__device__ __forceinline__ void wait_stage_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
 struct DevMatrix {
     int dtype = DT_F16;
     int rows = 0, cols = 0;

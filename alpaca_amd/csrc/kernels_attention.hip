@@ -9,7 +9,8 @@
 // flash_attn_kernel (prefill, f16 cache, hd 64/128): replaces the reference's
 // tensor-op and simdgroup prefill attention (tensor_attention.metal,
 // attention_prefill.metal).  A workgroup takes 64 queries of one head (16 per
-// wave) and walks 64-key blocks staged in LDS (K row-major, V transposed).
+// wave) and walks 64-key blocks that move global -> LDS by DMA, three blocks in
+// flight, K and V both row-major; V^T fragments come from LDS transpose reads.
 // Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_f16,
 // so each lane owns one query column: the online-softmax max/sum need only
 // two cross-lane shuffles, and the probabilities already sit in the B-operand
@@ -39,20 +40,48 @@ struct FlashArgs {
 
 constexpr int BQ = 64, BKV = 64;
 
+// Chunk swizzle of the K and V blocks in LDS: 16-byte chunk c of key row r
+// sits at slot c ^ kv_swz(r).  Over 8 consecutive rows kv_swz takes 8
+// distinct values (K fragment reads: 16-byte reads of one chunk from 8 rows
+// per LDS cycle), and over 4 consecutive rows it differs in bits 1-2 (V
+// transpose reads: 32 bytes from each of 4 rows), so neither read conflicts.
+__device__ __forceinline__ int kv_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
+// (i % 4) of the 4 halves addressed by lane 4j + i/4, for j = 0..3.  When
+// lanes 4j..4j+3 address key row R_j at dims d0, d0+4, d0+8, d0+12, lane i
+// gets V[R_0..R_3][d0 + i]: a V^T fragment read from row-major V.
+__device__ __forceinline__ f16x4 lds_read_tr(const uint8_t* p) {
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
+    return __builtin_bit_cast(f16x4, v);
+}
+
 template <int HD, bool OUT16>
 __global__ __launch_bounds__(256) void flash_attn_kernel(FlashArgs a) {
-    constexpr int LDK = HD + 8, LDV = BKV + 8, KS = HD / 32, DT = HD / 16;
-    __shared__ __attribute__((aligned(16))) f16 Ks[BKV][LDK];
-    __shared__ __attribute__((aligned(16))) f16 Vt[HD][LDV];
+    constexpr int KS = HD / 32, DT = HD / 16;
+    constexpr int ROWB = HD * 2;          // bytes per key row
+    constexpr int CH = HD / 8;            // 16-byte chunks per row
+    constexpr int RPI = 1024 / ROWB;      // key rows per DMA instruction
+    constexpr int TILE = BKV * ROWB;      // bytes of one K (or V) block
+    constexpr int PERW = TILE / 1024 / 4; // DMA instructions per wave per block and matrix
+    constexpr int PER = 2 * PERW;
+    // Three stage buffers, each K block then V block, both row-major and swizzled.
+    __shared__ __attribute__((aligned(16))) uint8_t st0[2 * TILE], st1[2 * TILE], st2[2 * TILE];
 
     const int h = blockIdx.x;
     const int qb = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks first
     const int kvh = h / (a.H / a.KVH);
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, c16 = lane & 15;
     const int qi = qb * BQ + wave * 16 + c16;
     const int qc = qi < a.T ? qi : a.T - 1;
     const int pos_q = a.start + qc;
+    // Positions of this wave's first and last query (clamped like qc).
+    const int wpos_lo = a.start + min(qb * BQ + wave * 16, a.T - 1);
+    const int wpos_hi = a.start + min(qb * BQ + wave * 16 + 15, a.T - 1);
 
     f16x8 qf[KS];
 #pragma unroll
@@ -64,82 +93,111 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(FlashArgs a) {
     const f16* kbase = a.kc + (int64_t)kvh * a.cap * HD;
     const f16* vbase = a.vc + (int64_t)kvh * a.cap * HD;
 
+    // K and V rows of key block kb into the stage buffer at LDS address sg.
+    // Rows past kend repeat row kend-1 (in bounds; masked or never reached).
+    auto issue = [&](uint32_t sg, int kb) {
+        const int key0 = kb * BKV;
+#pragma unroll
+        for (int i = 0; i < PERW; i++) {
+            const int r0 = (i * 4 + wave) * RPI, r = r0 + lane / CH, c = (lane % CH) ^ kv_swz(r);
+            const int64_t off = (int64_t)min(key0 + r, kend - 1) * HD + c * 8;
+            dma16(kbase + off, sg + r0 * ROWB);
+            dma16(vbase + off, sg + TILE + r0 * ROWB);
+        }
+    };
+
     float m = -INFINITY, lsum = 0.f;
     f32x4 oacc[DT];
 #pragma unroll
     for (int d = 0; d < DT; d++) oacc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int kb = 0; kb < nkb; kb++) {
+    auto compute = [&](const uint8_t* sg, int kb) {
         const int key0 = kb * BKV;
-        __syncthreads();
-        for (int seg = tid; seg < BKV * HD / 8; seg += 256) {
-            const int r = seg / (HD / 8), c = (seg % (HD / 8)) * 8, key = key0 + r;
-            int4 kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
-            if (key < kend) {
-                kv = *(const int4*)(kbase + (int64_t)key * HD + c);
-                vv = *(const int4*)(vbase + (int64_t)key * HD + c);
-            }
-            *(int4*)&Ks[r][c] = kv;
-            const f16* vh = (const f16*)&vv;
-#pragma unroll
-            for (int j = 0; j < 8; j++) Vt[c + j][r] = vh[j];
-        }
-        __syncthreads();
-
+        const uint8_t* Kt = sg;
+        const uint8_t* Vt = sg + TILE;
         // S^T tiles: sacc[t][r] = score(key0 + 16t + 4g + r, query qi)
         f32x4 sacc[4];
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             sacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const int r = 16 * t + c16;
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
-                const f16x8 kf = *(const f16x8*)&Ks[16 * t + c16][32 * ks + 8 * g];
+                const f16x8 kf = *(const f16x8*)(Kt + r * ROWB + (((4 * ks + g) ^ kv_swz(r)) * 16));
                 sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], sacc[t], 0, 0, 0);
             }
         }
+        // Masking only where some key of the block lies past some query of the wave.
+        if (key0 + BKV - 1 > wpos_lo) {
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (key0 + 16 * t + 4 * g + r > pos_q) sacc[t][r] = -INFINITY;
+        }
+        // Running max in log2 units (m, mn): the scale is positive, so the max
+        // of the raw scores scales to the max of the scaled ones.
         float mx = -INFINITY;
 #pragma unroll
-        for (int t = 0; t < 4; t++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int key = key0 + 16 * t + 4 * g + r;
-                float z = sacc[t][r] * a.scale_log2;
-                if (key > pos_q || key >= kend) z = -INFINITY;
-                sacc[t][r] = z;
-                mx = fmaxf(mx, z);
-            }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        for (int t = 0; t < 4; t++) mx = fmaxf(mx, fmaxf(fmaxf(sacc[t][0], sacc[t][1]), fmaxf(sacc[t][2], sacc[t][3])));
+        mx = fmaxf(mx, swizzle_xor16(mx));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mn = fmaxf(m, mx);  // finite: key 0 is visible to every query in block 0
-        const float alpha = exp2f(m - mn);
+        const float mn = fmaxf(m, mx * a.scale_log2);  // finite: key 0 is visible to every query in block 0
+        // v_exp_f32 without the library's denormal-result path: values below
+        // 2^-126 become 0, as they do anyway once P is rounded to f16.
+        const float alpha = __builtin_amdgcn_exp2f(m - mn);
+        // The row sum takes the float32 probabilities; P enters the MFMA as f16.
         float ps = 0.f;
         f16 ph[4][4];
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const f16 pv = (f16)exp2f(sacc[t][r] - mn);
-                ph[t][r] = pv;
-                ps += (float)pv;
+                const float e = __builtin_amdgcn_exp2f(fmaf(sacc[t][r], a.scale_log2, -mn));
+                ph[t][r] = (f16)e;
+                ps += e;
             }
         lsum = lsum * alpha + ps;
 #pragma unroll
         for (int d = 0; d < DT; d++) oacc[d] *= alpha;
+        // O^T += V^T P^T.  Key order inside a 32-key step, identical on both
+        // operands: slot e < 4 is key 32s + 4g + e, slot e >= 4 is 32s + 16 + 4g + e - 4.
 #pragma unroll
         for (int s = 0; s < 2; s++) {
             const f16x8 pf = {ph[2 * s][0], ph[2 * s][1], ph[2 * s][2], ph[2 * s][3],
                               ph[2 * s + 1][0], ph[2 * s + 1][1], ph[2 * s + 1][2], ph[2 * s + 1][3]};
+            const int ra = 32 * s + 4 * g + (c16 >> 2), rb = ra + 16;
 #pragma unroll
             for (int d = 0; d < DT; d++) {
-                const f16x4 lo = *(const f16x4*)&Vt[16 * d + c16][32 * s + 4 * g];
-                const f16x4 hi = *(const f16x4*)&Vt[16 * d + c16][32 * s + 16 + 4 * g];
+                const int cb = 2 * d + ((c16 & 3) >> 1), hb = (c16 & 1) * 8;
+                const f16x4 lo = lds_read_tr(Vt + ra * ROWB + ((cb ^ kv_swz(ra)) * 16) + hb);
+                const f16x4 hi = lds_read_tr(Vt + rb * ROWB + ((cb ^ kv_swz(rb)) * 16) + hb);
                 const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 oacc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, oacc[d], 0, 0, 0);
             }
         }
         m = mn;
+    };
+
+    // Three-stage pipeline as in the prefill GEMM: wait for block kb (block
+    // kb+1 stays in flight), barrier, refill the buffer of block kb-1 with
+    // block kb+2 (past the end: the last block again, never read), multiply.
+    // A wave skips blocks whose keys all lie past its queries.
+    auto step = [&](const uint8_t* cur, uint8_t* refill, int kb) {
+        wait_stage_barrier<PER>();
+        issue(lds_addr(refill), min(kb + 2, nkb - 1));
+        if (kb * BKV <= wpos_hi) compute(cur, kb);
+    };
+    issue(lds_addr(st0), 0);
+    issue(lds_addr(st1), min(1, nkb - 1));
+    for (int kb = 0; kb < nkb; kb += 3) {
+        step(st0, st2, kb);
+        if (kb + 1 < nkb) step(st1, st0, kb + 1);
+        if (kb + 2 < nkb) step(st2, st1, kb + 2);
     }
-    lsum += __shfl_xor(lsum, 16, 64);
+    wait_stage_barrier<0>();  // no DMA may still be writing LDS when the waves end
+
+    lsum += swizzle_xor16(lsum);
     lsum += __shfl_xor(lsum, 32, 64);
     if (qi >= a.T) return;
     const float inv = 1.0f / lsum;

@@ -500,38 +500,9 @@ __device__ __forceinline__ void nib4_to_f16(uint32_t nib, uint32_t& o0, uint32_t
 
 constexpr int DBK = 64;  // K per stage
 
-// global -> LDS DMA of 16 (or 4) bytes per lane: lane l writes LDS bytes
-// [lds + size*l, lds + size*(l+1)).  Issued through asm so that the only waits on
-// these loads are the explicit ones in wait_stage_barrier (the compiler's own
-// tracking of LDS DMA falls back to waiting for every outstanding load before
-// each LDS read, which would serialise the pipeline).  The asm sets m0, which
-// nothing else in these kernels uses; one wait state separates the m0 write from
-// the load that reads it (the compiler puts the same s_nop after its own m0
-// writes for LDS DMA).
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
-}
-__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
 __device__ __forceinline__ int swz_a(int r) { return (r & 7) ^ ((r >> 1) & 4); }
 __device__ __forceinline__ int swz_q8(int r) { return (r >> 2) & 3; }
 __device__ __forceinline__ int swz_q4(int r) { return (r >> 3) & 1; }
-
-// Wait until at most N of this wave's global loads are outstanding, and for
-// its LDS reads, then barrier.  The "memory" clobber keeps LDS accesses on
-// their side of the barrier.
-template <int N>
-__device__ __forceinline__ void wait_stage_barrier() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
-}
 
 // Byte layout of one stage buffer: A rows, then each matrix's weight rows,
 // then each matrix's scales.
