@@ -102,6 +102,26 @@ __device__ __forceinline__ float dpp_mov(float v) {
 __device__ __forceinline__ float swizzle_xor16(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
 }
+// Butterflies across 16-lane rows without the LDS crossbar (gfx950):
+// v_permlane16_swap(a, b) exchanges the odd 16-lane rows of a with the even
+// rows of b, so with a = b = v the two results hold {v[l], v[l ^ 16]};
+// v_permlane32_swap likewise {v[l], v[l ^ 32]}.  The two results are copied
+// out as integers before reinterpretation (a bit cast of an element of the
+// returned vector reads element 0).  op must be commutative.
+template <typename Op>
+__device__ __forceinline__ float xor16_combine(float v, Op op) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const unsigned a = p[0], b = p[1];
+    return op(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+template <typename Op>
+__device__ __forceinline__ float xor32_combine(float v, Op op) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const unsigned a = p[0], b = p[1];
+    return op(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
 // Reduction over aligned groups of N lanes (N a power of two up to 64); every
 // lane of a group gets the result.  All lanes combine in the same tree, so the
 // result is identical across the group.

@@ -9,8 +9,9 @@
 // flash_attn_kernel (prefill, f16 cache, hd 64/128): replaces the reference's
 // tensor-op and simdgroup prefill attention (tensor_attention.metal,
 // attention_prefill.metal).  A workgroup takes 64 queries of one head (16 per
-// wave) and walks 64-key blocks that move global -> LDS by DMA, three blocks in
-// flight, K and V both row-major; V^T fragments come from LDS transpose reads.
+// wave; at head dim 64 two sets of four waves split the key range) and walks
+// 64-key blocks that move global -> LDS by DMA, three blocks in flight, K and V
+// both row-major; V^T fragments come from LDS transpose reads.
 // Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_f16,
 // so each lane owns one query column: the online-softmax max/sum need only
 // two cross-lane shuffles, and the probabilities already sit in the B-operand
@@ -58,8 +59,14 @@ __device__ __forceinline__ f16x4 lds_read_tr(const uint8_t* p) {
     return __builtin_bit_cast(f16x4, v);
 }
 
-template <int HD, bool OUT16>
-__global__ __launch_bounds__(256) void flash_attn_kernel(FlashArgs a) {
+// NSET wave-sets per workgroup.  With NSET = 2 (head dim 64) a second set of
+// four waves takes the second half of the key blocks of the same 64 queries,
+// halving the sequential walk of the longest (causal) query blocks; the halves
+// merge at the end.  It costs LDS (one workgroup per CU), so the launcher uses
+// it only when one-set workgroups would not fill the chip.
+template <int HD, int NSET, bool OUT16>
+__global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
+    static_assert(NSET == 1 || (NSET == 2 && HD == 64), "two wave-sets fit LDS at head dim 64 only");
     constexpr int KS = HD / 32, DT = HD / 16;
     constexpr int ROWB = HD * 2;          // bytes per key row
     constexpr int CH = HD / 8;            // 16-byte chunks per row
@@ -67,21 +74,27 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(FlashArgs a) {
     constexpr int TILE = BKV * ROWB;      // bytes of one K (or V) block
     constexpr int PERW = TILE / 1024 / 4; // DMA instructions per wave per block and matrix
     constexpr int PER = 2 * PERW;
-    // Three stage buffers, each K block then V block, both row-major and swizzled.
-    __shared__ __attribute__((aligned(16))) uint8_t st0[2 * TILE], st1[2 * TILE], st2[2 * TILE];
+    // Three stage buffers per set, each K block then V block, both row-major and swizzled.
+    __shared__ __attribute__((aligned(16))) uint8_t sA0[2 * TILE], sA1[2 * TILE], sA2[2 * TILE];
+    __shared__ __attribute__((aligned(16))) uint8_t sB0[NSET > 1 ? 2 * TILE : 16], sB1[NSET > 1 ? 2 * TILE : 16],
+        sB2[NSET > 1 ? 2 * TILE : 16];
 
     const int h = blockIdx.x;
     const int qb = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks first
     const int kvh = h / (a.H / a.KVH);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int set = wave / 4, wl = wave % 4;  // wave-set, and the wave's 16 queries within the block
     const int g = lane >> 4, c16 = lane & 15;
-    const int qi = qb * BQ + wave * 16 + c16;
+    const int qi = qb * BQ + wl * 16 + c16;
     const int qc = qi < a.T ? qi : a.T - 1;
     const int pos_q = a.start + qc;
     // Positions of this wave's first and last query (clamped like qc).
-    const int wpos_lo = a.start + min(qb * BQ + wave * 16, a.T - 1);
-    const int wpos_hi = a.start + min(qb * BQ + wave * 16 + 15, a.T - 1);
+    const int wpos_lo = a.start + min(qb * BQ + wl * 16, a.T - 1);
+    const int wpos_hi = a.start + min(qb * BQ + wl * 16 + 15, a.T - 1);
+    uint8_t* const st0 = set ? sB0 : sA0;
+    uint8_t* const st1 = set ? sB1 : sA1;
+    uint8_t* const st2 = set ? sB2 : sA2;
 
     f16x8 qf[KS];
 #pragma unroll
@@ -90,16 +103,21 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(FlashArgs a) {
     const int last_q = (qb + 1) * BQ < a.T ? (qb + 1) * BQ : a.T;
     const int kend = a.start + last_q;  // keys [0, kend) cover every query of this block
     const int nkb = (kend + BKV - 1) / BKV;
+    // Key blocks of this set: [first, first + count); both sets run `steps` steps.
+    const int steps = (nkb + NSET - 1) / NSET;
+    const int first = set * steps, count = max(0, min(nkb - first, steps));
     const f16* kbase = a.kc + (int64_t)kvh * a.cap * HD;
     const f16* vbase = a.vc + (int64_t)kvh * a.cap * HD;
 
-    // K and V rows of key block kb into the stage buffer at LDS address sg.
-    // Rows past kend repeat row kend-1 (in bounds; masked or never reached).
-    auto issue = [&](uint32_t sg, int kb) {
-        const int key0 = kb * BKV;
+    // K and V rows of this set's i-th key block into the stage buffer at LDS
+    // address sg.  Past the set's last block (or for a set with none) the load
+    // repeats a valid block that is never read, so every step waits on the same
+    // count; rows past kend repeat row kend-1 (in bounds; masked or unused).
+    auto issue = [&](uint32_t sg, int i) {
+        const int key0 = min(first + min(i, max(count, 1) - 1), nkb - 1) * BKV;
 #pragma unroll
-        for (int i = 0; i < PERW; i++) {
-            const int r0 = (i * 4 + wave) * RPI, r = r0 + lane / CH, c = (lane % CH) ^ kv_swz(r);
+        for (int j = 0; j < PERW; j++) {
+            const int r0 = (j * 4 + wl) * RPI, r = r0 + lane / CH, c = (lane % CH) ^ kv_swz(r);
             const int64_t off = (int64_t)min(key0 + r, kend - 1) * HD + c * 8;
             dma16(kbase + off, sg + r0 * ROWB);
             dma16(vbase + off, sg + TILE + r0 * ROWB);
@@ -110,6 +128,8 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(FlashArgs a) {
     f32x4 oacc[DT];
 #pragma unroll
     for (int d = 0; d < DT; d++) oacc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto fmax2 = [](float x, float y) { return fmaxf(x, y); };
+    auto add2 = [](float x, float y) { return x + y; };
 
     auto compute = [&](const uint8_t* sg, int kb) {
         const int key0 = kb * BKV;
@@ -140,12 +160,14 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(FlashArgs a) {
         float mx = -INFINITY;
 #pragma unroll
         for (int t = 0; t < 4; t++) mx = fmaxf(mx, fmaxf(fmaxf(sacc[t][0], sacc[t][1]), fmaxf(sacc[t][2], sacc[t][3])));
-        mx = fmaxf(mx, swizzle_xor16(mx));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mn = fmaxf(m, mx * a.scale_log2);  // finite: key 0 is visible to every query in block 0
+        mx = xor32_combine(xor16_combine(mx, fmax2), fmax2);  // the 4 lanes of this query
+        const float mn = fmaxf(m, mx * a.scale_log2);
+        // -inf while every key seen so far is masked (possible in the second
+        // set); referencing 0 then keeps alpha and P at exactly 0.
+        const float mref = mn == -INFINITY ? 0.f : mn;
         // v_exp_f32 without the library's denormal-result path: values below
         // 2^-126 become 0, as they do anyway once P is rounded to f16.
-        const float alpha = __builtin_amdgcn_exp2f(m - mn);
+        const float alpha = __builtin_amdgcn_exp2f(m - mref);
         // The row sum takes the float32 probabilities; P enters the MFMA as f16.
         float ps = 0.f;
         f16 ph[4][4];
@@ -153,7 +175,7 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(FlashArgs a) {
         for (int t = 0; t < 4; t++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const float e = __builtin_amdgcn_exp2f(fmaf(sacc[t][r], a.scale_log2, -mn));
+                const float e = __builtin_amdgcn_exp2f(fmaf(sacc[t][r], a.scale_log2, -mref));
                 ph[t][r] = (f16)e;
                 ps += e;
             }
@@ -179,26 +201,51 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(FlashArgs a) {
         m = mn;
     };
 
-    // Three-stage pipeline as in the prefill GEMM: wait for block kb (block
-    // kb+1 stays in flight), barrier, refill the buffer of block kb-1 with
-    // block kb+2 (past the end: the last block again, never read), multiply.
-    // A wave skips blocks whose keys all lie past its queries.
-    auto step = [&](const uint8_t* cur, uint8_t* refill, int kb) {
+    // Three-stage pipeline as in the prefill GEMM: wait for the step's block
+    // (the next stays in flight), barrier, refill the buffer of the previous
+    // step two blocks ahead, multiply.  A wave skips blocks whose keys all lie
+    // past its queries.
+    auto step = [&](const uint8_t* cur, uint8_t* refill, int i) {
         wait_stage_barrier<PER>();
-        issue(lds_addr(refill), min(kb + 2, nkb - 1));
-        if (kb * BKV <= wpos_hi) compute(cur, kb);
+        issue(lds_addr(refill), i + 2);
+        const int kb = first + i;
+        if (i < count && kb * BKV <= wpos_hi) compute(cur, kb);
     };
     issue(lds_addr(st0), 0);
-    issue(lds_addr(st1), min(1, nkb - 1));
-    for (int kb = 0; kb < nkb; kb += 3) {
-        step(st0, st2, kb);
-        if (kb + 1 < nkb) step(st1, st0, kb + 1);
-        if (kb + 2 < nkb) step(st2, st1, kb + 2);
+    issue(lds_addr(st1), 1);
+    for (int i = 0; i < steps; i += 3) {
+        step(st0, st2, i);
+        if (i + 1 < steps) step(st1, st0, i + 1);
+        if (i + 2 < steps) step(st2, st1, i + 2);
     }
-    wait_stage_barrier<0>();  // no DMA may still be writing LDS when the waves end
+    wait_stage_barrier<0>();  // no DMA may still be writing LDS past this point
 
-    lsum += swizzle_xor16(lsum);
-    lsum += __shfl_xor(lsum, 32, 64);
+    lsum = xor32_combine(xor16_combine(lsum, add2), add2);
+    if constexpr (NSET > 1) {
+        // The second set hands (m, lsum, O) to the first through LDS (its own
+        // stage buffers, idle now); the first merges and writes the output.
+        static_assert(4 * DT * 4 * 64 * 4 <= 2 * TILE && 4 * 2 * 64 * 4 <= 2 * TILE, "merge scratch");
+        float* xo = (float*)sB0 + wl * DT * 4 * 64;  // O: 4 KB per wave
+        float* xml = (float*)sB1 + wl * 2 * 64;      // m, lsum
+        if (set == 1) {
+#pragma unroll
+            for (int d = 0; d < DT; d++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) xo[(d * 4 + r) * 64 + lane] = oacc[d][r];
+            xml[lane] = m;
+            xml[64 + lane] = lsum;
+        }
+        __syncthreads();
+        if (set == 1) return;
+        const float m1 = xml[lane], l1 = xml[64 + lane];
+        const float mt = fmaxf(m, m1);  // finite: the first set saw key 0
+        const float a0 = __builtin_amdgcn_exp2f(m - mt), a1 = __builtin_amdgcn_exp2f(m1 - mt);
+        lsum = lsum * a0 + l1 * a1;
+#pragma unroll
+        for (int d = 0; d < DT; d++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) oacc[d][r] = oacc[d][r] * a0 + xo[(d * 4 + r) * 64 + lane] * a1;
+    }
     if (qi >= a.T) return;
     const float inv = 1.0f / lsum;
     // oacc[d][r] = O(query qi, dim 16d + 4g + r)
@@ -465,12 +512,20 @@ hipError_t launch_flash_attention(const f16* q, int ldq, const f16* kc, const f1
     a.out32 = out_f32;
     a.out16 = out_f16;
     dim3 grid(heads, (tokens + BQ - 1) / BQ);
+    // One-set workgroups (48 KB of LDS at head dim 64) run three per CU: below
+    // three per CU the causal critical path dominates and two sets win.
+    const bool two_sets = (int64_t)grid.x * grid.y < 3 * 256;
     if (hd == 64) {
-        if (out_f16) flash_attn_kernel<64, true><<<grid, 256, 0, st>>>(a);
-        else flash_attn_kernel<64, false><<<grid, 256, 0, st>>>(a);
+        if (two_sets) {
+            if (out_f16) flash_attn_kernel<64, 2, true><<<grid, 512, 0, st>>>(a);
+            else flash_attn_kernel<64, 2, false><<<grid, 512, 0, st>>>(a);
+        } else {
+            if (out_f16) flash_attn_kernel<64, 1, true><<<grid, 256, 0, st>>>(a);
+            else flash_attn_kernel<64, 1, false><<<grid, 256, 0, st>>>(a);
+        }
     } else if (hd == 128) {
-        if (out_f16) flash_attn_kernel<128, true><<<grid, 256, 0, st>>>(a);
-        else flash_attn_kernel<128, false><<<grid, 256, 0, st>>>(a);
+        if (out_f16) flash_attn_kernel<128, 1, true><<<grid, 256, 0, st>>>(a);
+        else flash_attn_kernel<128, 1, false><<<grid, 256, 0, st>>>(a);
     } else {
         return hipErrorInvalidValue;
     }
