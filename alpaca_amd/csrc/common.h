@@ -131,9 +131,45 @@ __device__ __forceinline__ float lane_reduce(float v, Op op) {
     if (N >= 4) v = op(v, dpp_mov<0x4E>(v));
     if (N >= 8) v = op(v, dpp_mov<0x141>(v));
     if (N >= 16) v = op(v, dpp_mov<0x140>(v));
-    if (N >= 32) v = op(v, swizzle_xor16(v));
-    if (N >= 64) v = op(v, __shfl_xor(v, 32, 64));
+    if (N >= 32) v = xor16_combine(v, op);
+    if (N >= 64) v = xor32_combine(v, op);
     return v;
+}
+// The value of lane l ^ 16 (XOR = 16) or l ^ 32 (XOR = 32), from one permlane
+// swap: even rows find the partner in the second result, odd rows in the first.
+template <int XOR>
+__device__ __forceinline__ unsigned xor_partner(unsigned u) {
+    static_assert(XOR == 16 || XOR == 32, "permlane swap partners");
+    const int lane = __lane_id();
+    if constexpr (XOR == 16) {
+        const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        const unsigned a = p[0], b = p[1];
+        return (lane & 16) ? a : b;
+    } else {
+        const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        const unsigned a = p[0], b = p[1];
+        return (lane & 32) ? a : b;
+    }
+}
+__device__ __forceinline__ float xor_partner16(float v) { return __builtin_bit_cast(float, xor_partner<16>(__builtin_bit_cast(unsigned, v))); }
+__device__ __forceinline__ float xor_partner32(float v) { return __builtin_bit_cast(float, xor_partner<32>(__builtin_bit_cast(unsigned, v))); }
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+// Wave-wide arg-max over (value, index): the larger value wins, ties go to the
+// lower index.  The combine is symmetric, so every lane ends with the result.
+__device__ __forceinline__ void wave_argmax(float& best, int& bi) {
+    auto take = [&](float v2, int i2) {
+        if (v2 > best || (v2 == best && i2 < bi)) {
+            best = v2;
+            bi = i2;
+        }
+    };
+    take(dpp_mov<0xB1>(best), dpp_mov_i<0xB1>(bi));
+    take(dpp_mov<0x4E>(best), dpp_mov_i<0x4E>(bi));
+    take(dpp_mov<0x141>(best), dpp_mov_i<0x141>(bi));
+    take(dpp_mov<0x140>(best), dpp_mov_i<0x140>(bi));
+    take(xor_partner16(best), (int)xor_partner<16>((unsigned)bi));
+    take(xor_partner32(best), (int)xor_partner<32>((unsigned)bi));
 }
 struct AddOp {
     __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }

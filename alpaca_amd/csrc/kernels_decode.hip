@@ -285,7 +285,10 @@ struct Rows {
         float v = 0.f;
         if (r < r1) v = s0.finish(w0, r, w0.cols, li, xs);
         v = lane_sum<LPR>(v);
-        const float partner = __shfl_xor(v, LPR, 64);
+        float partner;
+        if constexpr (LPR == 16) partner = xor_partner16(v);
+        else if constexpr (LPR == 32) partner = xor_partner32(v);
+        else partner = __shfl_xor(v, LPR, 64);
         if (r < r1 && li == 0 && (local & 1) == 0) epi2(r, v, partner);
     }
     template <typename Epi2>
@@ -578,7 +581,7 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
             for (int e = 0; e < 8; e++) {
                 float v = acc[g][e];
                 if (TPR <= 8) v += dpp_mov<0x128>(v);
-                v += swizzle_xor16(v);
+                v = xor16_combine(v, [](float x, float y) { return x + y; });
                 acc[g][e] = v;
             }
         if ((lane & (32 - TPR)) == 0) {
@@ -735,15 +738,7 @@ struct PhaseLogits {
                 bi = r;
             }
         });
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float v2 = __shfl_xor(best, o, 64);
-            const int i2 = __shfl_xor(bi, o, 64);
-            if (v2 > best || (v2 == best && i2 < bi)) {
-                best = v2;
-                bi = i2;
-            }
-        }
+        wave_argmax(best, bi);
         __syncthreads();
         if ((threadIdx.x & 63) == 0) {
             sh.scr[threadIdx.x >> 6] = best;
@@ -871,15 +866,7 @@ __global__ __launch_bounds__(kT) void decode_step_kernel(DecodeParams kp) {
             bi = i;
         }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float v2 = __shfl_xor(best, o, 64);
-        const int i2 = __shfl_xor(bi, o, 64);
-        if (v2 > best || (v2 == best && i2 < bi)) {
-            best = v2;
-            bi = i2;
-        }
-    }
+    wave_argmax(best, bi);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) {
         red[threadIdx.x >> 6] = best;
