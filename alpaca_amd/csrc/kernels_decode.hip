@@ -39,6 +39,14 @@
 // words; cache rows of earlier positions come from earlier launches, whose
 // completion makes them visible.
 //
+// A wait copies words into LDS as they arrive, thread by thread.  When the
+// destination is a buffer the previous phase read (xn, the input row of QKV
+// and of gate/up), a workgroup barrier precedes the wait, so the waves of a
+// workgroup that finish their rows first (or have none) cannot overwrite the
+// row under the waves still reading it.  A wait into xres needs none: the
+// residual epilogue reads xres[r] before it publishes word r, and the next
+// phase writes xres[r] only once word r has arrived.
+//
 // The launch parameters and the current layer's table sit in LDS, so every
 // phase reads them with ds_read rather than with dependent memory loads.
 // Every phase is inlined into the kernel (a call would save and restore the
@@ -670,6 +678,12 @@ struct PhaseResidual {
         my_rows(which ? p.rows_down : p.rows_wo, W.rows, r0, r1);
         Rows<FMT, LPR, false> rw;
         rw.prefetch(W, W, r0, r1);
+        // The wait below fills xn, which the previous phase (QKV, or gate/up)
+        // reads as its input row: a wave that finished its rows early (or had
+        // none) must not overwrite it while another wave of this workgroup is
+        // still reading.  Attention and merge items end with a barrier, but a
+        // workgroup that has none goes straight from QKV to here.
+        __syncthreads();
         if (!wait_words(in, W.cols, sh.xn, c)) return false;
         const unsigned tag = c.tag;
         const float* xres = sh.xres;

@@ -78,6 +78,38 @@ def test_persistent_decode_matches_multi_kernel_and_oracle(hip_ctx, spec):
     assert fast.length == ref.length == 37 + 12
 
 
+# C4's layer shape (hidden 960, FFN 2560, 15 query / 5 KV heads, Q4_0) with 2 layers.
+C4_SHAPE = replace(synth.C4, config=replace(synth.C4.config, layer_count=2, vocab_size=2048, context_length=512),
+                   name="c4-shape-2l")
+
+
+@pytest.mark.parametrize("wgs", [128, 200, 256, 512])
+def test_persistent_decode_row_shares_at_c4_shape(hip_ctx, wgs):
+    """Grids whose row shares make the waves of a workgroup end a phase at
+    different times: at 128 workgroups each takes 20 gate/up rows, so wave 0
+    runs a second pass alone while the other waves already wait for the down
+    input; at 256, wave 3 has no gate/up rows at all.  The next phase's wait
+    must not overwrite the LDS input row under the waves still reading it
+    (that race moved logits by up to 15% of their peak, varying run to run).
+    The persistent path is held to the multi-kernel path, step by step."""
+    spec = C4_SHAPE
+    model = HIPLlamaModel(hip_ctx, spec.config, built(spec))
+    prompt = synth.prompt_tokens(spec, 300)
+    with env(ALPACA_HIP_PERSISTENT_DECODE=0):
+        ref = model.make_session(capacity=320, gemm_precision="exact")
+    with env(ALPACA_HIP_DECODE_WGS=wgs):
+        fast = model.make_session(capacity=320, gemm_precision="exact")
+    ref.forward(prompt)
+    fast.forward(prompt)
+    worst = 0.0
+    for step in range(10):
+        tok = int(prompt[step])
+        m = metrics(fast.decode(tok), ref.decode(tok))
+        worst = max(worst, m["max_rel_peak"])
+    print(f"[metrics] {spec.name} {wgs} workgroups: worst persistent vs multi-kernel peak-rel {worst:.2e}")
+    assert worst <= 1e-4
+
+
 def test_persistent_decode_across_attention_split_boundaries(hip_ctx):
     """Contexts on both sides of every split length (64..256 positions per
     split) and of the capacity: the split-K partials and their merge must
