@@ -249,11 +249,24 @@ hipError_t launch_gemv(const DevMatrix& w, const DevMatrix* w_up, const float* x
                        float* out, int mode, hipStream_t st);
 
 // prefill GEMM (kernels_gemm.hip)
-enum { GEMM_STORE = 0, GEMM_ACC = 1, GEMM_SWIGLU = 2 };
+enum { GEMM_STORE = 0, GEMM_ACC = 1, GEMM_SWIGLU = 2, GEMM_QKV_ROPE = 3 };
 // fast: x f16 [m][k] (row stride ldx); MFMA f16 with f32 accumulate.
 //   STORE/ACC write y f32 (row stride ldy); SWIGLU writes yh f16 (row stride ldy).
 hipError_t launch_gemm_mfma(const f16* x, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up, float* y,
                             f16* yh, int ldy, int mode, hipStream_t st);
+// The stacked [q|k|v] projection of m tokens at positions pos.. with the RoPE
+// (interleaved pairs) and KV-cache append in its epilogue: q rotated to qh f16
+// [m][heads*hd], k rotated and v copied to the f16 caches [kv_heads][capacity][hd].
+// Bit for bit the result of GEMM_STORE followed by launch_rope_store.
+// hipErrorNotSupported when the pipelined GEMM cannot take the shapes.
+struct QkvRope {
+    const float2* rope = nullptr;  // (cos, sin) [positions][hd/2]
+    f16* qh = nullptr;
+    f16* kc = nullptr;
+    f16* vc = nullptr;
+    int heads = 0, kv_heads = 0, hd = 0, pos = 0, capacity = 0;
+};
+hipError_t launch_gemm_qkv_rope(const f16* x, int ldx, int m, const DevMatrix& w, const QkvRope& o, hipStream_t st);
 // exact: x f32; float32 FMA in the reference's per-block order.  SWIGLU writes y f32.
 hipError_t launch_gemm_f32(const float* x, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up, float* y,
                            int ldy, int mode, hipStream_t st);

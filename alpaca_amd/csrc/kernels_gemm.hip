@@ -25,6 +25,8 @@
 // output equals the CPU reference's float32 result.
 #include "common.h"
 
+#include <type_traits>
+
 #include <cstdlib>
 #include <cstring>
 
@@ -41,6 +43,7 @@ struct GemmArgs {
     float* y;
     f16* yh;
     int ldy;
+    QkvRope qkv;  // GEMM_QKV_ROPE only (yh = qkv.qh, ldy = heads * hd)
 };
 
 template <int FMT>
@@ -529,12 +532,162 @@ struct DGemm {
     static_assert(BM % 32 == 0 && BN % 64 == 0, "tile shape");
 };
 
+// Epilogues that read memory (GEMM_ACC reads the residual rows, GEMM_QKV_ROPE
+// the RoPE table) work in 16-row groups (i) of the lane's C fragments and load
+// group i+1 before storing group i.  The vector memory counter retires in
+// order, so a load issued after a store waits for that store too; and the
+// compiler cannot reorder y[m*ldy+n] loads over stores it cannot prove
+// disjoint.  Written per element, every element would cost a full round trip.
+// Loads of rows or columns past the edge are clamped to the last valid one and
+// their results never stored.
+
+// GEMM_ACC: y += acc.  A wave whose fragments lie inside the matrix (the
+// usual case) stores without per-element edge tests.
+template <int TM, int TN>
+__device__ __forceinline__ void acc_epilogue(const GemmArgs& p, const f32x4 (&acc)[TM][TN], int mb, int nb, int M,
+                                             int N, int lane) {
+    const bool full = mb + 16 * TM <= M && nb + 16 * TN <= N;  // wave-uniform
+    float cur[TN][4], nxt[TN][4];
+    auto load = [&](int i, float (&v)[TN][4]) {
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = min(nb + 16 * j + (lane & 15), N - 1);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = min(mb + 16 * i + 4 * (lane >> 4) + r, M - 1);
+                v[j][r] = p.y[(int64_t)m * p.ldy + n];
+            }
+        }
+    };
+    auto run = [&](auto full_c) {
+        constexpr bool FULL = decltype(full_c)::value;
+        load(0, cur);
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            if (i + 1 < TM) load(i + 1, nxt);
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int n = nb + 16 * j + (lane & 15);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int m = mb + 16 * i + 4 * (lane >> 4) + r;
+                    if (FULL || (n < N && m < M)) p.y[(int64_t)m * p.ldy + n] = cur[j][r] + acc[i][j][r];
+                }
+            }
+            if (i + 1 < TM) {
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) cur[j][r] = nxt[j][r];
+            }
+        }
+    };
+    if (full) run(std::true_type{});
+    else run(std::false_type{});
+}
+
+// GEMM_QKV_ROPE.  Columns [0, QW) are q, [QW, QW+KW) k, then v.  A 16-column
+// fragment never straddles a head (hd % 16 == 0), so its region (q, k or v),
+// head and destination are wave-uniform and each element is one select chain
+// and one store.  Interleaved RoPE pairs (columns 2i, 2i+1) sit in
+// neighbouring lanes of the C layout: each lane takes its partner's value
+// with a DPP quad swap (every lane, before any edge test).  The (cos, sin)
+// rows of the tile's positions are one contiguous block of the table; the
+// workgroup copies it into the idle stage buffers with one batch of 16-byte
+// loads and lanes read their pairs from LDS.  The rotation is evaluated
+// without contraction as own*c + partner*(odd ? s : -s): for an even lane
+// (a = own, b = partner) that is a*c + (-(b*s)) == a*c - b*s exactly, for an
+// odd lane (b = own, a = partner) b*c + a*s == a*s + b*c, so q/k are bit for
+// bit those of rope_store_kernel (CPUOps.rope, CPUOps.swift:184-212;
+// KVCache.write, KVCache.swift:44-63).  smem holds at least BM * hd/2 float2.
+template <int BM, int TM, int TN>
+__device__ __forceinline__ void qkv_rope_epilogue(const GemmArgs& p, const f32x4 (&acc)[TM][TN], uint8_t* smem,
+                                                  int m0, int mb, int nb, int M, int N, int lane) {
+#pragma clang fp contract(off)
+    const QkvRope& o = p.qkv;
+    const int hd = o.hd, half = hd / 2, QW = o.heads * hd, KW = o.kv_heads * hd;
+    {
+        const int total = min(BM, M - m0) * half / 2;  // float4 = two (cos, sin) pairs
+        const float4* src = (const float4*)(o.rope + (int64_t)(o.pos + m0) * half);
+        float4* dst = (float4*)smem;
+        for (int base = 0; base < total; base += 8 * 256) {
+            float4 v[8];  // loads clamped to the last element (valid memory), stores guarded
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = src[min(base + (int)threadIdx.x + 256 * u, total - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int k = base + threadIdx.x + 256 * u;
+                if (k < total) dst[k] = v[u];
+            }
+        }
+        __syncthreads();
+    }
+    const float2* cs_rows = (const float2*)smem;
+    const bool full = mb + 16 * TM <= M;  // wave-uniform
+    const bool odd = lane & 1;
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int g0 = __builtin_amdgcn_readfirstlane(nb + 16 * j);  // first column of the fragment
+        if (g0 >= N) break;                                           // N % 16 == 0: whole fragments
+        const int region = g0 < QW ? 0 : g0 < QW + KW ? 1 : 2;
+        const int cn0 = g0 - (region == 0 ? 0 : region == 1 ? QW : QW + KW);
+        const int h = cn0 / hd, d = cn0 - h * hd + (lane & 15);
+        // element (m, column) lives at dst + m * stride (a 32-bit offset: m < M, stride <= heads * hd)
+        f16* dst;
+        int stride;
+        if (region == 0) {
+            dst = p.yh + g0 + (lane & 15);
+            stride = p.ldy;
+        } else {
+            dst = (region == 1 ? o.kc : o.vc) + ((int64_t)h * o.capacity + o.pos) * hd + d;
+            stride = hd;
+        }
+        const float2* cs_col = cs_rows + d / 2;
+        auto run = [&](auto full_c, auto rot_c) {
+            constexpr bool FULL = decltype(full_c)::value, ROT = decltype(rot_c)::value;
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                float pv[4];
+                if constexpr (ROT) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) pv[r] = dpp_mov<0xB1>(acc[i][j][r]);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int m = mb + 16 * i + 4 * (lane >> 4) + r;
+                    float out = acc[i][j][r];
+                    if constexpr (ROT) {
+                        const float2 cs = cs_col[(m - m0) * half];
+                        const float t1 = out * cs.x, t2 = pv[r] * (odd ? cs.y : -cs.y);
+                        out = t1 + t2;
+                    }
+                    if (FULL || m < M) dst[m * stride] = (f16)out;
+                }
+            }
+        };
+        if (full) {
+            if (region != 2) run(std::true_type{}, std::true_type{});
+            else run(std::true_type{}, std::false_type{});
+        } else {
+            if (region != 2) run(std::false_type{}, std::true_type{});
+            else run(std::false_type{}, std::false_type{});
+        }
+    }
+}
+
 template <int FMT, int BM, int BN, int WM, int WN, int MODE>
 __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
     using G = DGemm<FMT, BM, BN, WM, WN, MODE>;
     using L = DStage<FMT, BM, BN, G::NB>;
     constexpr int NB = G::NB, TM = G::TM, TN = G::TN, PER = G::PER;
-    __shared__ __attribute__((aligned(16))) uint8_t st0[L::BYTES], st1[L::BYTES], st2[L::BYTES];
+    // The three stage buffers, in one array that the GEMM_QKV_ROPE epilogue
+    // reuses for the tile's RoPE rows (BM positions x up to 64 pairs of 8 bytes).
+    constexpr int kStages = 3 * L::BYTES;
+    constexpr int kSmem = MODE == GEMM_QKV_ROPE && BM * 512 > kStages ? BM * 512 : kStages;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[kSmem];
+    uint8_t* const st0 = smem;
+    uint8_t* const st1 = smem + L::BYTES;
+    uint8_t* const st2 = smem + 2 * L::BYTES;
 
     const int K = p.w.cols, N = p.w.rows, M = p.M, nb = K >> 5, spitch = stage_scale_pitch(N);
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, tiles = tiles_m * tiles_n;
@@ -683,6 +836,14 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
     }
     // No DMA may still be writing this workgroup's LDS when its waves end.
     wait_stage_barrier<0>();
+    if constexpr (MODE == GEMM_QKV_ROPE) {
+        qkv_rope_epilogue<BM, TM, TN>(p, acc[0], smem, m0, m0 + wm * WM, n0 + wn * WN, M, N, lane);
+        return;
+    }
+    if constexpr (MODE == GEMM_ACC) {
+        acc_epilogue<TM, TN>(p, acc[0], m0 + wm * WM, n0 + wn * WN, M, N, lane);
+        return;
+    }
 
     // C layout of the 16x16 MFMA: lane holds rows 4*(lane/16)+r, column lane%16.
 #pragma unroll
@@ -750,6 +911,7 @@ template <int FMT>
 hipError_t dgemm_mode(const GemmArgs& a, int mode, hipStream_t st) {
     if (mode == GEMM_STORE) return pick_dgemm<FMT, GEMM_STORE>(a, st);
     if (mode == GEMM_ACC) return pick_dgemm<FMT, GEMM_ACC>(a, st);
+    if (mode == GEMM_QKV_ROPE) return pick_dgemm<FMT, GEMM_QKV_ROPE>(a, st);
     return pick_dgemm<FMT, GEMM_SWIGLU>(a, st);
 }
 
@@ -776,6 +938,31 @@ hipError_t launch_gemm_mfma(const f16* x, int ldx, int m, const DevMatrix& w, co
     case DT_Q8_0: return dgemm_mode<DT_Q8_0>(a, mode, st);
     case DT_Q4_0: return dgemm_mode<DT_Q4_0>(a, mode, st);
     default: return dgemm_mode<DT_F16>(a, mode, st);
+    }
+}
+
+hipError_t launch_gemm_qkv_rope(const f16* x, int ldx, int m, const DevMatrix& w, const QkvRope& o, hipStream_t st) {
+    if (m <= 0) return hipSuccess;
+    const bool quant = w.dtype != DT_F16;
+    // the pipelined kernel's conditions (as in launch_gemm_mfma); RoPE pairs and
+    // 16-column lane groups must not straddle a head
+    if (w.cols % DBK || ldx % 8 || ((uintptr_t)x & 15) || (quant && !w.s2) || o.hd % 16 || o.hd > 128 || o.heads <= 0 ||
+        o.kv_heads <= 0 || w.rows != (o.heads + 2 * o.kv_heads) * o.hd || !o.rope || !o.qh || !o.kc || !o.vc)
+        return hipErrorNotSupported;
+    GemmArgs a;
+    a.x = x;
+    a.ldx = ldx;
+    a.M = m;
+    a.w = w;
+    a.u = w;
+    a.y = nullptr;
+    a.yh = o.qh;
+    a.ldy = o.heads * o.hd;
+    a.qkv = o;
+    switch (w.dtype) {
+    case DT_Q8_0: return dgemm_mode<DT_Q8_0>(a, GEMM_QKV_ROPE, st);
+    case DT_Q4_0: return dgemm_mode<DT_Q4_0>(a, GEMM_QKV_ROPE, st);
+    default: return dgemm_mode<DT_F16>(a, GEMM_QKV_ROPE, st);
     }
 }
 

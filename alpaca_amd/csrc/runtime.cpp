@@ -574,6 +574,7 @@ struct StageMark {
 struct ahip_session {
     ahip_model* m = nullptr;
     int capacity = 0, max_batch = 0, kv_f16 = 1, fast = 1;
+    int fuse_qkv_rope = 1;  // ALPACA_HIP_FUSE_QKV_ROPE at creation; 0: RoPE + KV append as their own kernel
     hipStream_t stream = nullptr;
     std::vector<std::unique_ptr<DevBuf>> kc, vc;
     DevBuf x, xn, xh, qkv, qh, ctx, ctxh, ffn, ffnh, partials, logits, tokens, chain, dpos;
@@ -908,6 +909,7 @@ extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, i
     s->max_batch = max_batch;
     s->kv_f16 = kv_precision == AHIP_KV_F16;
     s->fast = gemm_precision == AHIP_GEMM_FAST;
+    s->fuse_qkv_rope = env_int("ALPACA_HIP_FUSE_QKV_ROPE", 1) != 0;
     HIP_OR(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate");
     const SessionSizes z = session_sizes(c, capacity, max_batch, s->kv_f16);
     for (int l = 0; l < c.layer_count; l++) {
@@ -1051,10 +1053,29 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
             s->stage("rmsnorm");
             LAUNCH(launch_rmsnorm(x, L.attn_norm.as<float>(), nullptr, xh, n, H, c.rms_norm_eps, st));
             s->stage("qkv projections");
-            LAUNCH(launch_gemm_mfma(xh, H, n, L.qkv.m, nullptr, qkv, nullptr, LDQKV, GEMM_STORE, st));
-            s->stage("rope + kv store");
-            LAUNCH(launch_rope_store(qkv, LDQKV, n, c.head_count, c.kv_head_count, hd, pos, rope, 1, flash ? 0 : 1,
-                                     flash ? s->qh.as<f16>() : nullptr, kc, vc, s->kv_f16, s->capacity, st));
+            hipError_t fused = hipErrorNotSupported;
+            if (flash && s->fuse_qkv_rope) {
+                // RoPE and the KV append in the GEMM epilogue (q/k/v never reach HBM as f32)
+                QkvRope o;
+                o.rope = rope;
+                o.qh = s->qh.as<f16>();
+                o.kc = (f16*)kc;
+                o.vc = (f16*)vc;
+                o.heads = c.head_count;
+                o.kv_heads = c.kv_head_count;
+                o.hd = hd;
+                o.pos = pos;
+                o.capacity = s->capacity;
+                fused = launch_gemm_qkv_rope(xh, H, n, L.qkv.m, o, st);
+                if (fused != hipErrorNotSupported) LAUNCH(fused);
+            }
+            if (fused == hipErrorNotSupported) {
+                LAUNCH(launch_gemm_mfma(xh, H, n, L.qkv.m, nullptr, qkv, nullptr, LDQKV, GEMM_STORE, st));
+                s->stage("rope + kv store");
+                LAUNCH(launch_rope_store(qkv, LDQKV, n, c.head_count, c.kv_head_count, hd, pos, rope, 1,
+                                         flash ? 0 : 1, flash ? s->qh.as<f16>() : nullptr, kc, vc, s->kv_f16,
+                                         s->capacity, st));
+            }
             s->stage("attention");
             if (flash) {
                 LAUNCH(launch_flash_attention(s->qh.as<f16>(), QW, (const f16*)kc, (const f16*)vc, s->capacity, n,

@@ -7,6 +7,7 @@ follows ErrorMetrics (Sources/AlpacaCore/Runtime/ErrorMetrics.swift:7-36).
 import base64
 import json
 import os
+from contextlib import contextmanager
 
 import numpy as np
 
@@ -19,6 +20,22 @@ def fixture(name: str) -> dict:
         with open(os.path.join(GOLDEN, name + ".json")) as f:
             _cache[name] = json.load(f)
     return _cache[name]
+
+
+@contextmanager
+def env(**kv):
+    """Sets environment variables for the duration of a with-block (the HIP
+    library reads its ALPACA_HIP_* switches when a session is created)."""
+    old = {k: os.environ.get(k) for k in kv}
+    os.environ.update({k: str(v) for k, v in kv.items()})
+    try:
+        yield
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
 
 
 def b64(s: str) -> np.ndarray:

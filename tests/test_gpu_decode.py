@@ -12,8 +12,6 @@ relative), after an exact-mode prefill (float32 GEMMs) so that the bound
 measures the decode step; between the two GPU paths, which compute the same float32
 products in a different summation order, 1e-4 of the logit peak.
 """
-import os
-from contextlib import contextmanager
 from dataclasses import replace
 
 import numpy as np
@@ -24,24 +22,10 @@ from alpaca_amd import synth
 from alpaca_amd._lib import HIPError
 from alpaca_amd.model import HIPLlamaModel
 from alpaca_amd.tensor import F16, Q4_0
-from tests.helpers import assert_close, metrics
+from tests.helpers import assert_close, env, metrics
 from tests.test_gpu_model import built, oracle_cfg, oracle_model
 
 pytestmark = pytest.mark.gpu
-
-
-@contextmanager
-def env(**kv):
-    old = {k: os.environ.get(k) for k in kv}
-    os.environ.update({k: str(v) for k, v in kv.items()})
-    try:
-        yield
-    finally:
-        for k, v in old.items():
-            if v is None:
-                os.environ.pop(k, None)
-            else:
-                os.environ[k] = v
 
 
 SPECS = [synth.TINY, synth.with_dtype(synth.TINY, Q4_0), synth.with_dtype(synth.TINY, F16),

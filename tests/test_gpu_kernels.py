@@ -30,9 +30,11 @@ def test_elementwise(hip_ops):  # KernelTests.swift:37-43
     assert_close(hip_ops.silu_mul(a, b), orc.mul(orc.silu(a), b), 1e-5, 1e-5, "silu*mul")
 
 
-@pytest.mark.parametrize("dim", [32, 576, 1536, 2048])
+# 30 (not a multiple of 4) and 4096 (past the register-resident row) take the
+# block-per-row kernel, the rest the wave-per-row one; 9 rows leave a partial block.
+@pytest.mark.parametrize("dim", [30, 32, 576, 960, 1536, 2048, 4096])
 def test_rmsnorm(hip_ops, dim):  # KernelTests.swift:45-50
-    x, w = rand((5, dim), 3, 2), rand((dim,), 4)
+    x, w = rand((9, dim), 3, 2), rand((dim,), 4)
     assert_close(hip_ops.rms_norm(x, w, 1e-5), orc.rmsnorm(x, w, 1e-5), 1e-5, 1e-5, f"rmsnorm {dim}")
 
 
