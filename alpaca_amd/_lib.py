@@ -11,7 +11,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libalpaca_hip.so")
 
-OK, NO_DEVICE, MODULE_LOAD, MISSING_KERNEL, ALLOC, COMMAND_FAILED, UNSUPPORTED, INVALID_ARGUMENT, BUSY = range(9)
+OK, NO_DEVICE, MODULE_LOAD, MISSING_KERNEL, ALLOC, COMMAND_FAILED, UNSUPPORTED, INVALID_ARGUMENT, BUSY, GGUF = range(10)
 F32, F16, Q8_0, Q4_0 = 0, 1, 2, 3
 KV_F16, KV_F32 = 0, 1
 GEMM_EXACT, GEMM_FAST = 0, 1
@@ -19,7 +19,13 @@ GEMM_EXACT, GEMM_FAST = 0, 1
 STATUS_NAMES = {
     NO_DEVICE: "no device", MODULE_LOAD: "module load", MISSING_KERNEL: "missing kernel", ALLOC: "allocation",
     COMMAND_FAILED: "command failed", UNSUPPORTED: "unsupported", INVALID_ARGUMENT: "invalid argument", BUSY: "busy",
+    GGUF: "gguf",
 }
+# GGUFError cases (ahip_gguf_error), Sources/AlpacaModels/GGUF/GGUFError.swift:5-19.
+GGUF_KINDS = {1: "cannotOpen", 2: "invalidMagic", 3: "unsupportedVersion", 4: "bigEndianNotSupported", 5: "truncated",
+              6: "malformed", 7: "limitExceeded", 8: "unsupportedTensorType", 9: "duplicateTensor",
+              10: "missingMetadata", 11: "missingTensor", 12: "unsupportedModel", 13: "tensorOutOfRange",
+              14: "tensorsOverlap"}
 
 
 class BackendUnavailable(RuntimeError):
@@ -36,6 +42,14 @@ class HIPError(RuntimeError):
 
 class InvalidArgument(HIPError, ValueError):
     pass
+
+
+class GGUFError(HIPError):
+    """AHIP_ERR_GGUF; ``kind`` names the GGUFError case (GGUF_KINDS)."""
+
+    def __init__(self, code: int, message: str, kind: str):
+        super().__init__(code, message)
+        self.kind = kind
 
 
 class Unsupported(HIPError):
@@ -60,6 +74,16 @@ class TensorDescC(C.Structure):
                 ("data", C.c_void_p), ("bytes", C.c_int64)]
 
 
+class GGUFTensorC(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("n_dims", C.c_int32), ("dims", C.c_int64 * 4), ("type", C.c_uint32),
+                ("file_offset", C.c_int64), ("byte_count", C.c_int64), ("data", C.c_void_p)]
+
+
+class LoadReportC(C.Structure):
+    _fields_ = [("mapped_weight_bytes", C.c_int64), ("converted_weight_bytes", C.c_int64),
+                ("converted_tensors", C.c_int32), ("notes", C.c_char * 2048)]
+
+
 class StageC(C.Structure):
     _fields_ = [("label", C.c_char * 48), ("seconds", C.c_double), ("dispatches", C.c_int32)]
 
@@ -79,6 +103,24 @@ SIGNATURES = {
     "ahip_model_destroy": (i, [vp]),
     "ahip_model_weight_bytes": (i, [vp, i64p]),
     "ahip_session_byte_count": (i, [C.POINTER(LlamaConfigC), i, i, i, i64p]),
+    "ahip_gguf_last_error_kind": (i, []),
+    "ahip_gguf_open": (i, [C.c_char_p, C.POINTER(vp)]),
+    "ahip_gguf_open_memory": (i, [vp, i64, C.POINTER(vp)]),
+    "ahip_gguf_close": (i, [vp]),
+    "ahip_gguf_header": (i, [vp, C.POINTER(C.c_uint32), i64p, i64p, i64p]),
+    "ahip_gguf_meta_count": (i, [vp, C.POINTER(C.c_int)]),
+    "ahip_gguf_meta_key": (i, [vp, i, C.POINTER(C.c_char_p), C.POINTER(C.c_uint32)]),
+    "ahip_gguf_meta_int": (i, [vp, C.c_char_p, i64, i64p]),
+    "ahip_gguf_meta_uint": (i, [vp, C.c_char_p, i64, C.POINTER(C.c_uint64)]),
+    "ahip_gguf_meta_float": (i, [vp, C.c_char_p, i64, dp]),
+    "ahip_gguf_meta_bool": (i, [vp, C.c_char_p, i64, C.POINTER(C.c_int)]),
+    "ahip_gguf_meta_string": (i, [vp, C.c_char_p, i64, C.POINTER(C.c_void_p), i64p]),
+    "ahip_gguf_meta_array": (i, [vp, C.c_char_p, C.POINTER(C.c_uint32), i64p]),
+    "ahip_gguf_tensor_count": (i, [vp, C.POINTER(C.c_int)]),
+    "ahip_gguf_tensor_at": (i, [vp, i, C.POINTER(GGUFTensorC)]),
+    "ahip_gguf_find_tensor": (i, [vp, C.c_char_p, C.POINTER(C.c_int)]),
+    "ahip_gguf_llama_config": (i, [vp, C.POINTER(LlamaConfigC)]),
+    "ahip_model_load_gguf": (i, [vp, vp, i, C.POINTER(vp), C.POINTER(LlamaConfigC), C.POINTER(LoadReportC)]),
     "ahip_session_create": (i, [vp, i, i, i, i, C.POINTER(vp)]),
     "ahip_session_destroy": (i, [vp]),
     "ahip_session_forward": (i, [vp, ip, i, C.POINTER(fp)]),
@@ -153,4 +195,6 @@ def check(rc: int) -> None:
         raise Unsupported(rc, msg)
     if rc == BUSY:
         raise Busy(rc, msg)
+    if rc == GGUF:
+        raise GGUFError(rc, msg, GGUF_KINDS.get(lib().ahip_gguf_last_error_kind(), "unknown"))
     raise HIPError(rc, msg)

@@ -47,6 +47,9 @@ static int fail(int code, const std::string& msg) {
 
 extern "C" const char* ahip_last_error(void) { return g_err.c_str(); }
 
+// For the library's other host sources (gguf.cpp).
+int ahip_fail(int code, const std::string& msg) { return fail(code, msg); }
+
 extern "C" const char* ahip_version(void) {
     return "alpaca_hip gfx950 (hand-written HIP; MFMA f16 prefill, dequant GEMV decode)";
 }
@@ -419,6 +422,8 @@ static int validate_config(const ahip_llama_config* c) {
         if (k % 32 || k > 12288) return fail(AHIP_ERR_UNSUPPORTED, "input widths must be multiples of 32 up to 12288");
     return AHIP_OK;
 }
+
+int ahip_validate_config(const ahip_llama_config* c) { return validate_config(c); }
 
 extern "C" int ahip_model_create(ahip_context* ctx, const ahip_llama_config* config, const ahip_tensor_desc* tensors,
                                  int count, int prefill_weight_cache, ahip_model** out) {

@@ -32,7 +32,9 @@ typedef enum {
     AHIP_ERR_COMMAND_FAILED = 5,   /* MetalError.commandFailed */
     AHIP_ERR_UNSUPPORTED = 6,      /* MetalError.unsupported */
     AHIP_ERR_INVALID_ARGUMENT = 7, /* MetalError.invalidArgument */
-    AHIP_ERR_BUSY = 8              /* re-entrant call on a busy session (MetalLlamaModel.swift:235, :275) */
+    AHIP_ERR_BUSY = 8,             /* re-entrant call on a busy session (MetalLlamaModel.swift:235, :275) */
+    AHIP_ERR_GGUF = 9              /* GGUFError (Sources/AlpacaModels/GGUF/GGUFError.swift:5-19); the case
+                                      is ahip_gguf_last_error_kind() */
 } ahip_status;
 
 /* Element formats, Sources/AlpacaCore/Tensor/DType.swift:8-56.
@@ -115,6 +117,102 @@ int ahip_model_create(ahip_context* ctx, const ahip_llama_config* config, const 
 int ahip_model_destroy(ahip_model* model);
 /* Bytes of weights resident in HBM (MetalLlamaModel.copiedWeightBytes, :30-32). */
 int ahip_model_weight_bytes(const ahip_model* model, int64_t* bytes);
+
+/* ------------------------------------------------------------ GGUF files */
+
+/* GGUFError cases (GGUFError.swift:5-19), the kind of the last AHIP_ERR_GGUF
+ * raised on this thread. */
+typedef enum {
+    AHIP_GGUF_CANNOT_OPEN = 1,
+    AHIP_GGUF_INVALID_MAGIC = 2,
+    AHIP_GGUF_UNSUPPORTED_VERSION = 3,
+    AHIP_GGUF_BIG_ENDIAN = 4,
+    AHIP_GGUF_TRUNCATED = 5,
+    AHIP_GGUF_MALFORMED = 6,
+    AHIP_GGUF_LIMIT_EXCEEDED = 7,
+    AHIP_GGUF_UNSUPPORTED_TENSOR_TYPE = 8,
+    AHIP_GGUF_DUPLICATE_TENSOR = 9,
+    AHIP_GGUF_MISSING_METADATA = 10,
+    AHIP_GGUF_MISSING_TENSOR = 11,
+    AHIP_GGUF_UNSUPPORTED_MODEL = 12,
+    AHIP_GGUF_TENSOR_OUT_OF_RANGE = 13,
+    AHIP_GGUF_TENSORS_OVERLAP = 14
+} ahip_gguf_error;
+int ahip_gguf_last_error_kind(void);
+
+/* GGML storage type ids of a GGUF tensor (GGMLType, GGUFTypes.swift:8-12). */
+typedef enum {
+    AHIP_GGML_F32 = 0, AHIP_GGML_F16 = 1, AHIP_GGML_Q4_0 = 2, AHIP_GGML_Q4_1 = 3, AHIP_GGML_Q5_0 = 6,
+    AHIP_GGML_Q5_1 = 7, AHIP_GGML_Q8_0 = 8, AHIP_GGML_Q8_1 = 9, AHIP_GGML_Q2_K = 10, AHIP_GGML_Q3_K = 11,
+    AHIP_GGML_Q4_K = 12, AHIP_GGML_Q5_K = 13, AHIP_GGML_Q6_K = 14, AHIP_GGML_Q8_K = 15, AHIP_GGML_BF16 = 30
+} ahip_ggml_type;
+
+/* GGUFTensorInfo (GGUFTypes.swift:72-84): dims in GGUF order (dims[0] varies
+ * fastest, so a [rows][cols] matrix has dims {cols, rows}); data points into
+ * the file's mapping and stays valid until ahip_gguf_close. */
+typedef struct {
+    const char* name;
+    int32_t n_dims;
+    int64_t dims[4];
+    uint32_t type;
+    int64_t file_offset;
+    int64_t byte_count;
+    const void* data;
+} ahip_gguf_tensor;
+
+typedef struct ahip_gguf ahip_gguf;
+
+/* GGUFFile.init(url:), GGUFFile.swift:32-35 and :42-131: maps the file
+ * read-only and validates header, metadata and tensor directory without
+ * trusting any length field (limits of GGUFFile.Limits, :13-21). */
+int ahip_gguf_open(const char* path, ahip_gguf** out);
+/* GGUFFile.init(data:), :38-40: validates a private copy of `bytes` bytes. */
+int ahip_gguf_open_memory(const void* data, int64_t bytes, ahip_gguf** out);
+int ahip_gguf_close(ahip_gguf* g);
+/* version, alignment, dataOffset, fileSize (GGUFFile.swift:23-28). */
+int ahip_gguf_header(const ahip_gguf* g, uint32_t* version, int64_t* alignment, int64_t* data_offset,
+                     int64_t* file_size);
+/* Metadata (GGUFFile.metadata, GGUFValue, GGUFTypes.swift:46-70): keys in file
+ * order with their GGUF value type id (0-12).  The typed getters follow
+ * GGUFValue.asInt / asDouble / asBool / asString; `index` >= 0 reads element
+ * `index` of an array value, -1 the value itself.  A missing key or a value of
+ * another type is AHIP_GGUF_MISSING_METADATA (GGUFError.missingMetadata). */
+int ahip_gguf_meta_count(const ahip_gguf* g, int* count);
+int ahip_gguf_meta_key(const ahip_gguf* g, int i, const char** key, uint32_t* type);
+int ahip_gguf_meta_int(const ahip_gguf* g, const char* key, int64_t index, int64_t* out);
+int ahip_gguf_meta_uint(const ahip_gguf* g, const char* key, int64_t index, uint64_t* out);
+int ahip_gguf_meta_float(const ahip_gguf* g, const char* key, int64_t index, double* out);
+int ahip_gguf_meta_bool(const ahip_gguf* g, const char* key, int64_t index, int* out);
+int ahip_gguf_meta_string(const ahip_gguf* g, const char* key, int64_t index, const char** data, int64_t* length);
+int ahip_gguf_meta_array(const ahip_gguf* g, const char* key, uint32_t* elem_type, int64_t* count);
+/* GGUFFile.tensors / info(for:) / rawBytes(of:), GGUFFile.swift:176-198. */
+int ahip_gguf_tensor_count(const ahip_gguf* g, int* count);
+int ahip_gguf_tensor_at(const ahip_gguf* g, int i, ahip_gguf_tensor* out);
+int ahip_gguf_find_tensor(const ahip_gguf* g, const char* name, int* index);
+
+/* LoadReport, Sources/AlpacaModels/Llama/LlamaLoader.swift:8-16. */
+typedef struct {
+    int64_t mapped_weight_bytes;    /* used in their on-disk format (F32, F16, Q8_0, Q4_0) */
+    int64_t converted_weight_bytes; /* expanded at load (Q4_1 -> F16) */
+    int32_t converted_tensors;
+    char notes[2048];               /* one line per converted tensor, truncated to fit */
+} ahip_load_report;
+
+/* LlamaLoader.load, configuration half (LlamaLoader.swift:36-72):
+ * general.architecture must be "llama"; llama.* keys as the reference reads
+ * them, with its defaults (head_dim = hidden / heads, kv heads = heads,
+ * eps 1e-5, theta 10000) and its refusals (value_length != key_length,
+ * partial rotary, RoPE scaling, experts); vocabulary from token_embd.weight;
+ * RoPE pairs interleaved.  The result is also checked as ahip_model_create
+ * would. */
+int ahip_gguf_llama_config(const ahip_gguf* g, ahip_llama_config* out);
+/* LlamaLoader.load, weights half (:74-104), then ahip_model_create: the
+ * blk.N.* / token_embd / output_norm / output (absent = tied) tensors go to
+ * HBM from the mapping; norms must be F32; Q4_1 tensors are expanded to F16
+ * (value = f16(d*q + m), :106-125) and reported; any other type is
+ * AHIP_GGUF_UNSUPPORTED_TENSOR_TYPE.  `config_out` and `report` may be null. */
+int ahip_model_load_gguf(ahip_context* ctx, const ahip_gguf* g, int prefill_weight_cache, ahip_model** out,
+                         ahip_llama_config* config_out, ahip_load_report* report);
 
 /* MetalLlamaModel.sessionByteCount, MetalLlamaModel.swift:123-127. */
 int ahip_session_byte_count(const ahip_llama_config* config, int capacity, int max_batch, int kv_precision,
