@@ -102,6 +102,7 @@ SIGNATURES = {
     "ahip_model_create": (i, [vp, C.POINTER(LlamaConfigC), C.POINTER(TensorDescC), i, i, C.POINTER(vp)]),
     "ahip_model_destroy": (i, [vp]),
     "ahip_model_weight_bytes": (i, [vp, i64p]),
+    "ahip_model_prefill_cache_bytes": (i, [vp, i64p]),
     "ahip_session_byte_count": (i, [C.POINTER(LlamaConfigC), i, i, i, i64p]),
     "ahip_gguf_last_error_kind": (i, []),
     "ahip_gguf_open": (i, [C.c_char_p, C.POINTER(vp)]),

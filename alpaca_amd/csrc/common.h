@@ -208,6 +208,8 @@ hipError_t launch_rmsnorm(const float* x, const float* w, float* out_f32, f16* o
                           float eps, hipStream_t st);
 hipError_t launch_embed(const int32_t* tokens, int count, const DevMatrix& table, float* out, hipStream_t st);
 hipError_t launch_dequant(const DevMatrix& m, float* out, hipStream_t st);
+// f16 copy of a matrix (the prefill weight cache): f16(d*q) per weight, cols % 8 == 0.
+hipError_t launch_dequant_f16(const DevMatrix& m, f16* out, hipStream_t st);
 // Greedy arg-max.  Writes the token to *chain_token and emitted[slot] (slot =
 // *pos_dev when pos_dev is set, which is then advanced by one).
 hipError_t launch_argmax(const float* logits, int n, int32_t* chain_token, int32_t* emitted, int slot,

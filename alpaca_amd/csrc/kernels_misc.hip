@@ -121,6 +121,22 @@ __global__ void dequant_kernel(DevMatrix m, float* out) {
         out[i] = load_elem(m, i / m.cols, (int)(i % m.cols));
 }
 
+// Half copy of a quantised matrix for the prefill weight cache: each weight
+// d*q (exact in float32) rounded once to f16 (MetalLlamaModel.buildPrefillCache,
+// MetalLlamaModel.swift:97-120).  One thread per 8 consecutive weights of a row.
+__global__ void dequant_f16_kernel(DevMatrix m, f16* out) {
+    const int64_t groups = (int64_t)m.rows * (m.cols / 8);
+    for (int64_t g = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; g < groups; g += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = g / (m.cols / 8);
+        const int k0 = (int)(g % (m.cols / 8)) * 8;
+        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+        h8 v;
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = (f16)load_elem(m, r, k0 + e);
+        *(h8*)(out + r * m.cols + k0) = v;
+    }
+}
+
 // Greedy arg-max: largest logit, lowest index on ties, NaN never wins
 // (Sampler.argmax, Sampler.swift:100-108; all-NaN input yields 0).  Writes the
 // next input token and emitted[slot].  One block of 1024 threads.
@@ -246,6 +262,13 @@ hipError_t launch_dequant(const DevMatrix& m, float* out, hipStream_t st) {
     if (n > 0) dequant_kernel<<<grid_for(n), kBlock, 0, st>>>(m, out);
     return hipGetLastError();
 }
+hipError_t launch_dequant_f16(const DevMatrix& m, f16* out, hipStream_t st) {
+    if (m.cols % 8) return hipErrorInvalidValue;
+    const int64_t groups = (int64_t)m.rows * (m.cols / 8);
+    if (groups > 0) dequant_f16_kernel<<<grid_for(groups), kBlock, 0, st>>>(m, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_argmax(const float* logits, int n, int32_t* chain, int32_t* emitted, int slot, int* pos_dev,
                          hipStream_t st) {
     argmax_kernel<<<1, 1024, 0, st>>>(logits, n, chain, emitted, slot, pos_dev);

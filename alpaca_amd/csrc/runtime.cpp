@@ -368,6 +368,23 @@ static int upload_matrix(int dt, const std::vector<std::pair<const void*, int64_
     return AHIP_OK;
 }
 
+// The prefill weight cache's f16 copy of a quantised matrix
+// (MetalLlamaModel.buildPrefillCache, MetalLlamaModel.swift:97-120); an F16
+// matrix needs none and gets an empty copy.
+static int half_copy(const OwnedMatrix& w, OwnedMatrix& h, hipStream_t st) {
+    if (w.m.dtype == AHIP_F16) return AHIP_OK;
+    const int64_t bytes = (int64_t)w.m.rows * w.m.cols * 2;
+    if (int rc = h.q.alloc(bytes)) return rc;
+    LAUNCH(launch_dequant_f16(w.m, h.q.as<f16>(), st));
+    h.m = DevMatrix{};
+    h.m.dtype = AHIP_F16;
+    h.m.rows = w.m.rows;
+    h.m.cols = w.m.cols;
+    h.m.q = h.q.as<uint8_t>();
+    h.bytes = bytes;
+    return AHIP_OK;
+}
+
 // RoPE (cos, sin) for positions [0, positions): frequencies and angles in
 // double, rounded once to float (CPUOps.rope, CPUOps.swift:196-201).
 static std::vector<float2> rope_table(int positions, int hd, float theta) {
@@ -392,12 +409,17 @@ struct ahip_model {
     struct Layer {
         DevBuf attn_norm, ffn_norm;
         OwnedMatrix qkv, wo, gate, up, down;
+        // prefill weight cache: f16 copies of the quantised projections (else empty)
+        OwnedMatrix qkv16, wo16, gate16, up16, down16;
+        // the matrices the fast (f16 MFMA) prefill multiplies by
+        const DevMatrix& pre(const OwnedMatrix& w, const OwnedMatrix& h) const { return h.m.q ? h.m : w.m; }
     };
     std::vector<std::unique_ptr<Layer>> layers;
     OwnedMatrix embed, output;
     bool tied = false;
     DevBuf output_norm, rope;
     int64_t weight_bytes = 0;
+    int64_t prefill_cache_bytes = 0;
     const DevMatrix& out_matrix() const { return tied ? embed.m : output.m; }
 };
 
@@ -427,7 +449,6 @@ int ahip_validate_config(const ahip_llama_config* c) { return validate_config(c)
 
 extern "C" int ahip_model_create(ahip_context* ctx, const ahip_llama_config* config, const ahip_tensor_desc* tensors,
                                  int count, int prefill_weight_cache, ahip_model** out) {
-    (void)prefill_weight_cache;
     if (!ctx || !out || (count && !tensors)) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
     if (int rc = validate_config(config)) return rc;
     const ahip_llama_config& c = *config;
@@ -517,6 +538,13 @@ extern "C" int ahip_model_create(ahip_context* ctx, const ahip_llama_config* con
         m->weight_bytes += L->qkv.bytes + L->wo.bytes + L->gate.bytes + L->up.bytes + L->down.bytes;
         m->layers.push_back(std::move(L));
     }
+    if (prefill_weight_cache)
+        for (auto& L : m->layers)
+            for (auto [w, h] : {std::pair{&L->qkv, &L->qkv16}, {&L->wo, &L->wo16}, {&L->gate, &L->gate16},
+                                {&L->up, &L->up16}, {&L->down, &L->down16}}) {
+                if (int rc = half_copy(*w, *h, st)) return rc;
+                m->prefill_cache_bytes += h->bytes;
+            }
     auto table = rope_table(c.context_length, c.head_dim, c.rope_theta);
     if (int rc = m->rope.alloc(table.size() * sizeof(float2))) return rc;
     HIP_OR(hipMemcpy(m->rope.p, table.data(), table.size() * sizeof(float2), hipMemcpyHostToDevice), "upload rope table");
@@ -535,6 +563,12 @@ extern "C" int ahip_model_destroy(ahip_model* m) {
 extern "C" int ahip_model_weight_bytes(const ahip_model* m, int64_t* bytes) {
     if (!m || !bytes) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
     *bytes = m->weight_bytes;
+    return AHIP_OK;
+}
+
+extern "C" int ahip_model_prefill_cache_bytes(const ahip_model* m, int64_t* bytes) {
+    if (!m || !bytes) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
+    *bytes = m->prefill_cache_bytes;
     return AHIP_OK;
 }
 
@@ -1071,11 +1105,11 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
                 o.hd = hd;
                 o.pos = pos;
                 o.capacity = s->capacity;
-                fused = launch_gemm_qkv_rope(xh, H, n, L.qkv.m, o, st);
+                fused = launch_gemm_qkv_rope(xh, H, n, L.pre(L.qkv, L.qkv16), o, st);
                 if (fused != hipErrorNotSupported) LAUNCH(fused);
             }
             if (fused == hipErrorNotSupported) {
-                LAUNCH(launch_gemm_mfma(xh, H, n, L.qkv.m, nullptr, qkv, nullptr, LDQKV, GEMM_STORE, st));
+                LAUNCH(launch_gemm_mfma(xh, H, n, L.pre(L.qkv, L.qkv16), nullptr, qkv, nullptr, LDQKV, GEMM_STORE, st));
                 s->stage("rope + kv store");
                 LAUNCH(launch_rope_store(qkv, LDQKV, n, c.head_count, c.kv_head_count, hd, pos, rope, 1,
                                          flash ? 0 : 1, flash ? s->qh.as<f16>() : nullptr, kc, vc, s->kv_f16,
@@ -1091,13 +1125,15 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
                 LAUNCH(launch_f32_to_f16(s->ctx.as<float>(), s->ctxh.as<f16>(), (int64_t)n * QW, st));
             }
             s->stage("attn out projection (+residual)");
-            LAUNCH(launch_gemm_mfma(s->ctxh.as<f16>(), QW, n, L.wo.m, nullptr, x, nullptr, H, GEMM_ACC, st));
+            LAUNCH(launch_gemm_mfma(s->ctxh.as<f16>(), QW, n, L.pre(L.wo, L.wo16), nullptr, x, nullptr, H, GEMM_ACC, st));
             s->stage("rmsnorm");
             LAUNCH(launch_rmsnorm(x, L.ffn_norm.as<float>(), nullptr, xh, n, H, c.rms_norm_eps, st));
             s->stage("ffn gate+up+silu");
-            LAUNCH(launch_gemm_mfma(xh, H, n, L.gate.m, &L.up.m, nullptr, s->ffnh.as<f16>(), F, GEMM_SWIGLU, st));
+            LAUNCH(launch_gemm_mfma(xh, H, n, L.pre(L.gate, L.gate16), &L.pre(L.up, L.up16), nullptr, s->ffnh.as<f16>(),
+                                    F, GEMM_SWIGLU, st));
             s->stage("ffn down (+residual)");
-            LAUNCH(launch_gemm_mfma(s->ffnh.as<f16>(), F, n, L.down.m, nullptr, x, nullptr, H, GEMM_ACC, st));
+            LAUNCH(launch_gemm_mfma(s->ffnh.as<f16>(), F, n, L.pre(L.down, L.down16), nullptr, x, nullptr, H, GEMM_ACC,
+                                    st));
         } else {
             float* xn = s->xn.as<float>();
             s->stage("rmsnorm");

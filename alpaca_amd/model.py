@@ -102,6 +102,13 @@ class HIPLlamaModel:
         L.check(L.lib().ahip_model_weight_bytes(self.handle, C.byref(v)))
         return v.value
 
+    @property
+    def prefill_cache_bytes(self) -> int:
+        """Bytes of the f16 prefill weight copies (MetalLlamaModel.prefillCacheBytes)."""
+        v = C.c_int64()
+        L.check(L.lib().ahip_model_prefill_cache_bytes(self.handle, C.byref(v)))
+        return v.value
+
     @staticmethod
     def session_byte_count(config: LlamaConfig, capacity: int, max_batch: int, kv_precision: str = "f16") -> int:
         v = C.c_int64()

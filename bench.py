@@ -22,6 +22,10 @@ embeddings), random-init synthetic weights, all resident in HBM.
   * roofline_prefill: the dominant prefill GEMM (MFMA, f16 operands, f32
     accumulate): algorithmic FLOPs per launch / mean launch time from the
     session's per-stage HIP events; peak 2.5 PFLOP/s dense fp16.
+  * prefill_weight_cache: the same prefill on a model created with the
+    prefill weight cache (MetalLlamaModel.buildPrefillCache, f16 copies of the
+    layer projections, as `--prefill-cache` in the reference CLI): tok/s and
+    the gate+up GEMM's rate.  Reported beside prefill_tok_s, not instead of it.
   * cpu_baseline: the C oracle (restatement of AlpacaCore's CPU path) on the
     host cores: decode steps at context 2048 (the oracle's cache is filled
     with synthetic rows, since prefilling 2048 positions on the CPU would take
@@ -144,6 +148,7 @@ def main() -> int:
     ap.add_argument("--prefill-runs", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--no-weight-cache", action="store_true", help="skip the prefill-weight-cache measurement")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the timed decode steps (for counter passes of the decode kernel)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -261,6 +266,34 @@ def main() -> int:
         roof_p["all_prefill_gemms_frac"] = round(gemm_f / gemm_s / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
         log(f"prefill dominant GEMM: {domp} {ach:.1f} TFLOP/s")
 
+    # ---------------------------------------------------------------- prefill with the weight cache
+    wcache = None
+    if not args.no_weight_cache:
+        cm = HIPLlamaModel(ctx, c, weights, prefill_weight_cache=True)
+        cp = cm.make_session(capacity=PREFILL_TOKENS, max_batch=PREFILL_TOKENS)
+        cp.forward(prompt)
+        cp.reset()
+        cw = []
+        for _ in range(max(1, args.prefill_runs)):
+            t0 = time.perf_counter()
+            cp.forward(prompt)
+            cw.append(time.perf_counter() - t0)
+            cp.reset()
+        wcache = {"prefill_tok_s": round(PREFILL_TOKENS / float(np.median(cw)), 1),
+                  "cache_bytes": cm.prefill_cache_bytes}
+        if not args.no_profile:
+            cp.profiling_enabled = True
+            cp.forward(prompt)
+            pr = cp.last_profile
+            cp.reset()
+            k = "ffn gate+up+silu"
+            if k in pr:
+                avg = pr[k].seconds / pr[k].dispatches
+                wcache["gate_up_TFLOPs"] = round(prefill_stage_flops(c, PREFILL_TOKENS)[k] / avg / 1e12, 2)
+        log(f"prefill 4096 with the weight cache: {wcache['prefill_tok_s']:.0f} tok/s")
+        cp.close()
+        cm.close()
+
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
     if not args.no_cpu_baseline:
@@ -280,6 +313,7 @@ def main() -> int:
                    "kv_cache": "f16", "prefill_precision": "fast (f16 MFMA, f32 accumulate)",
                    "greedy_depth": args.depth},
         "prefill_tok_s": round(prefill_tok_s, 1),
+        "prefill_weight_cache": wcache,
         "decode_ms_per_token": round(el / args.steps * 1e3, 4),
         "roofline": roof, "roofline_prefill": roof_p, "cpu_baseline": cpu,
         "stages_decode_per_token": stages_d, "stages_prefill": stages_p,

@@ -110,13 +110,20 @@ int ahip_context_destroy(ahip_context* ctx);
  * prefillWeightCache:), MetalLlamaModel.swift:38-94.  Validates the config
  * and every tensor shape (LlamaConfig.validate, LlamaWeights.validate), then
  * copies all tensors to HBM once, repacking Q8_0/Q4_0 blocks into separate
- * quant and scale streams.  `prefill_weight_cache` is accepted for interface
- * parity; the MFMA GEMM dequantises blocks in LDS, so no f16 copy is kept. */
+ * quant and scale streams.  `prefill_weight_cache` also keeps f16 copies of the
+ * layer projections for the fast prefill (ahip_model_prefill_cache_bytes). */
 int ahip_model_create(ahip_context* ctx, const ahip_llama_config* config, const ahip_tensor_desc* tensors,
                       int count, int prefill_weight_cache, ahip_model** out);
 int ahip_model_destroy(ahip_model* model);
 /* Bytes of weights resident in HBM (MetalLlamaModel.copiedWeightBytes, :30-32). */
 int ahip_model_weight_bytes(const ahip_model* model, int64_t* bytes);
+/* Bytes of the prefill weight cache (MetalLlamaModel.prefillCacheBytes, :23-24):
+ * with prefill_weight_cache set, every quantised layer projection also gets an
+ * f16 copy (each weight d*q rounded once to f16, buildPrefillCache :97-120)
+ * that the fast prefill GEMMs multiply by instead of dequantising blocks;
+ * decode and the exact prefill keep using the quantised weights.  0 when not
+ * requested or when the layers are already F16. */
+int ahip_model_prefill_cache_bytes(const ahip_model* model, int64_t* bytes);
 
 /* ------------------------------------------------------------ GGUF files */
 

@@ -6,6 +6,11 @@ the same float32 accumulators, so a fused session and an unfused one
 the prefill logits (which read q through attention) and the decode steps after
 it (which read the cached k/v rows), across two chunks so the second starts at
 a non-zero position.
+
+The prefill weight cache (MetalLlamaModel.buildPrefillCache, MetalLlamaModel.
+swift:97-120): a model created with it prefills exactly as a model whose layer
+projections are f16(d*q), and its exact prefill and decode are those of the
+model without the cache.
 """
 from dataclasses import replace
 
@@ -45,3 +50,51 @@ def test_fused_qkv_rope_is_bit_identical_to_unfused(hip_ctx, spec):
         a, b = fused.decode(tok), ref.decode(tok)
         assert np.array_equal(a, b), f"decode step {step} differs: max |d| {np.abs(a - b).max():.3e}"
         tok = int(np.argmax(a))
+
+
+# ------------------------------------------------------------------ prefill weight cache
+
+LAYER_MATS = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
+
+
+def half_layers(weights: dict) -> dict:
+    """The weights with every layer projection replaced by f16(d*q) (numpy)."""
+    import oracle.oracle as orc
+    from alpaca_amd.tensor import QTensor
+
+    out = dict(weights)
+    for name, t in weights.items():
+        if name.split(".")[-1] in LAYER_MATS:
+            v = orc.dequantize(t.dtype, t.data, t.rows * t.cols).astype(np.float16)
+            out[name] = QTensor(F16, t.rows, t.cols, v)
+    return out
+
+
+@pytest.mark.parametrize("spec", [synth.TINY, synth.with_dtype(synth.TINY, Q4_0)], ids=lambda s: s.name)
+def test_prefill_weight_cache_is_the_f16_model(hip_ctx, spec):
+    """A model built with the prefill weight cache prefills (fast path) exactly as a
+    model whose layer projections are the numpy f16 values of d*q: the cache holds
+    f16(d*q) and the fast GEMMs read it.  Decode and the exact prefill do not use it."""
+    w = built(spec)
+    c = spec.config
+    cached = HIPLlamaModel(hip_ctx, c, w, prefill_weight_cache=True)
+    plain = HIPLlamaModel(hip_ctx, c, w)
+    ref = HIPLlamaModel(hip_ctx, c, half_layers(w))
+    per_layer = sum(w[f"blk.0.{m}"].rows * w[f"blk.0.{m}"].cols for m in LAYER_MATS)
+    assert cached.prefill_cache_bytes == 2 * per_layer * c.layer_count and plain.prefill_cache_bytes == 0
+    prompt = synth.prompt_tokens(spec, 100)
+    a = cached.make_session(capacity=160, gemm_precision="fast").forward(prompt)
+    b = ref.make_session(capacity=160, gemm_precision="fast").forward(prompt)
+    assert np.array_equal(a, b)
+    # exact prefill and decode read the quantised weights
+    s1, s2 = cached.make_session(capacity=160, gemm_precision="exact"), plain.make_session(capacity=160,
+                                                                                          gemm_precision="exact")
+    assert np.array_equal(s1.forward(prompt), s2.forward(prompt))
+    for tok in (3, 17):
+        assert np.array_equal(s1.decode(tok), s2.decode(tok))
+
+
+def test_prefill_weight_cache_skips_f16_layers(hip_ctx):
+    spec = synth.with_dtype(synth.TINY, F16)
+    m = HIPLlamaModel(hip_ctx, spec.config, built(spec), prefill_weight_cache=True)
+    assert m.prefill_cache_bytes == 0
