@@ -212,6 +212,10 @@ hipError_t launch_dequant(const DevMatrix& m, float* out, hipStream_t st);
 hipError_t launch_dequant_f16(const DevMatrix& m, f16* out, hipStream_t st);
 // Greedy arg-max.  Writes the token to *chain_token and emitted[slot] (slot =
 // *pos_dev when pos_dev is set, which is then advanced by one).
+// Sampler.sample for a draw u (kernels_sample.hip): one workgroup; out[0] the
+// token, out[1] 1 when the logits hold a NaN; cand_idx / cand_p scratch of n.
+hipError_t launch_sample(const float* logits, int n, float temperature, int top_k, float top_p, double u,
+                         int32_t* out, int* status, uint32_t* cand_idx, double* cand_p, hipStream_t st);
 hipError_t launch_argmax(const float* logits, int n, int32_t* chain_token, int32_t* emitted, int slot,
                          int* pos_dev, hipStream_t st);
 // RoPE with a host-built (cos, sin) table [positions][hd/2]; q rotated in

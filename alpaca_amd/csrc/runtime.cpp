@@ -614,6 +614,8 @@ struct ahip_session {
     ahip_model* m = nullptr;
     int capacity = 0, max_batch = 0, kv_f16 = 1, fast = 1;
     int fuse_qkv_rope = 1;  // ALPACA_HIP_FUSE_QKV_ROPE at creation; 0: RoPE + KV append as their own kernel
+    bool logits_ready = false;  // `logits` holds the last forward's logits (for ahip_session_sample)
+    DevBuf sample_idx, sample_p, sample_out;  // sampler scratch, allocated on first use
     hipStream_t stream = nullptr;
     std::vector<std::unique_ptr<DevBuf>> kc, vc;
     DevBuf x, xn, xh, qkv, qh, ctx, ctxh, ffn, ffnh, partials, logits, tokens, chain, dpos;
@@ -1225,6 +1227,7 @@ extern "C" int ahip_session_forward(ahip_session* s, const int32_t* tokens, int 
         s->collect_profile();
     }
     s->length += n;
+    s->logits_ready = true;
     *logits = s->logits_host;
     return AHIP_OK;
 }
@@ -1281,6 +1284,7 @@ extern "C" int ahip_session_decode_greedy(ahip_session* s, int32_t start, int ma
     BusyGuard guard(s);
     if (!guard.ok) return fail(AHIP_ERR_BUSY, "session is already executing a forward pass");
     *fed_out = 0;
+    s->logits_ready = false;  // the chain does not keep its steps' logits
     if (start < 0 || start >= s->m->c.vocab_size)
         return fail(AHIP_ERR_INVALID_ARGUMENT, "token id outside vocabulary of " + std::to_string(s->m->c.vocab_size));
     const int budget = std::min(max_steps, s->capacity - s->length);
@@ -1360,7 +1364,51 @@ extern "C" int ahip_session_reset(ahip_session* s) {
     BusyGuard guard(s);
     if (!guard.ok) return fail(AHIP_ERR_BUSY, "session is busy");
     s->length = 0;
+    s->logits_ready = false;
     return AHIP_OK;
+}
+
+// ------------------------------------------------------------------ sampling
+
+// SamplingParameters.validate (Sampler.swift:21-25) and the draw's range.
+static int check_sampling(float temperature, int top_k, float top_p, double u) {
+    if (!std::isfinite(temperature) || temperature < 0)
+        return fail(AHIP_ERR_INVALID_ARGUMENT, "temperature must be finite and >= 0");
+    if (top_k < 0) return fail(AHIP_ERR_INVALID_ARGUMENT, "topK must be >= 0");
+    if (!(top_p > 0 && top_p <= 1)) return fail(AHIP_ERR_INVALID_ARGUMENT, "topP must be in (0, 1]");
+    if (!(u >= 0 && u < 1)) return fail(AHIP_ERR_INVALID_ARGUMENT, "the draw u must be in [0, 1)");
+    return AHIP_OK;
+}
+
+// One sample_kernel launch over device logits; the token comes back through a small copy.
+static int run_sample(const float* dlogits, int n, float temperature, int top_k, float top_p, double u,
+                      DevBuf& idx, DevBuf& prob, DevBuf& out, hipStream_t st, int32_t* token) {
+    if (!idx.p)
+        if (int rc = idx.alloc((size_t)n * 4)) return rc;
+    if (!prob.p)
+        if (int rc = prob.alloc((size_t)n * 8)) return rc;
+    if (!out.p)
+        if (int rc = out.alloc(8)) return rc;
+    LAUNCH(launch_sample(dlogits, n, temperature, top_k, top_p, u, out.as<int32_t>(), out.as<int>() + 1,
+                         idx.as<uint32_t>(), prob.as<double>(), st));
+    int32_t host[2] = {0, 0};
+    HIP_OR(hipMemcpyAsync(host, out.p, 8, hipMemcpyDeviceToHost, st), "sample download");
+    HIP_OR(hipStreamSynchronize(st), "sample");
+    if (host[1] == 1) return fail(AHIP_ERR_INVALID_ARGUMENT, "logits contain NaN");
+    *token = host[0];
+    return AHIP_OK;
+}
+
+extern "C" int ahip_session_sample(ahip_session* s, float temperature, int top_k, float top_p, double u,
+                                   int32_t* token) {
+    if (!s || !token) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
+    if (int rc = check_sampling(temperature, top_k, top_p, u)) return rc;
+    BusyGuard guard(s);
+    if (!guard.ok) return fail(AHIP_ERR_BUSY, "session is already executing a forward pass");
+    if (!s->logits_ready) return fail(AHIP_ERR_INVALID_ARGUMENT, "no logits to sample: call forward or decode first");
+    HIP_OR(hipSetDevice(s->m->device), "hipSetDevice");
+    return run_sample(s->logits.as<float>(), s->m->c.vocab_size, temperature, top_k, top_p, u, s->sample_idx,
+                      s->sample_p, s->sample_out, s->stream, token);
 }
 extern "C" int ahip_session_length(const ahip_session* s, int* v) {
     if (!s || !v) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
@@ -1661,6 +1709,17 @@ extern "C" int ahip_op_dequantize(ahip_context* ctx, int dtype, const void* src,
         if (int rc = dout.alloc(elements * 4)) return rc;
         LAUNCH(launch_dequant(M.m, dout.as<float>(), st));
         return download(out, dout, elements * 4, st);
+    });
+}
+
+extern "C" int ahip_op_sample(ahip_context* ctx, const float* logits, int n, float temperature, int top_k,
+                              float top_p, double u, int32_t* token) {
+    if (n <= 0 || !logits || !token) return fail(AHIP_ERR_INVALID_ARGUMENT, "cannot sample from empty logits");
+    if (int rc = check_sampling(temperature, top_k, top_p, u)) return rc;
+    return with_ctx(ctx, [&](hipStream_t st) -> int {
+        DevBuf dl, idx, prob, out;
+        if (int rc = upload(dl, logits, (size_t)n * 4, st)) return rc;
+        return run_sample(dl.as<float>(), n, temperature, top_k, top_p, u, idx, prob, out, st, token);
     });
 }
 

@@ -185,6 +185,12 @@ class HIPLlamaSession:
         L.check(rc)
         return fed.value
 
+    def sample(self, temperature: float, top_k: int = 0, top_p: float = 1.0, u: float = 0.0) -> int:
+        """Samples the last forward/decode logits on the device (ahip_session_sample)."""
+        r = C.c_int32()
+        L.check(L.lib().ahip_session_sample(self.handle, temperature, top_k, top_p, u, C.byref(r)))
+        return r.value
+
     def reset(self) -> None:
         L.check(L.lib().ahip_session_reset(self.handle))
         self.gpu_seconds = 0.0

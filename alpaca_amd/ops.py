@@ -122,6 +122,13 @@ class HIPOps:
         L.check(L.lib().ahip_op_dequantize(self.h, t.dtype, t.data.ctypes.data, t.rows * t.cols, _fp(out)))
         return out
 
+    def sample(self, logits, temperature: float, top_k: int, top_p: float, u: float) -> int:
+        """Sampler.sample (Sampler.swift:57-93) on the device for a draw u in [0, 1)."""
+        v = _f32(logits).ravel()
+        r = C.c_int32()
+        L.check(L.lib().ahip_op_sample(self.h, _fp(v), v.size, temperature, top_k, top_p, u, C.byref(r)))
+        return r.value
+
     def argmax(self, logits) -> int:
         v = _f32(logits).ravel()
         r = C.c_int32()

@@ -259,6 +259,16 @@ int ahip_session_decode_greedy(ahip_session* s, int32_t start, int max_steps, in
 
 /* MetalLlamaSession.reset / length / capacity / lastGPUSeconds /
  * lastEncodeSeconds (MetalLlamaModel.swift:151-160, :219). */
+/* Sampler.sample(logits:) (Sources/AlpacaCore/Runtime/Sampler.swift:57-93)
+ * on the device, over the logits of the session's last forward / decode call
+ * (they stay in HBM), for a draw `u` in [0, 1) from the caller's sampler RNG
+ * (the reference's Sampler owns a SplitMix64 and draws Double.random once per
+ * sample).  temperature 0 is the arg-max; top_k 0 disables top-k; top_p 1
+ * disables top-p; parameters are checked as SamplingParameters.validate
+ * (:21-25).  NaN logits are AHIP_ERR_INVALID_ARGUMENT (the Swift code throws).
+ * After a greedy chain or a reset there are no logits to sample. */
+int ahip_session_sample(ahip_session* s, float temperature, int top_k, float top_p, double u, int32_t* token);
+
 int ahip_session_reset(ahip_session* s);
 int ahip_session_length(const ahip_session* s, int* length);
 int ahip_session_capacity(const ahip_session* s, int* capacity);
@@ -314,6 +324,9 @@ int ahip_op_embed(ahip_context* ctx, const int32_t* tokens, int count, int dtype
 /* Block dequantisation of `elements` values (Quantization.swift:9-35 on GPU). */
 int ahip_op_dequantize(ahip_context* ctx, int dtype, const void* src, int64_t elements, float* out);
 /* GPU arg-max, lowest index on ties, NaN never wins (norm_embed.metal:93-121). */
+/* The same sampler over host logits (the op-level test API). */
+int ahip_op_sample(ahip_context* ctx, const float* logits, int n, float temperature, int top_k, float top_p,
+                   double u, int32_t* token);
 int ahip_op_argmax(ahip_context* ctx, const float* logits, int n, int32_t* index);
 
 /* Host block quantiser, Quantization.swift:39-73 (ggml quantize_row_*_ref):

@@ -19,7 +19,13 @@
  *   - tests/golden/tiny_llama.json: Hugging Face float64 logits of two tiny
  *     Llama models in both RoPE layouts (whole forward, KV cache, reset);
  *   - closed forms and invariants (softmax rows sum to one, RoPE preserves
- *     pair norms, Q4_0 nibble order, argmax tie rule, SplitMix64 vectors).
+ *     pair norms, Q4_0 nibble order, argmax tie rule, SplitMix64 vectors);
+ *   - the sampler: the assertions of the reference's SamplerTests.swift
+ *     (frequencies against softmax, top-k and top-p supports, seeds, extreme
+ *     logits) and brute-force checks of the inverse-CDF draw.  The mapping of
+ *     a SplitMix64 word to Double.random (orc_uniform53) restates the Swift
+ *     standard library and cannot be run here: parity unpinned for the exact
+ *     token stream of a seed, pinned for the draw given u.
  * Every exported function is covered by at least one of these.
  */
 #include <math.h>
@@ -412,6 +418,80 @@ int orc_argmax(const float* logits, int n) {
         if (logits[i] > logits[best]) best = i;
     }
     return best;
+}
+
+/* Double.random(in: 0..<1, using:) over SplitMix64 as the Swift standard
+ * library defines it for Double (53 significand bits): the low 53 bits of
+ * next() times 2^-53 (stdlib FloatingPointRandom.swift; the value is never 1). */
+double orc_uniform53(uint64_t* state) {
+    return (double)(orc_splitmix_next(state) & ((1ull << 53) - 1)) * 0x1p-53;
+}
+
+/* Sampler.sample(logits:), Runtime/Sampler.swift:57-93, for a draw u in
+ * [0, 1) (the RNG stays with the caller): temperature 0 is the arg-max; NaN
+ * returns -1 (the Swift code throws); top-k keeps the k largest logits (ties
+ * by lower index); probabilities exp((l - top) / t) in double; top-p keeps the
+ * shortest prefix whose cumulative p/sum reaches top_p; the draw walks the
+ * kept probabilities in order against u * sum.  Candidates are sorted by
+ * logit, descending, index ascending, exactly when top-k or top-p applies. */
+static const float* g_sort_logits;
+static int cmp_desc(const void* a, const void* b) {
+    const int i = *(const int*)a, j = *(const int*)b;
+    const float x = g_sort_logits[i], y = g_sort_logits[j];
+    if (x != y) return x > y ? -1 : 1;
+    return i < j ? -1 : (i > j ? 1 : 0);
+}
+int orc_sample(const float* logits, int n, float temperature, int top_k, float top_p, double u) {
+    if (n <= 0) return -1;
+    if (temperature == 0.0f) return orc_argmax(logits, n);
+    for (int i = 0; i < n; i++)
+        if (isnan(logits[i])) return -1;
+    int* cand = (int*)malloc(sizeof(int) * (size_t)n);
+    double* probs = (double*)malloc(sizeof(double) * (size_t)n);
+    for (int i = 0; i < n; i++) cand[i] = i;
+    int count = n;
+    const int k = top_k > 0 ? (top_k < n ? top_k : n) : n;
+    if (k < n || top_p < 1.0f) {
+        g_sort_logits = logits;
+        qsort(cand, (size_t)n, sizeof(int), cmp_desc);
+        count = k;
+    }
+    const double t = (double)temperature;
+    double top = (double)logits[cand[0]];
+    for (int i = 1; i < count; i++)
+        if ((double)logits[cand[i]] > top) top = (double)logits[cand[i]];
+    double sum = 0.0;
+    for (int i = 0; i < count; i++) {
+        probs[i] = exp(((double)logits[cand[i]] - top) / t);
+        sum += probs[i];
+    }
+    if (top_p < 1.0f) {
+        double cumulative = 0.0;
+        int keep = count;
+        for (int i = 0; i < count; i++) {
+            cumulative += probs[i] / sum;
+            if (cumulative >= (double)top_p) {
+                keep = i + 1;
+                break;
+            }
+        }
+        count = keep;
+        sum = 0.0;
+        for (int i = 0; i < count; i++) sum += probs[i];
+    }
+    const double target = u * sum;
+    double acc = 0.0;
+    int token = cand[count - 1];
+    for (int i = 0; i < count; i++) {
+        acc += probs[i];
+        if (target < acc) {
+            token = cand[i];
+            break;
+        }
+    }
+    free(cand);
+    free(probs);
+    return token;
 }
 
 /* ---------------------------------------------------------------- model */

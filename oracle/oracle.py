@@ -58,6 +58,8 @@ def lib():
             "orc_attention": (None, [fp, C.c_int, C.c_int, C.c_int, fp, fp, C.c_int, C.c_int, C.c_int, fp, fp]),
             "orc_embed": (C.c_int, [ip, C.c_int, C.c_int, vp, C.c_int, C.c_int, fp]),
             "orc_argmax": (C.c_int, [fp, C.c_int]),
+            "orc_uniform53": (C.c_double, [C.POINTER(C.c_uint64)]),
+            "orc_sample": (C.c_int, [fp, C.c_int, C.c_float, C.c_int, C.c_float, C.c_double]),
             "orc_model_create": (vp, [vp, C.c_int, C.c_int, C.c_int, vp, vp, fp]),
             "orc_model_set_layer": (None, [vp, C.c_int, fp, vp, vp, vp, vp, fp, vp, vp, vp]),
             "orc_model_destroy": (None, [vp]),
@@ -246,6 +248,42 @@ def argmax(logits) -> int:
     if r < 0:
         raise ValueError("logits contain NaN")
     return r
+
+
+def sample(logits, temperature: float, top_k: int, top_p: float, u: float) -> int:
+    """Sampler.sample (Sampler.swift:57-93) for a given draw u in [0, 1)."""
+    v = f32(logits)
+    if v.size == 0:
+        raise ValueError("cannot sample from empty logits")
+    r = lib().orc_sample(_f(v), v.size, temperature, top_k, top_p, u)
+    if r < 0:
+        raise ValueError("logits contain NaN")
+    return r
+
+
+class Sampler:
+    """Sampler (Sampler.swift:43-55): validated parameters and a SplitMix64
+    stream; each sample() draws one uniform (orc_uniform53) unless greedy."""
+
+    def __init__(self, temperature: float = 0.8, top_k: int = 0, top_p: float = 1.0, seed: int = 0):
+        if not (np.isfinite(temperature) and temperature >= 0):
+            raise ValueError("temperature must be finite and >= 0")
+        if top_k < 0:
+            raise ValueError("topK must be >= 0")
+        if not (0 < top_p <= 1):
+            raise ValueError("topP must be in (0, 1]")
+        self.temperature, self.top_k, self.top_p = float(temperature), int(top_k), float(top_p)
+        self.state = C.c_uint64(seed)
+
+    def draw(self) -> float:
+        return lib().orc_uniform53(C.byref(self.state))
+
+    def sample(self, logits) -> int:
+        if len(logits) == 0:
+            raise ValueError("cannot sample from empty logits")  # checked before greedy, Sampler.swift:60
+        if self.temperature == 0:
+            return argmax(logits)
+        return sample(logits, self.temperature, self.top_k, self.top_p, self.draw())
 
 
 def set_threads(n: int) -> None:
