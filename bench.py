@@ -26,6 +26,10 @@ embeddings), random-init synthetic weights, all resident in HBM.
     prefill weight cache (MetalLlamaModel.buildPrefillCache, f16 copies of the
     layer projections, as `--prefill-cache` in the reference CLI): tok/s and
     the gate+up GEMM's rate.  Reported beside prefill_tok_s, not instead of it.
+  * other_configs: decode and prefill of configs C4 (360M-shape Q4_0, decode
+    at context 2048) and C5 (1.7B-shape Q8_0, decode at 4096, 4096-token
+    prefill) with their fractions of the HBM and MFMA rooflines; reported
+    beside the C1 value, not instead of it.
   * cpu_baseline: the C oracle (restatement of AlpacaCore's CPU path) on the
     host cores: decode steps at context 2048 (the oracle's cache is filled
     with synthetic rows, since prefilling 2048 positions on the CPU would take
@@ -52,15 +56,17 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def q8_bytes(rows: int, cols: int) -> int:
-    return rows * cols // 32 * 34
+def q8_bytes(rows: int, cols: int, block: int = 34) -> int:
+    """Bytes of a rows x cols matrix in 32-weight blocks of `block` bytes (Q8_0 34, Q4_0 18)."""
+    return rows * cols // 32 * block
 
 
-def decode_token_bytes(c, ctx_len: float) -> float:
+def decode_token_bytes(c, ctx_len: float, block: int = 34) -> float:
     """Algorithmic HBM bytes of one decode token at context ctx_len."""
     H, QW, KW, F, V, L = c.hidden_size, c.query_width, c.kv_width, c.feed_forward_size, c.vocab_size, c.layer_count
-    proj = L * (q8_bytes(QW + 2 * KW, H) + q8_bytes(H, QW) + 2 * q8_bytes(F, H) + q8_bytes(H, F))
-    return proj + q8_bytes(V, H) + (2 * L + 1) * H * 4 + 2 * L * ctx_len * KW * 2 + 2 * L * KW * 2
+    b = block
+    proj = L * (q8_bytes(QW + 2 * KW, H, b) + q8_bytes(H, QW, b) + 2 * q8_bytes(F, H, b) + q8_bytes(H, F, b))
+    return proj + q8_bytes(V, H, b) + (2 * L + 1) * H * 4 + 2 * L * ctx_len * KW * 2 + 2 * L * KW * 2
 
 
 def decode_phase_bytes(c, ctx_len: float) -> dict:
@@ -85,6 +91,46 @@ def prefill_stage_flops(c, T: int) -> dict:
         "ffn down (+residual)": 2 * T * H * F,
         "attention": 2 * hd * nh * T * (T + 1),  # QK^T and PV over the causal triangle
     }
+
+
+def other_config(ctx, spec, ctx_len: int, prefill_tokens: int, steps: int = 64) -> dict:
+    """Decode at ctx_len and a prefill of prefill_tokens on another BASELINE config
+    (random-init weights of its shape): tok/s and the fraction of the roofline."""
+    import numpy as np
+
+    from alpaca_amd import synth
+    from alpaca_amd.model import HIPLlamaModel
+    from alpaca_amd.tensor import Q4_0
+    c = spec.config
+    model = HIPLlamaModel(ctx, c, synth.build_weights(spec))
+    prompt = synth.prompt_tokens(spec, max(ctx_len, prefill_tokens))
+    s = model.make_session(capacity=ctx_len + steps + 16, max_batch=4096)
+    first = int(np.argmax(s.forward(prompt[:ctx_len])))
+    t0 = time.perf_counter()
+    s.decode_greedy(first, steps, lambda t: True)
+    el = time.perf_counter() - t0
+    launch = s.last_gpu_seconds / steps
+    tok_bytes = decode_token_bytes(c, ctx_len + (steps - 1) / 2 + 1, 18 if spec.dtype == Q4_0 else 34)
+    s.close()
+    p = model.make_session(capacity=prefill_tokens, max_batch=4096)
+    p.forward(prompt[:prefill_tokens])
+    p.reset()
+    walls = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        p.forward(prompt[:prefill_tokens])
+        walls.append(time.perf_counter() - t0)
+        p.reset()
+    wall = float(np.median(walls))
+    # the stage FLOPs are per layer
+    flops = c.layer_count * sum(prefill_stage_flops(c, prefill_tokens).values()) + 2 * c.vocab_size * c.hidden_size
+    p.close()
+    model.close()
+    return {"decode_ctx": ctx_len, "decode_tok_s": round(steps / el, 1), "decode_avg_launch_us": round(launch * 1e6, 1),
+            "decode_hbm_frac": round(tok_bytes / launch / 1e9 / HBM_PEAK_GBS, 4),
+            "prefill_tokens": prefill_tokens, "prefill_tok_s": round(prefill_tokens / wall, 1),
+            "prefill_mfma_frac": round(flops / wall / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+            "prefill_note": "wall clock of forward, GEMMs + causal attention + last-token logits"}
 
 
 def stage_table(profile: dict, units: dict, scale: float, unit: str, per: int = 1) -> dict:
@@ -149,6 +195,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--no-weight-cache", action="store_true", help="skip the prefill-weight-cache measurement")
+    ap.add_argument("--no-other-configs", action="store_true", help="skip the C4 / C5 decode and prefill lines")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the timed decode steps (for counter passes of the decode kernel)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -294,6 +341,16 @@ def main() -> int:
         cp.close()
         cm.close()
 
+    # ---------------------------------------------------------------- other BASELINE configs
+    others = None
+    if not args.no_other_configs:
+        others = {}
+        for key, sp, ctx_len, pre in (("C4 360M-shape Q4_0", synth.C4, 2048, 2048),
+                                      ("C5 1.7B-shape Q8_0", synth.C5, 4096, 4096)):
+            others[key] = other_config(ctx, sp, ctx_len, pre)
+            log(f"{key}: decode {others[key]['decode_tok_s']} tok/s at ctx {ctx_len} "
+                f"({100 * others[key]['decode_hbm_frac']:.1f}% of HBM), prefill {others[key]['prefill_tok_s']} tok/s")
+
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
     if not args.no_cpu_baseline:
@@ -314,6 +371,7 @@ def main() -> int:
                    "greedy_depth": args.depth},
         "prefill_tok_s": round(prefill_tok_s, 1),
         "prefill_weight_cache": wcache,
+        "other_configs": others,
         "decode_ms_per_token": round(el / args.steps * 1e3, 4),
         "roofline": roof, "roofline_prefill": roof_p, "cpu_baseline": cpu,
         "stages_decode_per_token": stages_d, "stages_prefill": stages_p,
