@@ -196,6 +196,8 @@ def main() -> int:
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--no-weight-cache", action="store_true", help="skip the prefill-weight-cache measurement")
     ap.add_argument("--no-other-configs", action="store_true", help="skip the C4 / C5 decode and prefill lines")
+    ap.add_argument("--config", choices=("C1", "C4", "C5"), default="C1",
+                    help="model config of a --decode-only run (default C1, the headline)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the timed decode steps (for counter passes of the decode kernel)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -224,25 +226,31 @@ def main() -> int:
     from alpaca_amd import synth
     from alpaca_amd.model import HIPContext, HIPLlamaModel
 
-    spec = synth.C1
+    # --config picks another BASELINE config for a --decode-only run (counter passes of its decode)
+    spec = {"C1": synth.C1, "C4": synth.C4, "C5": synth.C5}[args.config]
+    decode_ctx = {"C1": DECODE_CTX, "C4": 2048, "C5": 4096}[args.config]
+    block = 18 if args.config == "C4" else 34
+    if args.config != "C1" and not args.decode_only:
+        log("--config other than C1 is for --decode-only runs")
+        return 2
     c = spec.config
     t0 = time.perf_counter()
     weights = synth.build_weights(spec)
-    log(f"synthetic C1 weights built in {time.perf_counter() - t0:.1f}s")
+    log(f"synthetic {args.config} weights built in {time.perf_counter() - t0:.1f}s")
     ctx = HIPContext(0)
     model = HIPLlamaModel(ctx, c, weights)
     log(f"model resident: {model.weight_bytes / 1e6:.1f} MB")
     prompt = synth.prompt_tokens(spec, PREFILL_TOKENS)
 
     # ---------------------------------------------------------------- decode
-    cap = DECODE_CTX + args.steps + 16
+    cap = decode_ctx + args.steps + 16
     s = model.make_session(capacity=cap, max_batch=PREFILL_TOKENS)
-    first = int(np.argmax(s.forward(prompt[: DECODE_CTX - args.warmup])))
+    first = int(np.argmax(s.forward(prompt[: decode_ctx - args.warmup])))
     toks = []
     if args.warmup:
         s.decode_greedy(first, args.warmup, lambda t: toks.append(t) or True, depth=args.depth)
         first = toks[-1]
-    assert s.length == DECODE_CTX, s.length
+    assert s.length == decode_ctx, s.length
     log(f"decode: context {s.length}, timing {args.steps} steps")
     timed = []
     t0 = time.perf_counter()
@@ -252,20 +260,21 @@ def main() -> int:
     assert fed == args.steps
     decode_tok_s = args.steps / el
     avg_launch = gpu_s / args.steps
-    mean_ctx = DECODE_CTX + (args.steps - 1) / 2 + 1
-    tok_bytes = decode_token_bytes(c, mean_ctx)
+    mean_ctx = decode_ctx + (args.steps - 1) / 2 + 1
+    tok_bytes = decode_token_bytes(c, mean_ctx, block)
     achieved = tok_bytes / avg_launch / 1e9
     roof = {"bound": "hbm", "kernel": "decode_step_kernel (persistent, one cooperative launch per token)",
             "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 5),
-            "traffic": measured_traffic(os.path.dirname(os.path.abspath(__file__))),
+            "traffic": measured_traffic(os.path.dirname(os.path.abspath(__file__))) if args.config == "C1" else None,
             "traffic_source": "profiles/c1_decode_hbm_counters.md (rocprofv3 FETCH_SIZE x2.00 + WRITE_SIZE x1.00)",
             "bytes_per_launch": int(tok_bytes), "avg_launch_us": round(avg_launch * 1e6, 3),
             "timing": "HIP events on the session stream around the timed steps, divided by the steps"}
     log(f"decode: {decode_tok_s:.1f} tok/s ({el / args.steps * 1e3:.3f} ms/token wall, "
         f"{avg_launch * 1e6:.1f} us/launch GPU, {achieved:.0f} GB/s algorithmic)")
     if args.decode_only:
-        print(json.dumps({"decode_tok_s": round(decode_tok_s, 2), "roofline": roof}), flush=True)
+        print(json.dumps({"config": args.config, "decode_ctx": decode_ctx, "decode_tok_s": round(decode_tok_s, 2),
+                          "roofline": roof}), flush=True)
         s.close()
         model.close()
         ctx.close()
