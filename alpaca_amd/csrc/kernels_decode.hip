@@ -80,6 +80,21 @@ __device__ __host__ inline int split_len_for(int len, int kv_heads, int target) 
     return sl < kMinSplitLen ? kMinSplitLen : (sl > kMaxSplitLen ? kMaxSplitLen : sl);
 }
 
+// Item `it` of the attention phase: KV head j, split s.  Items over full splits
+// come first (head-major) and the last split of every head, which holds the
+// context's remainder, after them, so the workgroups that run one item more than
+// the others run a short one.
+__device__ inline void item_split(int it, int S, int kv_heads, int& j, int& s) {
+    const int per = S - 1, full = kv_heads * per;
+    if (it < full) {
+        j = it / per;
+        s = it - j * per;
+    } else {
+        j = it - full;
+        s = per;
+    }
+}
+
 // Group-size bucket: the kernel variant sized for G query heads per KV head.
 __host__ __device__ inline int group_bucket(int g) { return g <= 1 ? 1 : g <= 2 ? 2 : g <= 4 ? 4 : g <= 8 ? 8 : 16; }
 
@@ -458,28 +473,53 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
     auto sub = [&](int k) {
         if (sub_trace && tid == 0) *gptr(sub_trace + (int64_t)k * gridDim.x + blockIdx.x) = wall_clock64();
     };
-    for (int it = blockIdx.x; it < items; it += gridDim.x) {
-        sub(0);
-        const int j = it / S, s = it - j * S;
-        const int p0 = s * SL, p1 = min(p0 + SL, len), n = p1 - p0;
-        const int nc = min(p1, pos) - p0;  // positions read from the cache
-        const bool has_cur = p1 == len;
-        const f16* kb = kcache + ((int64_t)j * cap + p0) * HD;
-        const f16* vb = vcache + ((int64_t)j * cap + p0) * HD;
-        // cache rows past nc are loaded from row 0 of the split (valid memory) and never used
-        int4 kr[NKP][KV4];
+    // An item's cached K/V rows (cache rows past nc are loaded from row 0 of the
+    // split, valid memory, and never used).  A workgroup with several items loads
+    // the next item's K rows once the current scores are done and its V rows once
+    // the current P.V is done, so those loads overlap the rest of the current item.
+    int4 kr[NKP][KV4];
+    int4 vr[NVP];
+    auto rows_of = [&](int t, int64_t& base, int& ncached) {
+        int jt, st;
+        item_split(t, S, kvh, jt, st);
+        const int q0 = st * SL;
+        ncached = min(min(q0 + SL, len), pos) - q0;
+        base = ((int64_t)jt * cap + q0) * HD;
+    };
+    auto load_k = [&](int t) {
+        int64_t base;
+        int ncached;
+        rows_of(t, base, ncached);
 #pragma unroll
         for (int k = 0; k < NKP; k++) {
             const int r = k * PPP + pq;
 #pragma unroll
-            for (int u = 0; u < KV4; u++) kr[k][u] = gload_i4(kb + (int64_t)(r < nc ? r : 0) * HD + tq * DPT + 8 * u);
+            for (int u = 0; u < KV4; u++)
+                kr[k][u] = gload_i4(kcache + base + (int64_t)(r < ncached ? r : 0) * HD + tq * DPT + 8 * u);
         }
-        int4 vr[NVP];
+    };
+    auto load_v = [&](int t) {
+        int64_t base;
+        int ncached;
+        rows_of(t, base, ncached);
 #pragma unroll
         for (int k = 0; k < NVP; k++) {
             const int r = k * RPP + rq;
-            vr[k] = gload_i4(vb + (int64_t)(r < nc ? r : 0) * HD + tr * 8);
+            vr[k] = gload_i4(vcache + base + (int64_t)(r < ncached ? r : 0) * HD + tr * 8);
         }
+    };
+    if (blockIdx.x < items) {
+        load_k(blockIdx.x);
+        load_v(blockIdx.x);
+    }
+    for (int it = blockIdx.x; it < items; it += gridDim.x) {
+        sub(0);
+        int j, s;
+        item_split(it, S, kvh, j, s);
+        const int p0 = s * SL, p1 = min(p0 + SL, len), n = p1 - p0;
+        const int nc = min(p1, pos) - p0;  // positions read from the cache
+        const bool has_cur = p1 == len;
+        const int next = it + (int)gridDim.x;
         sub(1);
         if (!wait_words(qkv + j * G * HD, G * HD, qs, c)) return false;
         sub(2);
@@ -528,6 +568,7 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
                 }
             }
         }
+        if (next < items) load_k(next);  // kr is free once the scores are done
         __syncthreads();
         float sc[GM];
 #pragma unroll
@@ -581,6 +622,7 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
                 }
             }
         }
+        if (next < items) load_v(next);  // vr is free once P.V is done
         // sum the row groups: xor 8 (DPP) and xor 16 (swizzle) inside each 32-lane half,
         // then the 8 half-wave partials through LDS
 #pragma unroll
