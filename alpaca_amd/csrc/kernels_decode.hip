@@ -160,12 +160,14 @@ __device__ __noinline__ void raise_abort(Ctl c) {
     if (c.status) *(volatile int*)c.status = 1;
 }
 
-// Waits until the n words at src carry this launch's tag and copies their
-// values to dst (LDS).  Called by every thread of the workgroup; returns false
-// (for every thread) when the launch is aborting.  All of a thread's pending
-// words are re-polled together, so a wait costs one round trip once the data
-// is there.  Indices past n are clamped to word n-1 for loading (never stored).
-__device__ __forceinline__ bool wait_words(const u64* src, int n, float* dst, const Ctl& c) {
+// Waits until the n words src(0..n-1) carry this launch's tag and copies their
+// values to dst[0..n-1] (LDS).  Called by every thread of the workgroup;
+// returns false (for every thread) when the launch is aborting.  All of a
+// thread's pending words are re-polled together, so a wait costs one round
+// trip once the data is there.  Indices past n are clamped to word n-1 for
+// loading (never stored).
+template <class Src>
+__device__ __forceinline__ bool wait_words_at(Src src, int n, float* dst, const Ctl& c) {
     constexpr int B = 8;
     int bad = 0;
     for (int base = 0; base < n && !bad; base += B * kT) {
@@ -174,7 +176,7 @@ __device__ __forceinline__ bool wait_words(const u64* src, int n, float* dst, co
 #pragma unroll
         for (int k = 0; k < B; k++) {
             const int i = base + threadIdx.x + k * kT;
-            w[k] = ld_word(src + (i < n ? i : n - 1));
+            w[k] = ld_word(src(i < n ? i : n - 1));
             if (i < n) pend |= 1u << k;
         }
         long long t0 = 0;
@@ -198,12 +200,15 @@ __device__ __forceinline__ bool wait_words(const u64* src, int n, float* dst, co
 #pragma unroll
             for (int k = 0; k < B; k++) {
                 const int i = base + threadIdx.x + k * kT;
-                if ((pend >> k) & 1u) w[k] = ld_word(src + (i < n ? i : n - 1));
+                if ((pend >> k) & 1u) w[k] = ld_word(src(i < n ? i : n - 1));
             }
         }
     }
     if (bad) raise_abort(c);
     return !__syncthreads_or(bad);
+}
+__device__ __forceinline__ bool wait_words(const u64* src, int n, float* dst, const Ctl& c) {
+    return wait_words_at([src](int i) { return src + i; }, n, dst, c);
 }
 
 // Block-wide sum over the 256 threads (result in every thread).
@@ -430,24 +435,61 @@ struct PhaseQKV {
     }
 };
 
+// V rows in LDS: 16-byte chunk c of row r sits at slot c ^ vt_swz(r).  Over 8
+// consecutive rows vt_swz takes 8 distinct values, and over 4 consecutive rows
+// it differs in bits 1-2, so neither the row stores nor the transpose reads
+// (8 bytes from each of 4 rows per lane group) conflict.
+__device__ __forceinline__ int vt_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Eight floats from 16-byte-aligned LDS, as two 16-byte reads.
+struct float8 {
+    float v[8];
+};
+__device__ __forceinline__ float8 ld_f8(const float* p) {
+    const float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
+    return float8{{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}};
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
+// (i % 4) of the 4 halves addressed by lane 4j + i/4, for j = 0..3.  When
+// lanes 4j..4j+3 address V row R_j at dims d0, d0+4, d0+8, d0+12, lane i gets
+// V[R_0..R_3][d0 + i]: a V^T fragment read from row-major V.
+__device__ __forceinline__ f16x4 vt_read_tr(const uint8_t* p) {
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
+    return __builtin_bit_cast(f16x4, v);
+}
+
 // P2: split-K attention over the f16 cache.  Item (j, s): KV head j, context
-// positions [s*SL, min((s+1)*SL, len)).  Scores: TPP = HD/DPT threads per
-// position, each holding a DPT-wide slice of the G query rows in registers
-// and a DPT-wide slice of the K row (prefetched before the wait); the partial
-// dots are reduced across the TPP lanes.  P.V: HD/8 threads per V row.
-// Writes, per query head g of the group, the words
+// positions [s*SL, min((s+1)*SL, len)), SL <= 256, cut into 32-position
+// chunks; chunk ch belongs to wave ch % 4.  The scores are computed transposed
+// with v_mfma_f32_16x16x32_f16, S^T = K Q^T: the A operand is a K row fragment
+// loaded straight from the cache into registers (16 bytes per lane, prefetched
+// before the query arrives), the B operand the G query rows of the group
+// (columns past G are zero).  Each query value enters as two f16 terms,
+// hi = f16(q) and lo = f16(q - hi), which carry q to ~2^-22, so with K exact in
+// f16 and float32 accumulation the scores keep float32 accuracy.  A lane then
+// holds one query column at 4 positions of each 16-position tile: the B
+// operand layout of O^T += V^T P^T once the position order inside a
+// 32-position step is permuted identically on both operands.  P = 2^(s - max)
+// enters as hi + lo of P * 2^14 (scaled so that lo stays out of the f16
+// subnormals); V^T fragments come from LDS transpose reads of the V rows, which
+// are loaded into registers (prefetched) and stored row-major to LDS.  Writes,
+// per query head g of the group, the words
 // [max (base-2 units), sum, unnormalised output[HD]] of the split
 // (attention_decode.metal:27-116 computes the same triple).
 template <int HD, int GM>
 __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int pos, Ctl c) {
-    constexpr int DPT = GM <= 4 ? 16 : 8;      // query/key dims per thread in the scores
-    constexpr int KV4 = DPT / 8;               // 16-byte K chunks per thread and position
-    constexpr int TPP = HD / DPT;              // threads per position
-    constexpr int PPP = kT / TPP;              // positions per score pass
-    constexpr int NKP = kMaxSplitLen / PPP;    // score passes
-    constexpr int TPR = HD / 8;                // threads per V row
-    constexpr int RPP = kT / TPR;              // V rows per pass
-    constexpr int NVP = kMaxSplitLen / RPP;    // V passes
+    constexpr int KC = HD / 32;                      // 32-dim steps of a score tile
+    constexpr int DT = HD / 16;                      // 16-dim tiles of the output
+    constexpr int NCH = kMaxSplitLen / 32 / kWaves;  // 32-position chunks per wave
+    constexpr int ROWB = HD * 2;                     // bytes per V row in LDS
+    constexpr int TPR = HD / 8;                      // threads per V row (V loads)
+    constexpr int RPP = kT / TPR;                    // V rows per pass
+    constexpr int NVP = kMaxSplitLen / RPP;          // V passes
+    static_assert(32 % RPP == 0 || RPP % 32 == 0, "V passes cover whole 32-position chunks");
+    constexpr float kPScale = 16384.f, kPUnscale = 1.f / 16384.f;
     const DecodeParams& p = P();
     const DecLayer& L = LY();
     float* scr = lds_of().scr;
@@ -458,16 +500,19 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
     const int S = (len + SL - 1) / SL, items = kvh * S;
     const f16* kcache = (const f16*)L.kc;
     const f16* vcache = (const f16*)L.vc;
-    float* qs = scr;                        // [GM][HD]
-    float* kcur = qs + GM * HD;             // [HD]
-    float* vcur = kcur + HD;                // [HD]
-    float* es = vcur + HD;                  // [GM][kMaxSplitLen]: scores, then probabilities
-    float* red = es + GM * kMaxSplitLen;    // [GM][8]
-    float* ws = red + GM * 8;               // [2*kWaves][GM][HD]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int tr = tid % TPR, rq = tid / TPR;      // P.V layout
-    const int tq = tid % TPP, pq = tid / TPP;      // score layout
+    float* qs = scr;                                   // [G][HD] query rows, then k and v of the current position
+    float* kcur = qs + G * HD;                         // [HD]
+    float* vcur = kcur + HD;                           // [HD]
+    float* red = scr + GM * HD + 2 * HD;               // [GM][8]: per-wave max, then sum
+    float* ws = red + GM * 8;                          // [kWaves][GM][HD]
+    uint8_t* vt = (uint8_t*)(ws + kWaves * GM * HD);   // [kMaxSplitLen][HD] f16 V rows, chunk-swizzled
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c16 = lane & 15, q4 = lane >> 4;         // MFMA layout: column / row group
+    const int tr = tid % TPR, rq = tid / TPR;          // V load layout
     const float sl2 = 1.4426950408889634f / sqrtf((float)HD);
+    auto fmax2 = [](float x, float y) { return fmaxf(x, y); };
+    auto add2 = [](float x, float y) { return x + y; };
     unsigned long long* sub_trace =
         p.trace ? p.trace + (int64_t)decode_trace_points(p.n_layers) * gridDim.x : nullptr;
     auto sub = [&](int k) {
@@ -476,34 +521,40 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
     // An item's cached K/V rows (cache rows past nc are loaded from row 0 of the
     // split, valid memory, and never used).  A workgroup with several items loads
     // the next item's K rows once the current scores are done and its V rows once
-    // the current P.V is done, so those loads overlap the rest of the current item.
-    int4 kr[NKP][KV4];
+    // the current ones are in LDS, so those loads overlap the rest of the current item.
+    int4 kr[NCH][2][KC];
     int4 vr[NVP];
-    auto rows_of = [&](int t, int64_t& base, int& ncached) {
+    auto rows_of = [&](int t, int64_t& base, int& ncached, int& nrows) {
         int jt, st;
         item_split(t, S, kvh, jt, st);
-        const int q0 = st * SL;
-        ncached = min(min(q0 + SL, len), pos) - q0;
+        const int q0 = st * SL, q1 = min(q0 + SL, len);
+        ncached = min(q1, pos) - q0;
+        nrows = q1 - q0;
         base = ((int64_t)jt * cap + q0) * HD;
     };
     auto load_k = [&](int t) {
         int64_t base;
-        int ncached;
-        rows_of(t, base, ncached);
+        int ncached, nrows;
+        rows_of(t, base, ncached, nrows);
 #pragma unroll
-        for (int k = 0; k < NKP; k++) {
-            const int r = k * PPP + pq;
+        for (int ci = 0; ci < NCH; ci++) {
+            if (32 * (wave + kWaves * ci) >= nrows) continue;  // uniform across the wave
 #pragma unroll
-            for (int u = 0; u < KV4; u++)
-                kr[k][u] = gload_i4(kcache + base + (int64_t)(r < ncached ? r : 0) * HD + tq * DPT + 8 * u);
+            for (int u = 0; u < 2; u++) {
+                const int r = 32 * (wave + kWaves * ci) + 16 * u + c16;
+                const f16* row = kcache + base + (int64_t)(r < ncached ? r : 0) * HD + 8 * q4;
+#pragma unroll
+                for (int kc = 0; kc < KC; kc++) kr[ci][u][kc] = gload_i4(row + 32 * kc);
+            }
         }
     };
     auto load_v = [&](int t) {
         int64_t base;
-        int ncached;
-        rows_of(t, base, ncached);
+        int ncached, nrows;
+        rows_of(t, base, ncached, nrows);
 #pragma unroll
         for (int k = 0; k < NVP; k++) {
+            if ((k * RPP & ~31) >= nrows) continue;  // whole 32-row chunks; uniform across the workgroup
             const int r = k * RPP + rq;
             vr[k] = gload_i4(vcache + base + (int64_t)(r < ncached ? r : 0) * HD + tr * 8);
         }
@@ -518,129 +569,140 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
         item_split(it, S, kvh, j, s);
         const int p0 = s * SL, p1 = min(p0 + SL, len), n = p1 - p0;
         const int nc = min(p1, pos) - p0;  // positions read from the cache
-        const bool has_cur = p1 == len;
+        const bool has_cur = p1 == len;    // then position nc (the last) is the current one
         const int next = it + (int)gridDim.x;
         sub(1);
-        if (!wait_words(qkv + j * G * HD, G * HD, qs, c)) return false;
-        sub(2);
-        if (has_cur) {
-            if (!wait_words(qkv + QW + j * HD, HD, kcur, c)) return false;
-            if (!wait_words(qkv + QW + KW + j * HD, HD, vcur, c)) return false;
+        // the query rows, and for the split holding the current position its k
+        // and v rows, in one round trip
+        {
+            const int nq = G * HD, qo = j * G * HD, dk = QW + j * HD - nq - qo, dv = KW - HD;
+            const u64* qb = qkv + qo;
+            // sums of selects, not a chained select (which the compiler may turn into a stack lookup)
+            auto src = [qb, nq, dk, dv](int i) { return qb + i + (i >= nq ? dk : 0) + (i >= nq + HD ? dv : 0); };
+            if (!wait_words_at(src, has_cur ? nq + 2 * HD : nq, qs, c)) return false;
         }
-        for (int i = G * HD + tid; i < GM * HD; i += kT) qs[i] = 0.f;  // rows past the group
-        __syncthreads();
+        sub(2);
         sub(3);
-        // this thread's slice of the query rows, in base-2 exponent units
-        float qr[GM][DPT];
+        // B operand: column c16 = query head of the group, dims 32kc + 8q4 .. +7,
+        // in base-2 exponent units, as hi + lo
+        // (read unconditionally from a valid row and scaled by 0 past G: no branches)
+        f16x8 qh[KC], ql[KC];
+        {
+            const float* qrow = qs + (c16 < G ? c16 : 0) * HD + 8 * q4;
+            const float qm = c16 < G ? sl2 : 0.f;
 #pragma unroll
-        for (int g = 0; g < GM; g++)
+            for (int kc = 0; kc < KC; kc++) {
+                const float8 q8 = ld_f8(qrow + 32 * kc);
 #pragma unroll
-            for (int e = 0; e < DPT; e += 4) {
-                const float4 t = *(const float4*)&qs[g * HD + tq * DPT + e];
-                qr[g][e] = t.x * sl2;
-                qr[g][e + 1] = t.y * sl2;
-                qr[g][e + 2] = t.z * sl2;
-                qr[g][e + 3] = t.w * sl2;
+                for (int e = 0; e < 8; e++) {
+                    const float x = q8.v[e] * qm;
+                    const f16 h = (f16)x;
+                    qh[kc][e] = h;
+                    ql[kc][e] = (f16)(x - (float)h);
+                }
             }
+        }
+        // S^T tiles: sacc[ci][u][r] = score(position 32ch + 16u + 4q4 + r, query column c16)
+        f32x4 sacc[NCH][2];
+        float mx = -INFINITY;
 #pragma unroll
-        for (int k = 0; k < NKP; k++) {
-            if (k * PPP < n) {  // uniform across the workgroup
-                const int r = k * PPP + pq;
-                float kf[DPT];
-                if (r < nc) {
+        for (int ci = 0; ci < NCH; ci++) {
+            const int ch = wave + kWaves * ci;
 #pragma unroll
-                    for (int u = 0; u < KV4; u++) {
-                        const f16* kh = (const f16*)&kr[k][u];
+            for (int u = 0; u < 2; u++) {
+                sacc[ci][u] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+                if (32 * ch >= n) continue;  // uniform across the wave
+                f16x8 kf[KC];
 #pragma unroll
-                        for (int e = 0; e < 8; e++) kf[8 * u + e] = (float)kh[e];
+                for (int kc = 0; kc < KC; kc++) kf[kc] = __builtin_bit_cast(f16x8, kr[ci][u][kc]);
+                if (has_cur && 32 * ch + 16 * u + c16 == nc) {  // the current position's k row
+#pragma unroll
+                    for (int kc = 0; kc < KC; kc++) {
+                        const float8 k8 = ld_f8(kcur + 32 * kc + 8 * q4);
+#pragma unroll
+                        for (int e = 0; e < 8; e++) kf[kc][e] = (f16)k8.v[e];
                     }
-                } else {
+                }
+                f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int e = 0; e < DPT; e++) kf[e] = kcur[tq * DPT + e];
+                for (int kc = 0; kc < KC; kc++) {
+                    a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[kc], qh[kc], a, 0, 0, 0);
+                    a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[kc], ql[kc], a, 0, 0, 0);
                 }
 #pragma unroll
-                for (int g = 0; g < GM; g++) {
-                    float d = 0.f;
-#pragma unroll
-                    for (int e = 0; e < DPT; e++) d += qr[g][e] * kf[e];
-                    d = lane_sum<TPP>(d);
-                    if (tq == 0 && r < kMaxSplitLen) es[g * kMaxSplitLen + r] = d;
+                for (int r = 0; r < 4; r++) {
+                    const float v = 32 * ch + 16 * u + 4 * q4 + r < n ? a[r] : -INFINITY;
+                    sacc[ci][u][r] = v;
+                    mx = fmaxf(mx, v);
                 }
             }
         }
         if (next < items) load_k(next);  // kr is free once the scores are done
-        __syncthreads();
-        float sc[GM];
-#pragma unroll
-        for (int g = 0; g < GM; g++) sc[g] = (tid < n && g < G) ? es[g * kMaxSplitLen + tid] : -INFINITY;
-#pragma unroll
-        for (int g = 0; g < GM; g++) {
-            const float m = wave_max(sc[g]);
-            if (lane == 0) red[g * 8 + wave] = m;
-        }
-        __syncthreads();
-        sub(4);
-        float mloc[GM];
-#pragma unroll
-        for (int g = 0; g < GM; g++)
-            mloc[g] = fmaxf(fmaxf(red[g * 8 + 0], red[g * 8 + 1]), fmaxf(red[g * 8 + 2], red[g * 8 + 3]));
-#pragma unroll
-        for (int g = 0; g < GM; g++) {
-            const float e = (tid < n && g < G) ? exp2f(sc[g] - mloc[g]) : 0.f;
-            es[g * kMaxSplitLen + tid] = e;
-            const float sum = wave_sum(e);
-            if (lane == 0) red[g * 8 + 4 + wave] = sum;
-        }
-        __syncthreads();
-        sub(5);
-        float acc[GM][8];
-#pragma unroll
-        for (int g = 0; g < GM; g++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) acc[g][e] = 0.f;
+        mx = xor32_combine(xor16_combine(mx, fmax2), fmax2);
+        if (q4 == 0 && c16 < G) red[c16 * 8 + wave] = mx;
+        // V rows to LDS.  Rows past the split get P = 0 but still enter the MFMA,
+        // so they are stored as zeros: no uninitialised value may enter (0 * NaN).
 #pragma unroll
         for (int k = 0; k < NVP; k++) {
+            if ((k * RPP & ~31) >= n) continue;  // every row of an active chunk is read
             const int r = k * RPP + rq;
-            if (k * RPP < n) {  // uniform across the workgroup
-                float vf[8];
-                if (r < nc) {
-                    const f16* vh = (const f16*)&vr[k];
+            int4 v = vr[k];
+            if (r >= nc) {
+                const float8 v8 = ld_f8(vcur + tr * 8);
+                f16x8 h;
 #pragma unroll
-                    for (int e = 0; e < 8; e++) vf[e] = (float)vh[e];
-                } else if (r < n) {  // the current position
+                for (int e = 0; e < 8; e++) h[e] = r < n ? (f16)v8.v[e] : (f16)0.f;  // r == nc: current
+                v = __builtin_bit_cast(int4, h);
+            }
+            *(int4*)(vt + r * ROWB + ((tr ^ vt_swz(r)) * 16)) = v;
+        }
+        if (next < items) load_v(next);  // vr is free once its rows are in LDS
+        __syncthreads();
+        sub(4);
+        const int gq = c16 < G ? c16 : 0;
+        const float mg = fmaxf(fmaxf(red[gq * 8 + 0], red[gq * 8 + 1]), fmaxf(red[gq * 8 + 2], red[gq * 8 + 3]));
+        // P in the B-operand layout: slot 4u + r of chunk ci is position 32ch + 16u + 4q4 + r
+        f16x8 ph[NCH], pl[NCH];
+        float ls = 0.f;
 #pragma unroll
-                    for (int e = 0; e < 8; e++) vf[e] = vcur[tr * 8 + e];
-                } else {  // past the split: probability 0, and no uninitialised value may enter
+        for (int ci = 0; ci < NCH; ci++)
 #pragma unroll
-                    for (int e = 0; e < 8; e++) vf[e] = 0.f;
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float e = exp2f(sacc[ci][u][r] - mg);  // 0 for masked positions
+                    ls += e;
+                    const float x = e * kPScale;
+                    const f16 h = (f16)x;
+                    ph[ci][4 * u + r] = h;
+                    pl[ci][4 * u + r] = (f16)(x - (float)h);
                 }
+        ls = xor32_combine(xor16_combine(ls, add2), add2);
+        if (q4 == 0 && c16 < G) red[c16 * 8 + 4 + wave] = ls;
+        sub(5);
+        // O^T += V^T P^T: oacc[dt][r] = output(dim 16dt + 4q4 + r, query column c16) * 2^14
+        f32x4 oacc[DT];
 #pragma unroll
-                for (int g = 0; g < GM; g++) {
-                    const float pe = es[g * kMaxSplitLen + (r < kMaxSplitLen ? r : 0)];  // zero past n
+        for (int dt = 0; dt < DT; dt++) oacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int e = 0; e < 8; e++) acc[g][e] += pe * vf[e];
-                }
+        for (int ci = 0; ci < NCH; ci++) {
+            const int ch = wave + kWaves * ci;
+            if (32 * ch >= n) continue;  // uniform across the wave
+            const int ra = 32 * ch + 4 * q4 + (c16 >> 2), rb = ra + 16;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                const int cb = 2 * dt + ((c16 & 3) >> 1), hb = (c16 & 1) * 8;
+                const f16x4 lo = vt_read_tr(vt + ra * ROWB + ((cb ^ vt_swz(ra)) * 16) + hb);
+                const f16x4 hi = vt_read_tr(vt + rb * ROWB + ((cb ^ vt_swz(rb)) * 16) + hb);
+                const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph[ci], oacc[dt], 0, 0, 0);
+                oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl[ci], oacc[dt], 0, 0, 0);
             }
         }
-        if (next < items) load_v(next);  // vr is free once P.V is done
-        // sum the row groups: xor 8 (DPP) and xor 16 (swizzle) inside each 32-lane half,
-        // then the 8 half-wave partials through LDS
+        if (c16 < G) {
 #pragma unroll
-        for (int g = 0; g < GM; g++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                float v = acc[g][e];
-                if (TPR <= 8) v += dpp_mov<0x128>(v);
-                v = xor16_combine(v, [](float x, float y) { return x + y; });
-                acc[g][e] = v;
-            }
-        if ((lane & (32 - TPR)) == 0) {
-            const int slot = wave * 2 + (lane >> 5);
-#pragma unroll
-            for (int g = 0; g < GM; g++)
-                if (g < G)
-#pragma unroll
-                    for (int e = 0; e < 8; e++) ws[(slot * GM + g) * HD + tr * 8 + e] = acc[g][e];
+            for (int dt = 0; dt < DT; dt++)
+                *(f32x4*)&ws[(wave * GM + c16) * HD + 16 * dt + 4 * q4] = oacc[dt];
         }
         __syncthreads();
         sub(6);
@@ -653,9 +715,9 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
                 v = (red[g * 8 + 4] + red[g * 8 + 5]) + (red[g * 8 + 6] + red[g * 8 + 7]);
             } else {
                 const int d = e - 2;
-                v = 0.f;
-#pragma unroll
-                for (int slot = 0; slot < 2 * kWaves; slot++) v += ws[(slot * GM + g) * HD + d];
+                v = ((ws[(0 * GM + g) * HD + d] + ws[(1 * GM + g) * HD + d]) +
+                     (ws[(2 * GM + g) * HD + d] + ws[(3 * GM + g) * HD + d])) *
+                    kPUnscale;
             }
             put_word(part + ((int64_t)(j * G + g) * max_splits + s) * (HD + 2) + e, v, c.tag);
         }
@@ -1007,7 +1069,7 @@ size_t decode_lds_bytes(const DecodeParams& p, int grid) {
     size_t scr = 0;
     auto need = [&](size_t floats) { scr = floats > scr ? floats : scr; };
     need((size_t)p.rows_qkv);                                                    // QKV row buffer
-    need((size_t)GM * HD + 2 * HD + (size_t)GM * kMaxSplitLen + GM * 8 + (size_t)2 * kWaves * GM * HD);  // attention
+    need((size_t)GM * HD + 2 * HD + GM * 8 + (size_t)kWaves * GM * HD + (size_t)kMaxSplitLen * HD / 2);  // attention
     need((size_t)p.max_splits * (HD + 2) + p.max_splits);                         // merge
     need(16);                                                                     // logits arg-max
     need((size_t)2 * grid);                                                       // candidates

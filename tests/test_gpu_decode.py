@@ -28,9 +28,16 @@ from tests.test_gpu_model import built, oracle_cfg, oracle_model
 pytestmark = pytest.mark.gpu
 
 
+def shaped(name, **kw):
+    return replace(synth.TINY, config=replace(synth.TINY.config, **kw), name=name)
+
+
+# query heads per KV head 1, 2, 4 and 8 at head dim 64; 2 and 4 at head dim 128
+HD128_G4 = shaped("tiny-hd128-g4", head_count=4, kv_head_count=1, head_dim=128)
 SPECS = [synth.TINY, synth.with_dtype(synth.TINY, Q4_0), synth.with_dtype(synth.TINY, F16),
-         replace(synth.TINY, config=replace(synth.TINY.config, head_count=8, kv_head_count=2), name="tiny-g4"),
-         replace(synth.TINY, config=replace(synth.TINY.config, head_count=4, kv_head_count=4), name="tiny-mha")]
+         shaped("tiny-g4", head_count=8, kv_head_count=2), shaped("tiny-mha", head_count=4, kv_head_count=4),
+         shaped("tiny-g8", head_count=8, kv_head_count=1),
+         shaped("tiny-hd128", head_count=2, kv_head_count=1, head_dim=128), HD128_G4]
 
 
 @pytest.mark.parametrize("spec", SPECS, ids=lambda s: s.name)
@@ -94,11 +101,11 @@ def test_persistent_decode_row_shares_at_c4_shape(hip_ctx, wgs):
     assert worst <= 1e-4
 
 
-def test_persistent_decode_across_attention_split_boundaries(hip_ctx):
+@pytest.mark.parametrize("spec", [synth.TINY, HD128_G4], ids=lambda s: s.name)
+def test_persistent_decode_across_attention_split_boundaries(hip_ctx, spec):
     """Contexts on both sides of every split length (64..256 positions per
     split) and of the capacity: the split-K partials and their merge must
     cover exactly positions 0..pos."""
-    spec = synth.TINY
     c = spec.config
     w = built(spec)
     model = HIPLlamaModel(hip_ctx, c, w)
