@@ -756,11 +756,15 @@ __device__ __forceinline__ bool merge_phase(const u64* part, u64* ctx, int pos, 
         }
         l = block_sum4(l, red + 4);
         const float inv = 1.0f / l;
-        for (int d = threadIdx.x; d < HD; d += kT) {
-            float o = 0.f;
-            for (int s = 0; s < S; s++) o += wsplit[s] * scr[s * (HD + 2) + 2 + d];
-            put_word(ctx + h * HD + d, o * inv, c.tag);
-        }
+        // QPD neighbouring lanes per output dim, lane q summing the splits
+        // s = q mod QPD, so the whole workgroup shares the loop over the splits
+        constexpr int QPD = kT / HD;
+        const int d = threadIdx.x / QPD, q = threadIdx.x % QPD;
+        float o = 0.f;
+#pragma unroll 4
+        for (int s = q; s < S; s += QPD) o += wsplit[s] * scr[s * (HD + 2) + 2 + d];
+        o = lane_sum<QPD>(o);
+        if (q == 0) put_word(ctx + h * HD + d, o * inv, c.tag);
         __syncthreads();
     }
     return true;
