@@ -248,16 +248,27 @@ struct NormGain {
 };
 
 // x (LDS, n floats) -> out = (x * (1/sqrt(mean(x^2) + eps))) * w  (CPUOps.rmsNorm, CPUOps.swift:144-159).
+// The thread's first kNormRegs values are read once, unconditionally (index
+// clamped, value unused past n), so the reads are in flight together.
 __device__ __forceinline__ void rmsnorm_lds(const float* x, const NormGain& g, int n, float eps, float* out,
                                             float* red) {
+    float xv[kNormRegs];
+#pragma unroll
+    for (int k = 0; k < kNormRegs; k++) {
+        const int i = threadIdx.x + k * kT;
+        xv[k] = x[i < n ? i : 0];
+    }
     float ss = 0.f;
-    for (int i = threadIdx.x; i < n; i += kT) ss += x[i] * x[i];
+#pragma unroll
+    for (int k = 0; k < kNormRegs; k++)
+        if (threadIdx.x + k * kT < n) ss += xv[k] * xv[k];
+    for (int i = threadIdx.x + kNormRegs * kT; i < n; i += kT) ss += x[i] * x[i];
     ss = block_sum4(ss, red);
     const float scale = 1.0f / sqrtf(ss / (float)n + eps);
 #pragma unroll
     for (int k = 0; k < kNormRegs; k++) {
         const int i = threadIdx.x + k * kT;
-        if (i < n) out[i] = (x[i] * scale) * g.r[k];
+        if (i < n) out[i] = (xv[k] * scale) * g.r[k];
     }
     for (int i = threadIdx.x + kNormRegs * kT; i < n; i += kT) out[i] = (x[i] * scale) * *gptr(g.w + i);
     __syncthreads();

@@ -24,10 +24,15 @@ def fixture(name: str) -> dict:
 
 @contextmanager
 def env(**kv):
-    """Sets environment variables for the duration of a with-block (the HIP
-    library reads its ALPACA_HIP_* switches when a session is created)."""
+    """Sets environment variables (None: unsets one) for the duration of a
+    with-block (the HIP library reads its ALPACA_HIP_* switches when a session
+    is created)."""
     old = {k: os.environ.get(k) for k in kv}
-    os.environ.update({k: str(v) for k, v in kv.items()})
+    for k, v in kv.items():
+        if v is None:
+            os.environ.pop(k, None)
+        else:
+            os.environ[k] = str(v)
     try:
         yield
     finally:
