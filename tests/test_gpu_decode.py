@@ -37,7 +37,7 @@ HD128_G4 = shaped("tiny-hd128-g4", head_count=4, kv_head_count=1, head_dim=128)
 SPECS = [synth.TINY, synth.with_dtype(synth.TINY, Q4_0), synth.with_dtype(synth.TINY, F16),
          shaped("tiny-g4", head_count=8, kv_head_count=2), shaped("tiny-mha", head_count=4, kv_head_count=4),
          shaped("tiny-g8", head_count=8, kv_head_count=1),
-         shaped("tiny-hd128", head_count=2, kv_head_count=1, head_dim=128), HD128_G4]
+         shaped("tiny-hd128-g2", head_count=2, kv_head_count=1, head_dim=128), HD128_G4]
 
 
 @pytest.mark.parametrize("spec", SPECS, ids=lambda s: s.name)

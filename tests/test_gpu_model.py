@@ -40,9 +40,10 @@ _models = {}
 
 
 def built(spec):
-    if spec.name not in _models:
-        _models[spec.name] = synth.build_weights(spec)
-    return _models[spec.name]
+    key = repr(spec)  # the whole spec: two specs may share a name across test files
+    if key not in _models:
+        _models[key] = synth.build_weights(spec)
+    return _models[key]
 
 
 def gpu_model(ctx, spec):
