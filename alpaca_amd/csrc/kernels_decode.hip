@@ -165,9 +165,10 @@ __device__ __noinline__ void raise_abort(Ctl c) {
 // returns false (for every thread) when the launch is aborting.  All of a
 // thread's pending words are re-polled together, so a wait costs one round
 // trip once the data is there.  Indices past n are clamped to word n-1 for
-// loading (never stored).
+// loading (never stored).  With keep, thread t also returns in keep[k] the
+// value of word t + 256k (k < 8; undefined past n).
 template <class Src>
-__device__ __forceinline__ bool wait_words_at(Src src, int n, float* dst, const Ctl& c) {
+__device__ __forceinline__ bool wait_words_at(Src src, int n, float* dst, const Ctl& c, float* keep = nullptr) {
     constexpr int B = 8;
     int bad = 0;
     for (int base = 0; base < n && !bad; base += B * kT) {
@@ -202,6 +203,10 @@ __device__ __forceinline__ bool wait_words_at(Src src, int n, float* dst, const 
                 const int i = base + threadIdx.x + k * kT;
                 if ((pend >> k) & 1u) w[k] = ld_word(src(i < n ? i : n - 1));
             }
+        }
+        if (keep && base == 0) {
+#pragma unroll
+            for (int k = 0; k < B; k++) keep[k] = __uint_as_float((unsigned)w[k]);
         }
     }
     if (bad) raise_abort(c);
@@ -272,6 +277,31 @@ __device__ __forceinline__ void rmsnorm_lds(const float* x, const NormGain& g, i
     }
     for (int i = threadIdx.x + kNormRegs * kT; i < n; i += kT) out[i] = (x[i] * scale) * *gptr(g.w + i);
     __syncthreads();
+}
+
+// wait_words of an RMSNorm's input row into x, then the norm into out exactly
+// as rmsnorm_lds computes it, with the values a thread polled taken from its
+// registers instead of being read back from LDS.
+__device__ __forceinline__ bool wait_rmsnorm(const u64* src, int n, float* x, const NormGain& g, float eps,
+                                             float* out, float* red, const Ctl& c) {
+    static_assert(kNormRegs == 8, "one register per word of the first wait pass");
+    float v[kNormRegs];
+    if (!wait_words_at([src](int i) { return src + i; }, n, x, c, v)) return false;
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < kNormRegs; k++)
+        if (threadIdx.x + k * kT < n) ss += v[k] * v[k];
+    for (int i = threadIdx.x + kNormRegs * kT; i < n; i += kT) ss += x[i] * x[i];
+    ss = block_sum4(ss, red);
+    const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+#pragma unroll
+    for (int k = 0; k < kNormRegs; k++) {
+        const int i = threadIdx.x + k * kT;
+        if (i < n) out[i] = (v[k] * scale) * g.r[k];
+    }
+    for (int i = threadIdx.x + kNormRegs * kT; i < n; i += kT) out[i] = (x[i] * scale) * *gptr(g.w + i);
+    __syncthreads();
+    return true;
 }
 
 // ------------------------------------------------------------------ GEMV rows
@@ -831,8 +861,7 @@ struct PhaseGateUp {
         rw.prefetch(Wg, Wu, r0, r1);
         NormGain gain;
         gain.load(L.ffn_norm, p.hidden);
-        if (!wait_words(in, p.hidden, sh.xres, c)) return false;
-        rmsnorm_lds(sh.xres, gain, p.hidden, p.eps, sh.xn, sh.red);
+        if (!wait_rmsnorm(in, p.hidden, sh.xres, gain, p.eps, sh.xn, sh.red, c)) return false;
         const unsigned tag = c.tag;
         u64* o = out;
         rw.run(Wg, Wu, r0, r1, sh.xn,
