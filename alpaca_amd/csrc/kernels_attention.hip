@@ -42,11 +42,19 @@ struct FlashArgs {
 constexpr int BQ = 64, BKV = 64;
 
 // Chunk swizzle of the K and V blocks in LDS: 16-byte chunk c of key row r
-// sits at slot c ^ kv_swz(r).  Over 8 consecutive rows kv_swz takes 8
-// distinct values (K fragment reads: 16-byte reads of one chunk from 8 rows
-// per LDS cycle), and over 4 consecutive rows it differs in bits 1-2 (V
-// transpose reads: 32 bytes from each of 4 rows), so neither read conflicts.
-__device__ __forceinline__ int kv_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+// sits at slot c ^ kv_swz(r), kv_swz(r) = (r0^r3, r0^r2, r1) (bits of r).
+// K fragment reads (one chunk from each of 16 consecutive rows): kv_swz takes
+// 8 distinct values over any 8 consecutive rows and over the 8 even (and the 8
+// odd) rows of 16, so 16 lanes x 16 bytes cover 64 banks once at head dim 64
+// (rows of 128 bytes: even and odd rows fall in different bank halves).  V
+// transpose reads (8 bytes from chunks 2d, 2d+1 of 4 consecutive rows): the
+// two rows of one parity select different chunk pairs.  Found by exhaustive
+// search over 3x4 XOR matrices against both bank models (64 banks / 16 lanes,
+// 32 banks / 8 lanes); the former swizzle left the K reads 2-way conflicted and
+// SQ_LDS_BANK_CONFLICT at half of SQ_LDS_IDX_ACTIVE.
+__device__ __forceinline__ int kv_swz(int r) {
+    return (((r ^ (r >> 3)) & 1) | (((r ^ (r >> 2)) & 1) << 1) | (((r >> 1) & 1) << 2));
+}
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 

@@ -476,11 +476,13 @@ struct PhaseQKV {
     }
 };
 
-// V rows in LDS: 16-byte chunk c of row r sits at slot c ^ vt_swz(r).  Over 8
-// consecutive rows vt_swz takes 8 distinct values, and over 4 consecutive rows
-// it differs in bits 1-2, so neither the row stores nor the transpose reads
-// (8 bytes from each of 4 rows per lane group) conflict.
-__device__ __forceinline__ int vt_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+// V rows in LDS: 16-byte chunk c of row r sits at slot c ^ vt_swz(r), the
+// swizzle of the prefill flash kernel (kernels_attention.hip): the transpose
+// reads (8 bytes from chunks 2d, 2d+1 of 4 consecutive rows per 16 lanes) and
+// the row stores (whole rows) do not conflict.
+__device__ __forceinline__ int vt_swz(int r) {
+    return (((r ^ (r >> 3)) & 1) | (((r ^ (r >> 2)) & 1) << 1) | (((r >> 1) & 1) << 2));
+}
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
