@@ -897,12 +897,16 @@ hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
     auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     constexpr int kCUs = 256;
     const int f = forced_tile();
+    // The 256-row tiles hold more accumulators than the 256 architectural VGPRs
+    // (344-353 with AGPR spills) and are slower wherever measured; they stay
+    // reachable through ALPACA_HIP_GEMM_TILE=256.  128x128 tiles (~190 VGPRs,
+    // two workgroups per CU) pay off once the grid has two per CU.
     if constexpr (MODE == GEMM_SWIGLU) {
-        if (f == 1 || (f == 0 && tiles(256, 64) >= kCUs)) return run_dgemm<FMT, 256, 64, 128, 32, MODE>(a, st);
+        if (f == 1) return run_dgemm<FMT, 256, 64, 128, 32, MODE>(a, st);
         return run_dgemm<FMT, 128, 64, 64, 32, MODE>(a, st);
     } else {
-        if (f == 1 || (f == 0 && tiles(256, 128) >= kCUs)) return run_dgemm<FMT, 256, 128, 128, 64, MODE>(a, st);
-        if (f == 2 || (f == 0 && tiles(128, 128) >= kCUs)) return run_dgemm<FMT, 128, 128, 64, 64, MODE>(a, st);
+        if (f == 1) return run_dgemm<FMT, 256, 128, 128, 64, MODE>(a, st);
+        if (f == 2 || (f == 0 && tiles(128, 128) >= 2 * kCUs)) return run_dgemm<FMT, 128, 128, 64, 64, MODE>(a, st);
         return run_dgemm<FMT, 128, 64, 64, 32, MODE>(a, st);
     }
 }
