@@ -518,7 +518,8 @@ __device__ __forceinline__ f16x4 vt_read_tr(const uint8_t* p) {
 // 32-position step is permuted identically on both operands.  P = 2^(s - max)
 // enters as hi + lo of P * 2^14 (scaled so that lo stays out of the f16
 // subnormals); V^T fragments come from LDS transpose reads of the V rows, which
-// are loaded into registers (prefetched) and stored row-major to LDS.  Writes,
+// move global -> LDS by DMA (no registers; a workgroup with several items
+// requests the next item's V and K rows as soon as the current P.V is done).  Writes,
 // per query head g of the group, the words
 // [max (base-2 units), sum, unnormalised output[HD]] of the split
 // (attention_decode.metal:27-116 computes the same triple).
@@ -528,10 +529,6 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
     constexpr int DT = HD / 16;                      // 16-dim tiles of the output
     constexpr int NCH = kMaxSplitLen / 32 / kWaves;  // 32-position chunks per wave
     constexpr int ROWB = HD * 2;                     // bytes per V row in LDS
-    constexpr int TPR = HD / 8;                      // threads per V row (V loads)
-    constexpr int RPP = kT / TPR;                    // V rows per pass
-    constexpr int NVP = kMaxSplitLen / RPP;          // V passes
-    static_assert(32 % RPP == 0 || RPP % 32 == 0, "V passes cover whole 32-position chunks");
     constexpr float kPScale = 16384.f, kPUnscale = 1.f / 16384.f;
     const DecodeParams& p = P();
     const DecLayer& L = LY();
@@ -552,7 +549,6 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c16 = lane & 15, q4 = lane >> 4;         // MFMA layout: column / row group
-    const int tr = tid % TPR, rq = tid / TPR;          // V load layout
     const float sl2 = 1.4426950408889634f / sqrtf((float)HD);
     auto fmax2 = [](float x, float y) { return fmaxf(x, y); };
     auto add2 = [](float x, float y) { return x + y; };
@@ -561,12 +557,11 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
     auto sub = [&](int k) {
         if (sub_trace && tid == 0) *gptr(sub_trace + (int64_t)k * gridDim.x + blockIdx.x) = wall_clock64();
     };
-    // An item's cached K/V rows (cache rows past nc are loaded from row 0 of the
+    // An item's cached K rows (cache rows past nc are loaded from row 0 of the
     // split, valid memory, and never used).  A workgroup with several items loads
-    // the next item's K rows once the current scores are done and its V rows once
-    // the current ones are in LDS, so those loads overlap the rest of the current item.
+    // the next item's K rows and V rows once the current P.V is done, so those
+    // loads overlap the publication of the current item.
     int4 kr[NCH][2][KC];
-    int4 vr[NVP];
     auto rows_of = [&](int t, int64_t& base, int& ncached, int& nrows) {
         int jt, st;
         item_split(t, S, kvh, jt, st);
@@ -591,20 +586,27 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
             }
         }
     };
-    auto load_v = [&](int t) {
+    // V rows go global -> LDS by DMA (no registers): one global_load_lds_dwordx4
+    // moves RPI whole rows, lane L filling slot L % CH of row L / CH with the
+    // cache chunk that the swizzle puts there.  Every row of the 32-row chunks
+    // the item covers is written; rows past the cached ones load row 0 of the
+    // split (valid memory) and are overwritten before use.  Issued only when the
+    // previous item's P.V reads of vt are over (after a barrier).
+    auto dma_v = [&](int t) {
+        constexpr int CH = HD / 8, RPI = 64 / CH;
         int64_t base;
         int ncached, nrows;
         rows_of(t, base, ncached, nrows);
-#pragma unroll
-        for (int k = 0; k < NVP; k++) {
-            if ((k * RPP & ~31) >= nrows) continue;  // whole 32-row chunks; uniform across the workgroup
-            const int r = k * RPP + rq;
-            vr[k] = gload_i4(vcache + base + (int64_t)(r < ncached ? r : 0) * HD + tr * 8);
+        const int ninst = ((nrows + 31) & ~31) / RPI;
+        const uint32_t vt_lds = __builtin_amdgcn_readfirstlane(lds_addr(vt));  // uniform: m0 takes an SGPR
+        for (int i = wave; i < ninst; i += kWaves) {
+            const int r = i * RPI + lane / CH, chunk = (lane % CH) ^ vt_swz(r);
+            dma16(vcache + base + (int64_t)(r < ncached ? r : 0) * HD + chunk * 8, vt_lds + i * RPI * ROWB);
         }
     };
     if (blockIdx.x < items) {
         load_k(blockIdx.x);
-        load_v(blockIdx.x);
+        dma_v(blockIdx.x);
     }
     for (int it = blockIdx.x; it < items; it += gridDim.x) {
         sub(0);
@@ -680,26 +682,33 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
                 }
             }
         }
-        if (next < items) load_k(next);  // kr is free once the scores are done
         mx = xor32_combine(xor16_combine(mx, fmax2), fmax2);
         if (q4 == 0 && c16 < G) red[c16 * 8 + wave] = mx;
-        // V rows to LDS.  Rows past the split get P = 0 but still enter the MFMA,
-        // so they are stored as zeros: no uninitialised value may enter (0 * NaN).
-#pragma unroll
-        for (int k = 0; k < NVP; k++) {
-            if ((k * RPP & ~31) >= n) continue;  // every row of an active chunk is read
-            const int r = k * RPP + rq;
-            int4 v = vr[k];
-            if (r >= nc) {
-                const float8 v8 = ld_f8(vcur + tr * 8);
+        // The V rows are in LDS once this wave's DMA has landed (the barrier
+        // below then covers every wave's).  Rows past the cached ones are
+        // rewritten: the current position's v row, and zeros past the split
+        // (they get P = 0 but still enter the MFMA: no uninitialised value may
+        // enter, 0 * NaN).  Each wave rewrites only rows its own DMA wrote, so
+        // the rewrite cannot be overtaken by another wave's DMA.
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        {
+            constexpr int CH = HD / 8, RPI = 64 / CH;
+            const int end = (n + 31) & ~31;
+            for (int i = lane; i < (end - nc) * CH; i += 64) {
+                const int r = nc + i / CH, slot = i % CH, chunk = slot ^ vt_swz(r);
+                if ((r / RPI) % kWaves != wave) continue;
                 f16x8 h;
+                if (r < n) {  // r == nc: the current position
+                    const float8 v8 = ld_f8(vcur + chunk * 8);
 #pragma unroll
-                for (int e = 0; e < 8; e++) h[e] = r < n ? (f16)v8.v[e] : (f16)0.f;  // r == nc: current
-                v = __builtin_bit_cast(int4, h);
+                    for (int e = 0; e < 8; e++) h[e] = (f16)v8.v[e];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) h[e] = (f16)0.f;
+                }
+                *(f16x8*)(vt + r * ROWB + slot * 16) = h;
             }
-            *(int4*)(vt + r * ROWB + ((tr ^ vt_swz(r)) * 16)) = v;
         }
-        if (next < items) load_v(next);  // vr is free once its rows are in LDS
         __syncthreads();
         sub(4);
         const int gq = c16 < G ? c16 : 0;
@@ -748,6 +757,10 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
                 *(f32x4*)&ws[(wave * GM + c16) * HD + 16 * dt + 4 * q4] = oacc[dt];
         }
         __syncthreads();
+        if (next < items) {  // every wave is done with vt and kr: the next item's rows
+            dma_v(next);
+            load_k(next);
+        }
         sub(6);
         for (int i = tid; i < G * (HD + 2); i += kT) {
             const int g = i / (HD + 2), e = i - g * (HD + 2);
