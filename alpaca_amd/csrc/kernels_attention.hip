@@ -83,9 +83,12 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
     constexpr int PERW = TILE / 1024 / 4; // DMA instructions per wave per block and matrix
     constexpr int PER = 2 * PERW;
     // Three stage buffers per set, each K block then V block, both row-major and swizzled.
-    __shared__ __attribute__((aligned(16))) uint8_t sA0[2 * TILE], sA1[2 * TILE], sA2[2 * TILE];
+    // With two sets the pipeline is two stages deep (64 KB of LDS, two
+    // workgroups per CU); with one set, three (48 KB, three per CU).
+    constexpr int NSTAGE = NSET > 1 ? 2 : 3;
+    __shared__ __attribute__((aligned(16))) uint8_t sA0[2 * TILE], sA1[2 * TILE], sA2[NSTAGE > 2 ? 2 * TILE : 16];
     __shared__ __attribute__((aligned(16))) uint8_t sB0[NSET > 1 ? 2 * TILE : 16], sB1[NSET > 1 ? 2 * TILE : 16],
-        sB2[NSET > 1 ? 2 * TILE : 16];
+        sB2[NSET > 1 && NSTAGE > 2 ? 2 * TILE : 16];
 
     const int h = blockIdx.x;
     const int qb = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks first
@@ -219,12 +222,29 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
         const int kb = first + i;
         if (i < count && kb * BKV <= wpos_hi) compute(cur, kb);
     };
-    issue(lds_addr(st0), 0);
-    issue(lds_addr(st1), 1);
-    for (int i = 0; i < steps; i += 3) {
-        step(st0, st2, i);
-        if (i + 1 < steps) step(st1, st0, i + 1);
-        if (i + 2 < steps) step(st2, st1, i + 2);
+    if constexpr (NSTAGE == 3) {
+        issue(lds_addr(st0), 0);
+        issue(lds_addr(st1), 1);
+        for (int i = 0; i < steps; i += 3) {
+            step(st0, st2, i);
+            if (i + 1 < steps) step(st1, st0, i + 1);
+            if (i + 2 < steps) step(st2, st1, i + 2);
+        }
+    } else {
+        // wait for the step's block (nothing else in flight), barrier (every
+        // wave is done with the other buffer), refill it with the next block,
+        // multiply
+        auto step2 = [&](const uint8_t* cur, uint8_t* refill, int i) {
+            wait_stage_barrier<0>();
+            issue(lds_addr(refill), i + 1);
+            const int kb = first + i;
+            if (i < count && kb * BKV <= wpos_hi) compute(cur, kb);
+        };
+        issue(lds_addr(st0), 0);
+        for (int i = 0; i < steps; i += 2) {
+            step2(st0, st1, i);
+            if (i + 1 < steps) step2(st1, st0, i + 1);
+        }
     }
     wait_stage_barrier<0>();  // no DMA may still be writing LDS past this point
 
