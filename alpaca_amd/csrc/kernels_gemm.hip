@@ -682,12 +682,15 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
     constexpr int NB = G::NB, TM = G::TM, TN = G::TN, PER = G::PER;
     // The three stage buffers, in one array that the GEMM_QKV_ROPE epilogue
     // reuses for the tile's RoPE rows (BM positions x up to 64 pairs of 8 bytes).
-    constexpr int kStages = 3 * L::BYTES;
+    // 128x64 tiles pipeline two stages deep (three workgroups per CU at ~169
+    // VGPRs), the others three.
+    constexpr int NSTAGE = BM == 128 && BN == 64 ? 2 : 3;
+    constexpr int kStages = NSTAGE * L::BYTES;
     constexpr int kSmem = MODE == GEMM_QKV_ROPE && BM * 512 > kStages ? BM * 512 : kStages;
     __shared__ __attribute__((aligned(16))) uint8_t smem[kSmem];
     uint8_t* const st0 = smem;
     uint8_t* const st1 = smem + L::BYTES;
-    uint8_t* const st2 = smem + 2 * L::BYTES;
+    uint8_t* const st2 = smem + (NSTAGE > 2 ? 2 : 0) * L::BYTES;
 
     const int K = p.w.cols, N = p.w.rows, M = p.M, nb = K >> 5, spitch = stage_scale_pitch(N);
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, tiles = tiles_m * tiles_n;
@@ -827,12 +830,27 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
         issue(lds_addr(refill), min(kt + 2, nk - 1));
         compute(cur);
     };
-    issue(lds_addr(st0), 0);
-    issue(lds_addr(st1), min(1, nk - 1));
-    for (int kt = 0; kt < nk; kt += 3) {
-        step(st0, st2, kt);
-        if (kt + 1 < nk) step(st1, st0, kt + 1);
-        if (kt + 2 < nk) step(st2, st1, kt + 2);
+    if constexpr (NSTAGE == 3) {
+        issue(lds_addr(st0), 0);
+        issue(lds_addr(st1), min(1, nk - 1));
+        for (int kt = 0; kt < nk; kt += 3) {
+            step(st0, st2, kt);
+            if (kt + 1 < nk) step(st1, st0, kt + 1);
+            if (kt + 2 < nk) step(st2, st1, kt + 2);
+        }
+    } else {
+        // wait for the stage (nothing else in flight), barrier (every wave is
+        // done with the other buffer), refill it with the next stage, multiply
+        auto step2 = [&](const uint8_t* cur, uint8_t* refill, int kt) {
+            wait_stage_barrier<0>();
+            issue(lds_addr(refill), min(kt + 1, nk - 1));
+            compute(cur);
+        };
+        issue(lds_addr(st0), 0);
+        for (int kt = 0; kt < nk; kt += 2) {
+            step2(st0, st1, kt);
+            if (kt + 1 < nk) step2(st1, st0, kt + 1);
+        }
     }
     // No DMA may still be writing this workgroup's LDS when its waves end.
     wait_stage_barrier<0>();
