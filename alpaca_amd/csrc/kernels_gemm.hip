@@ -908,7 +908,7 @@ int forced_tile() {
     return v;
 }
 
-// Tile choice: the largest tile whose grid still gives every CU a workgroup.
+// Tile choice, counted in rounds of resident workgroups over the 256 CUs.
 template <int FMT, int MODE>
 hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
     const int M = a.M, N = a.w.rows;
@@ -917,14 +917,17 @@ hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
     const int f = forced_tile();
     // The 256-row tiles hold more accumulators than the 256 architectural VGPRs
     // (344-353 with AGPR spills) and are slower wherever measured; they stay
-    // reachable through ALPACA_HIP_GEMM_TILE=256.  128x128 tiles (~190 VGPRs,
-    // two workgroups per CU) pay off once the grid has two per CU.
+    // reachable through ALPACA_HIP_GEMM_TILE=256.  128x64 tiles run three
+    // workgroups per CU (~169 VGPRs, two LDS stages) and are kept while their
+    // grid fits in one such round; past it (a near-empty second round, e.g. a
+    // 1600-column QKV over 4096 rows: 800 tiles for 768 slots) 128x128 tiles
+    // (~190 VGPRs, two per CU) are faster.
     if constexpr (MODE == GEMM_SWIGLU) {
         if (f == 1) return run_dgemm<FMT, 256, 64, 128, 32, MODE>(a, st);
         return run_dgemm<FMT, 128, 64, 64, 32, MODE>(a, st);
     } else {
         if (f == 1) return run_dgemm<FMT, 256, 128, 128, 64, MODE>(a, st);
-        if (f == 2 || (f == 0 && tiles(128, 128) >= 2 * kCUs)) return run_dgemm<FMT, 128, 128, 64, 64, MODE>(a, st);
+        if (f == 2 || (f == 0 && tiles(128, 64) > 3 * kCUs)) return run_dgemm<FMT, 128, 128, 64, 64, MODE>(a, st);
         return run_dgemm<FMT, 128, 64, 64, 32, MODE>(a, st);
     }
 }
