@@ -308,7 +308,7 @@ struct DecodeParams {
     unsigned long long* trace = nullptr;  // [decode_trace_points][grid] wall-clock stamps, or null
     long long timeout_ticks = 0;   // bound on every wait, in wall-clock ticks
     int abort_at_layer = -1;       // failure-path tests: workgroup 0 aborts the launch at this layer
-    int target_items = 64;         // attention work items to aim for
+    int target_items = 96;         // attention work items to aim for
     int max_splits = 1;            // splits per head the partial buffer holds
     int stage = 0;                 // floats of the LDS staging row
     // exchange-word offsets within one layer's block, and the block size

@@ -769,7 +769,7 @@ static int setup_persistent_decode(ahip_session* s) {
     p.embed = m->embed.m;
     p.out = m->out_matrix();
     p.out_norm = m->output_norm.as<float>();
-    p.target_items = std::max(1, env_int("ALPACA_HIP_DECODE_ITEMS", 64));
+    p.target_items = std::max(1, env_int("ALPACA_HIP_DECODE_ITEMS", 96));
     p.max_splits = decode_attention_max_splits(s->capacity, c.kv_head_count, p.target_items);
     p.stage = std::max(H, std::max(QW, F));
     p.off_part = QW + 2 * KW;
