@@ -10,6 +10,8 @@ import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libalpaca_hip.so")
+# the shim's test code object (ahip_module_load)
+SHIM_CODE_OBJECT = os.path.join(HERE, "shim_kernels.hsaco")
 
 OK, NO_DEVICE, MODULE_LOAD, MISSING_KERNEL, ALLOC, COMMAND_FAILED, UNSUPPORTED, INVALID_ARGUMENT, BUSY, GGUF = range(10)
 F32, F16, Q8_0, Q4_0 = 0, 1, 2, 3
@@ -160,6 +162,26 @@ SIGNATURES = {
     "ahip_memcpy_dtoh": (i, [vp, vp, vp, i64]),
     "ahip_memset": (i, [vp, vp, i, i64]),
     "ahip_synchronize": (i, [vp]),
+    "ahip_stream_create": (i, [vp, C.POINTER(vp)]),
+    "ahip_stream_destroy": (i, [vp]),
+    "ahip_stream_synchronize": (i, [vp]),
+    "ahip_stream_wait_event": (i, [vp, vp]),
+    "ahip_event_create": (i, [vp, C.POINTER(vp)]),
+    "ahip_event_destroy": (i, [vp]),
+    "ahip_event_record": (i, [vp, vp]),
+    "ahip_event_synchronize": (i, [vp]),
+    "ahip_event_elapsed_ms": (i, [vp, vp, fp]),
+    "ahip_host_alloc": (i, [vp, i64, C.POINTER(vp)]),
+    "ahip_host_free": (i, [vp, vp]),
+    "ahip_memcpy_htod_async": (i, [vp, vp, i64, vp]),
+    "ahip_memcpy_dtoh_async": (i, [vp, vp, i64, vp]),
+    "ahip_memcpy_dtod_async": (i, [vp, vp, i64, vp]),
+    "ahip_module_load": (i, [vp, C.c_char_p, C.POINTER(vp)]),
+    "ahip_module_load_data": (i, [vp, vp, C.POINTER(vp)]),
+    "ahip_module_unload": (i, [vp]),
+    "ahip_module_has_kernel": (i, [vp, C.c_char_p, C.POINTER(C.c_int)]),
+    "ahip_module_launch": (i, [vp, C.c_char_p, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.c_uint32, vp,
+                               C.POINTER(vp)]),
     "ahip_dev_pack_weight": (i, [vp, i, vp, i, i, C.POINTER(vp)]),
     "ahip_dev_weight_free": (i, [vp, vp]),
     "ahip_dev_gemv": (i, [vp, vp, vp, vp, i, dp]),

@@ -27,7 +27,7 @@ SOURCES = [("kernels_decode.hip", f"kernels_decode_{fmt}_hd{hd}",
            for fmt, hd in DECODE_VARIANTS]
 SOURCES += [(src, os.path.splitext(src)[0], []) for src in
             ("kernels_decode.hip", "kernels_misc.hip", "kernels_gemv.hip", "kernels_sample.hip", "runtime.cpp",
-             "gguf.cpp")]
+             "gguf.cpp", "shim.cpp")]
 # The prefill GEMMs scale each MFMA result on the VALU, and flash attention
 # rescales its output accumulators every key block; the VGPR form of the MFMA
 # keeps those results where the VALU reads them (the AGPR form adds a
@@ -57,11 +57,27 @@ def _compile(item) -> str:
     return obj
 
 
+# A stand-alone gfx950 code object for the shim's module-load tests.
+SHIM_SRC, SHIM_CO = "shim_kernels.hip", os.path.join(HERE, "shim_kernels.hsaco")
+
+
+def _code_object() -> str:
+    cmd = [hipcc(), "-O3", "-std=c++17", f"--offload-arch={ARCH}", "--genco", "-Xclang", "-target-feature",
+           "-Xclang", "-packed-fp32-ops", os.path.join(CSRC, SHIM_SRC), "-o", SHIM_CO + ".tmp"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"code object build failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(SHIM_CO + ".tmp", SHIM_CO)
+    return SHIM_CO
+
+
 def build(jobs: int = 0) -> str:
     os.makedirs(BUILD, exist_ok=True)
     jobs = jobs or min(8, os.cpu_count() or 1)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        co = ex.submit(_code_object)
         objs = list(ex.map(_compile, SOURCES))
+        co.result()
     tmp = LIB + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -675,18 +675,22 @@ __device__ __forceinline__ void qkv_rope_epilogue(const GemmArgs& p, const f32x4
     }
 }
 
-template <int FMT, int BM, int BN, int WM, int WN, int MODE>
+// RH: for GEMM_QKV_ROPE, the largest head dim the RoPE staging holds (64 or
+// 128); 0 for the other modes.
+template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH>
 __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
     using G = DGemm<FMT, BM, BN, WM, WN, MODE>;
     using L = DStage<FMT, BM, BN, G::NB>;
     constexpr int NB = G::NB, TM = G::TM, TN = G::TN, PER = G::PER;
-    // The three stage buffers, in one array that the GEMM_QKV_ROPE epilogue
-    // reuses for the tile's RoPE rows (BM positions x up to 64 pairs of 8 bytes).
+    // The stage buffers, in one array that the GEMM_QKV_ROPE epilogue reuses
+    // for the tile's RoPE rows (BM positions x RH/2 pairs of 8 bytes: 32 KB at
+    // head dim 64, so a 128x64 QKV tile keeps the two-stage footprint).
     // 128x64 tiles pipeline two stages deep (three workgroups per CU at ~169
     // VGPRs), the others three.
     constexpr int NSTAGE = BM == 128 && BN == 64 ? 2 : 3;
     constexpr int kStages = NSTAGE * L::BYTES;
-    constexpr int kSmem = MODE == GEMM_QKV_ROPE && BM * 512 > kStages ? BM * 512 : kStages;
+    constexpr int kRope = MODE == GEMM_QKV_ROPE ? BM * RH * 4 : 0;
+    constexpr int kSmem = kRope > kStages ? kRope : kStages;
     __shared__ __attribute__((aligned(16))) uint8_t smem[kSmem];
     uint8_t* const st0 = smem;
     uint8_t* const st1 = smem + L::BYTES;
@@ -887,57 +891,86 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
         }
 }
 
-template <int FMT, int BM, int BN, int WM, int WN, int MODE>
+template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH>
 hipError_t run_dgemm(const GemmArgs& a, hipStream_t st) {
     const int tiles = ((a.M + BM - 1) / BM) * ((a.w.rows + BN - 1) / BN);
-    dgemm_kernel<FMT, BM, BN, WM, WN, MODE><<<tiles, 256, 0, st>>>(a);
+    dgemm_kernel<FMT, BM, BN, WM, WN, MODE, RH><<<tiles, 256, 0, st>>>(a);
     return hipGetLastError();
 }
 
-// ALPACA_HIP_GEMM_TILE=256 | 128x128 | 128x64 forces a tile family (tuning);
-// 256 means 256x128 (256x64 per matrix for SwiGLU).
+// ALPACA_HIP_GEMM_TILE=256 | 128x128 | 128x64 forces a tile family (tuning and
+// tests; read on every launch); 256 means 256x128 (256x64 per matrix for
+// SwiGLU).
 int forced_tile() {
+    const char* e = std::getenv("ALPACA_HIP_GEMM_TILE");
+    if (!e) return 0;
+    if (!std::strcmp(e, "256")) return 1;
+    if (!std::strcmp(e, "128x128")) return 2;
+    if (!std::strcmp(e, "128x64")) return 3;
+    return 0;
+}
+
+// Compute units of the current device (cached per device id).
+int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+        cus[dev] = n > 0 ? n : 256;
+    }
+    return cus[dev];
+}
+
+// Resident workgroups per CU of one instantiation (registers and LDS as
+// compiled), asked once per process.
+template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH>
+int resident_per_cu() {
     static const int v = [] {
-        const char* e = std::getenv("ALPACA_HIP_GEMM_TILE");
-        if (!e) return 0;
-        if (!std::strcmp(e, "256")) return 1;
-        if (!std::strcmp(e, "128x128")) return 2;
-        if (!std::strcmp(e, "128x64")) return 3;
-        return 0;
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, dgemm_kernel<FMT, BM, BN, WM, WN, MODE, RH>, 256, 0) !=
+                hipSuccess || n < 1) {
+            hipGetLastError();
+            return 1;
+        }
+        return n;
     }();
     return v;
 }
 
-// Tile choice, counted in rounds of resident workgroups over the 256 CUs.
-template <int FMT, int MODE>
+// Tile choice, counted in rounds of resident workgroups over the device's CUs.
+template <int FMT, int MODE, int RH>
 hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
     const int M = a.M, N = a.w.rows;
     auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-    constexpr int kCUs = 256;
     const int f = forced_tile();
     // The 256-row tiles hold more accumulators than the 256 architectural VGPRs
     // (344-353 with AGPR spills) and are slower wherever measured; they stay
-    // reachable through ALPACA_HIP_GEMM_TILE=256.  128x64 tiles run three
-    // workgroups per CU (~169 VGPRs, two LDS stages) and are kept while their
-    // grid fits in one such round; past it (a near-empty second round, e.g. a
-    // 1600-column QKV over 4096 rows: 800 tiles for 768 slots) 128x128 tiles
-    // (~190 VGPRs, two per CU) are faster.
+    // reachable through ALPACA_HIP_GEMM_TILE=256.  128x64 tiles (~169 VGPRs,
+    // two LDS stages) are kept while their grid fits in one round of the
+    // workgroups the device holds at once; past it (a near-empty second round,
+    // e.g. a 1600-column QKV over 4096 rows) 128x128 tiles are faster.
     if constexpr (MODE == GEMM_SWIGLU) {
-        if (f == 1) return run_dgemm<FMT, 256, 64, 128, 32, MODE>(a, st);
-        return run_dgemm<FMT, 128, 64, 64, 32, MODE>(a, st);
+        if (f == 1) return run_dgemm<FMT, 256, 64, 128, 32, MODE, RH>(a, st);
+        return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH>(a, st);
     } else {
-        if (f == 1) return run_dgemm<FMT, 256, 128, 128, 64, MODE>(a, st);
-        if (f == 2 || (f == 0 && tiles(128, 64) > 3 * kCUs)) return run_dgemm<FMT, 128, 128, 64, 64, MODE>(a, st);
-        return run_dgemm<FMT, 128, 64, 64, 32, MODE>(a, st);
+        if (f == 1) return run_dgemm<FMT, 256, 128, 128, 64, MODE, RH>(a, st);
+        const int slots = resident_per_cu<FMT, 128, 64, 64, 32, MODE, RH>() * device_cus();
+        if (f == 2 || (f == 0 && tiles(128, 64) > slots)) return run_dgemm<FMT, 128, 128, 64, 64, MODE, RH>(a, st);
+        return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH>(a, st);
     }
 }
 
 template <int FMT>
 hipError_t dgemm_mode(const GemmArgs& a, int mode, hipStream_t st) {
-    if (mode == GEMM_STORE) return pick_dgemm<FMT, GEMM_STORE>(a, st);
-    if (mode == GEMM_ACC) return pick_dgemm<FMT, GEMM_ACC>(a, st);
-    if (mode == GEMM_QKV_ROPE) return pick_dgemm<FMT, GEMM_QKV_ROPE>(a, st);
-    return pick_dgemm<FMT, GEMM_SWIGLU>(a, st);
+    if (mode == GEMM_STORE) return pick_dgemm<FMT, GEMM_STORE, 0>(a, st);
+    if (mode == GEMM_ACC) return pick_dgemm<FMT, GEMM_ACC, 0>(a, st);
+    if (mode == GEMM_QKV_ROPE) {
+        if (a.qkv.hd <= 64) return pick_dgemm<FMT, GEMM_QKV_ROPE, 64>(a, st);
+        return pick_dgemm<FMT, GEMM_QKV_ROPE, 128>(a, st);
+    }
+    return pick_dgemm<FMT, GEMM_SWIGLU, 0>(a, st);
 }
 
 }  // namespace

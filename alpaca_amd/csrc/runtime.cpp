@@ -17,12 +17,14 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
 
 #include "../../include/alpaca_hip.h"
 #include "common.h"
+#include "host.h"
 
 // ------------------------------------------------------------------ errors
 
@@ -33,16 +35,25 @@ static int fail(int code, const std::string& msg) {
     return code;
 }
 
-#define HIP_OR(expr, what)                                                                                  \
-    do {                                                                                                    \
-        hipError_t e_ = (expr);                                                                             \
-        if (e_ != hipSuccess) return fail(AHIP_ERR_COMMAND_FAILED, std::string(what) + ": " + hipGetErrorString(e_)); \
+// A failed HIP call is also the thread's last HIP error, which later kernel
+// launches read back (hipGetLastError) to detect their own failure; both
+// macros clear it once the failure is reported.
+#define HIP_OR(expr, what)                                                                             \
+    do {                                                                                               \
+        hipError_t e_ = (expr);                                                                        \
+        if (e_ != hipSuccess) {                                                                        \
+            hipGetLastError();                                                                         \
+            return fail(AHIP_ERR_COMMAND_FAILED, std::string(what) + ": " + hipGetErrorString(e_));    \
+        }                                                                                              \
     } while (0)
 
-#define LAUNCH(expr)                                                                                          \
-    do {                                                                                                      \
-        hipError_t e_ = (expr);                                                                               \
-        if (e_ != hipSuccess) return fail(AHIP_ERR_COMMAND_FAILED, std::string("kernel launch: ") + hipGetErrorString(e_)); \
+#define LAUNCH(expr)                                                                                   \
+    do {                                                                                               \
+        hipError_t e_ = (expr);                                                                        \
+        if (e_ != hipSuccess) {                                                                        \
+            hipGetLastError();                                                                         \
+            return fail(AHIP_ERR_COMMAND_FAILED, std::string("kernel launch: ") + hipGetErrorString(e_)); \
+        }                                                                                              \
     } while (0)
 
 extern "C" const char* ahip_last_error(void) { return g_err.c_str(); }
@@ -225,11 +236,6 @@ extern "C" int ahip_device_count(int* count) {
     *count = n;
     return AHIP_OK;
 }
-
-struct ahip_context {
-    int device = 0;
-    hipStream_t stream = nullptr;
-};
 
 extern "C" int ahip_context_create(int device, ahip_context** out) {
     if (!out) return fail(AHIP_ERR_INVALID_ARGUMENT, "null out");
@@ -632,6 +638,7 @@ struct ahip_session {
     size_t pdec_lds = 0;
     DecodeParams pdec_params;
     DevBuf pdec_layers, pdec_xbuf, pdec_ctl;  // ctl: [0] epoch, [1] abort word
+    hipEvent_t pdec_peer = nullptr;          // recorded on another session's stream to order after it
     int64_t pdec_xbuf_bytes = 0;
     int* pdec_status = nullptr;              // mapped host word, set by an aborting launch
     uint64_t pdec_launches = 0;
@@ -660,6 +667,7 @@ struct ahip_session {
         if (emitted_host) hipHostFree(emitted_host);
         if (tokens_host) hipHostFree(tokens_host);
         if (pdec_status) hipHostFree(pdec_status);
+        if (pdec_peer) hipEventDestroy(pdec_peer);
         if (stream) hipStreamDestroy(stream);
     }
 
@@ -714,6 +722,23 @@ struct ahip_session {
     }
 };
 
+
+// Persistent decode launches of all sessions on one device run one at a time.
+// Each launch needs every one of its workgroups resident at once (one per CU,
+// cooperative), so two launches on two sessions' streams could each hold part
+// of the chip and spin in their bounded waits until both abort.  The device
+// remembers the stream of its last persistent launch; a launch from another
+// session first records an event at the tail of that stream and makes its own
+// stream wait for it (on the GPU; the host never blocks).  Consecutive launches
+// of one session are ordered by its stream alone and record nothing.
+namespace {
+struct PdecOrder {
+    std::mutex lock;
+    const ahip_session* last = nullptr;  // session of the device's last persistent launch
+    hipStream_t last_stream = nullptr;   // its stream
+};
+PdecOrder g_pdec_order[64];
+}  // namespace
 
 // ------------------------------------------------------------------ persistent decode setup
 
@@ -847,10 +872,12 @@ static int setup_persistent_decode(ahip_session* s) {
     s->pdec_fmt = fmt;
     s->pdec_grid = grid;
     s->pdec_lds = lds;
+    HIP_OR(hipEventCreateWithFlags(&s->pdec_peer, hipEventDisableTiming), "hipEventCreate");
     if (int rc = pdec_reset_words(s)) return rc;
     s->pdec = true;
     return AHIP_OK;
 }
+
 
 // Enqueues one persistent decode launch: the token in `chain` at position
 // *dpos; the arg-max goes to `chain` (and emitted[pos] when `emitted`), the
@@ -870,7 +897,15 @@ static int pdec_launch(ahip_session* s, bool logits, bool emitted) {
         HIP_OR(hipMemsetAsync(s->pdec_trace.p, 0, n * 8, s->stream), "clear trace");
         p.trace = s->pdec_trace.as<unsigned long long>();
     }
+    PdecOrder& order = g_pdec_order[s->m->device & 63];
+    std::lock_guard<std::mutex> g(order.lock);
+    if (order.last && order.last != s) {
+        HIP_OR(hipEventRecord(s->pdec_peer, order.last_stream), "hipEventRecord on the previous session's stream");
+        HIP_OR(hipStreamWaitEvent(s->stream, s->pdec_peer, 0), "order after another session");
+    }
     LAUNCH(launch_decode_step(s->pdec_fmt, p, s->pdec_grid, s->pdec_lds, s->pdec_coop, s->stream));
+    order.last = s;
+    order.last_stream = s->stream;
     s->pdec_launches++;
     return AHIP_OK;
 }
@@ -986,6 +1021,14 @@ extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, i
 extern "C" int ahip_session_destroy(ahip_session* s) {
     if (!s) return AHIP_OK;
     hipSetDevice(s->m->device);
+    {
+        PdecOrder& order = g_pdec_order[s->m->device & 63];
+        std::lock_guard<std::mutex> g(order.lock);
+        if (order.last == s) {
+            order.last = nullptr;
+            order.last_stream = nullptr;
+        }
+    }
     delete s;
     return AHIP_OK;
 }

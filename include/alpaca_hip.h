@@ -81,6 +81,7 @@ typedef struct {
 } ahip_tensor_desc;
 
 typedef struct ahip_context ahip_context;
+typedef struct ahip_stream ahip_stream;
 typedef struct ahip_model ahip_model;
 typedef struct ahip_session ahip_session;
 
@@ -355,6 +356,51 @@ int ahip_memcpy_htod(ahip_context* ctx, void* dst, const void* src, int64_t byte
 int ahip_memcpy_dtoh(ahip_context* ctx, void* dst, const void* src, int64_t bytes);
 int ahip_memset(ahip_context* ctx, void* dst, int value, int64_t bytes);
 int ahip_synchronize(ahip_context* ctx);
+
+typedef struct ahip_event ahip_event;
+
+/* Streams: the session's own command queue (MetalLlamaModel.swift:214-215
+ * makes one per session; MTLCommandQueue, MetalContext.swift:48-57), at the
+ * default priority.  _synchronize is commit + waitUntilCompleted. */
+int ahip_stream_create(ahip_context* ctx, ahip_stream** out);
+int ahip_stream_destroy(ahip_stream* s);
+int ahip_stream_synchronize(ahip_stream* s);
+/* Work queued on `s` after this call waits for `e` (command-buffer ordering
+ * across queues). */
+int ahip_stream_wait_event(ahip_stream* s, ahip_event* e);
+
+/* Events: the command buffer's gpuStartTime / gpuEndTime pair
+ * (MetalOps.swift:18-28, MetalLlamaModel.swift:255-260). */
+int ahip_event_create(ahip_context* ctx, ahip_event** out);
+int ahip_event_destroy(ahip_event* e);
+int ahip_event_record(ahip_event* e, ahip_stream* s);
+int ahip_event_synchronize(ahip_event* e);
+/* Milliseconds between two recorded events. */
+int ahip_event_elapsed_ms(const ahip_event* start, const ahip_event* end, float* ms);
+
+/* Pinned host memory for asynchronous copies (the shared-storage MTLBuffers of
+ * MetalContext.makeBuffer, MetalContext.swift:113-125, are host-visible). */
+int ahip_host_alloc(ahip_context* ctx, int64_t bytes, void** ptr);
+int ahip_host_free(ahip_context* ctx, void* ptr);
+/* Copies ordered on `s`; host buffers should be pinned (ahip_host_alloc). */
+int ahip_memcpy_htod_async(void* dst, const void* src, int64_t bytes, ahip_stream* s);
+int ahip_memcpy_dtoh_async(void* dst, const void* src, int64_t bytes, ahip_stream* s);
+int ahip_memcpy_dtod_async(void* dst, const void* src, int64_t bytes, ahip_stream* s);
+
+/* Code-object modules (MetalContext.compileLibrary + pipeline(name),
+ * MetalContext.swift:59-111): a gfx950 code object from a file or memory,
+ * kernels found by name (AHIP_ERR_MISSING_KERNEL = MetalError.missingFunction)
+ * and launched with hipModuleLaunchKernel.  `args` holds one pointer per kernel
+ * argument, to a value laid out as the kernel declares it.  The library ships
+ * one such object, shim_kernels.hsaco next to libalpaca_hip.so
+ * (ahip_shim_axpy, ahip_shim_fill_u32), for the shim's own tests. */
+typedef struct ahip_module ahip_module;
+int ahip_module_load(ahip_context* ctx, const char* path, ahip_module** out);
+int ahip_module_load_data(ahip_context* ctx, const void* image, ahip_module** out);
+int ahip_module_unload(ahip_module* m);
+int ahip_module_has_kernel(ahip_module* m, const char* name, int* found);
+int ahip_module_launch(ahip_module* m, const char* kernel, const uint32_t grid[3], const uint32_t block[3],
+                       uint32_t shared_bytes, ahip_stream* s, void** args);
 
 /* Device-resident kernel launches on the context stream, timed with HIP events
  * recorded on that stream around `iters` back-to-back launches: *avg_seconds

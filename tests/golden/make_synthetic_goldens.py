@@ -13,7 +13,19 @@ outputs on larger inputs so GPU runs can be checked without re-running it:
     minutes: a 256-token prompt, then 8 greedy steps.
   * C2 (seed 1): the two isolated Q8_0 GEMMs, M = 2048.
   * C3 (seed 2): causal GQA attention over T = 4096 after RoPE, and the
-    decode query at position 2048.
+    decode query at position 2047 over the L = 2048 visible cache rows.
+
+With --workloads it writes workload_goldens.npz instead: the model workloads
+exactly as bench.py times them, with full logit vectors (float32):
+
+  * C1L: C1 decode at context 2048: a 2045-token prompt, then 131 greedy
+    steps (3 that bring the context to 2048, then 128 timed ones);
+  * C4W: C4's 2048-token prompt, then 256 greedy steps (context 2048-2303);
+  * C5W: C5's 4096-token prompt, then 256 greedy steps (context 4096-4351).
+
+Per case: the greedy ids and top-2 margins of every step, and the full
+logits of the prefill (step 0) and of greedy steps 1-8 and the last one.
+The C5W prefill takes the oracle about half an hour on 8 cores.
 
 Model cases use an f16-rounded KV cache (the GPU default).  Recorded: SHA-256
 of the inputs (weights in GGUF block bytes, prompt ids), first and last 16
@@ -106,21 +118,82 @@ def c3_case() -> dict:
     k16 = kr.astype(np.float16).astype(np.float32)  # the cache holds f16 rows
     v32 = v.astype(np.float32)
     o = orc.attention(qr, k16, v32, 0)
-    # decode: the query of position 2048 over rows 0..2048 (L = 2049 visible) of the same cache
-    od = orc.attention(qr[2048:2049], k16[:2049], v32[:2049], 2048)
+    # decode: the query of position 2047 over rows 0..2047 (L = 2048 visible) of the same cache
+    od = orc.attention(qr[2047:2048], k16[:2048], v32[:2048], 2047)
     return {"tokens": q.shape[0], "heads": q.shape[1], "kv_heads": k.shape[1], "head_dim": q.shape[2],
             "theta": theta, "q_sha256": sha(q), "k_sha256": sha(k), "v_sha256": sha(v),
             "out_sample_stride": SAMPLE_STRIDE, "out_sample": sample(o),
-            "decode_position": 2048, "decode_out": od.ravel().astype(np.float64).tolist()}
+            "decode_position": 2047, "decode_visible_rows": 2048,
+            "decode_out": od.ravel().astype(np.float64).tolist()}
+
+
+# (key, spec, prompt length, greedy steps): the decode workloads bench.py times
+WORKLOAD_CASES = [("C1L", synth.C1, 2045, 131), ("C4W", synth.C4, 2048, 256), ("C5W", synth.C5, 4096, 256)]
+FULL_LOGIT_STEPS = 8  # greedy steps 1..8 (and the last) keep their full logits
+
+
+def workload_case(key, spec, n_prompt, n_greedy, log) -> dict:
+    c = spec.config
+    t0 = time.time()
+    w = synth.build_weights(spec)
+    om = orc.OracleModel(oracle_cfg(c), {n: (t.dtype, t.data) for n, t in w.items()})
+    prompt = synth.prompt_tokens(spec, n_prompt)
+    kv = orc.OracleKV(oracle_cfg(c), n_prompt + n_greedy + 1, rounds_f16=True)
+    logits = orc.forward(om, kv, prompt)
+    log(f"{key}: prefill of {n_prompt} tokens in {time.time() - t0:.0f} s")
+    keep_steps = [0] + list(range(1, FULL_LOGIT_STEPS + 1)) + [n_greedy]
+    kept = {0: logits.astype(np.float32)}
+    ids, margins = [int(orc.argmax(logits))], [top2(logits)]
+    # step i (1-based) feeds greedy id i-1 at position n_prompt + i - 1
+    for i in range(1, n_greedy + 1):
+        logits = orc.forward(om, kv, [ids[-1]])
+        if i in keep_steps:
+            kept[i] = logits.astype(np.float32)
+        ids.append(int(orc.argmax(logits)))
+        margins.append(top2(logits))
+        if i % 32 == 0:
+            log(f"{key}: {i} greedy steps, {time.time() - t0:.0f} s")
+    # ids[k] / margins[k] (k = 0..n_greedy): arg-max and top-2 margin of step
+    # k's logits (step 0 = the prefill); decode_greedy(ids[0], n_greedy) emits
+    # ids[1..n_greedy]
+    steps = sorted(kept)
+    return {f"{key}_ids": np.asarray(ids, np.int32), f"{key}_margins": np.asarray(margins, np.float64),
+            f"{key}_logit_steps": np.asarray(steps, np.int32),
+            f"{key}_logits": np.stack([kept[i] for i in steps]).astype(np.float32),
+            f"{key}_meta": np.array(json.dumps({
+                "spec": spec.name, "seed": spec.seed, "prompt_len": n_prompt, "greedy_steps": n_greedy,
+                "kv": "f16-rounded", "weights_sha256": weights_sha(spec, w),
+                "prompt_sha256": sha(prompt.astype(np.int32))}))}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--threads", type=int, default=os.cpu_count() or 1)
-    ap.add_argument("--out", default=os.path.join(HERE, "synthetic_goldens.json"))
+    ap.add_argument("--out", default=None)
+    ap.add_argument("--workloads", action="store_true", help="write workload_goldens.npz (long)")
+    ap.add_argument("--cases", default=",".join(k for k, *_ in WORKLOAD_CASES),
+                    help="workload cases to compute (with --workloads)")
     a = ap.parse_args()
     orc.build()
     orc.set_threads(a.threads)
+
+    def log(msg):
+        print(msg, flush=True)
+
+    if a.workloads:
+        out = a.out or os.path.join(HERE, "workload_goldens.npz")
+        arrays = {}
+        if os.path.exists(out):  # keep cases computed earlier
+            with np.load(out) as z:
+                arrays = {k: z[k] for k in z.files}
+        for key, spec, n_prompt, n_greedy in WORKLOAD_CASES:
+            if key not in a.cases.split(","):
+                continue
+            arrays.update(workload_case(key, spec, n_prompt, n_greedy, log))
+            np.savez_compressed(out, **arrays)
+            log(f"{key}: greedy {arrays[key + '_ids'][:12].tolist()}..., wrote {out}")
+        return
+    a.out = a.out or os.path.join(HERE, "synthetic_goldens.json")
     res = {"generator": "tests/golden/make_synthetic_goldens.py", "oracle": "oracle/alpaca_oracle.c", "models": {}}
     for key, spec, n_prompt, n_greedy in MODEL_CASES:
         t0 = time.time()

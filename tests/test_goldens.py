@@ -72,3 +72,30 @@ def test_oracle_reproduces_c2_golden():
     for case in golden()["c2"]:
         x, w = synth.c2_gemm_case(case["n"], case["k"])
         assert sha(orc.linear(x, w.dtype, w.data, case["n"])) == case["y_sha256"]
+
+
+WORKLOADS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "workload_goldens.npz")
+
+
+@pytest.mark.parametrize("key,spec,base", [("C1L", synth.C1, "C1"), ("C4W", synth.C4, "C4"), ("C5W", synth.C5, "C5")])
+def test_workload_goldens_describe_the_benched_inputs(key, spec, base):
+    """workload_goldens.npz (make_synthetic_goldens.py --workloads): the same
+    weights as the model goldens of the config, the bench's prompt (the
+    config's prompt stream, cut at the recorded length), one greedy id and
+    top-2 margin per step and full 49,152-logit rows for the prefill, steps
+    1-8 and the last step."""
+    import json
+    with np.load(WORKLOADS) as z:
+        if key + "_meta" not in z.files:
+            pytest.skip(f"{key} not computed")
+        meta = json.loads(str(z[key + "_meta"]))
+        ids, margins, steps, logits = (z[key + s] for s in ("_ids", "_margins", "_logit_steps", "_logits"))
+    n, g = meta["prompt_len"], meta["greedy_steps"]
+    assert meta["weights_sha256"] == golden()["models"][base]["weights_sha256"]
+    assert sha(synth.prompt_tokens(spec, n).astype(np.int32)) == meta["prompt_sha256"]
+    assert ids.shape == (g + 1,) and margins.shape == (g + 1,) and (margins >= 0).all()
+    assert steps.tolist() == [0] + list(range(1, 9)) + [g]
+    assert logits.shape == (len(steps), spec.config.vocab_size) and logits.dtype == np.float32
+    assert np.isfinite(logits).all()
+    # each kept row's arg-max is the recorded greedy id of its step
+    assert [int(np.argmax(r)) for r in logits] == [int(ids[s]) for s in steps]

@@ -187,3 +187,54 @@ def test_persistent_decode_abort_is_reported_and_session_recovers(hip_ctx):
     ref.forward(prompt)
     m = metrics(ok.decode(7), ref.decode(7))
     assert m["max_rel_peak"] <= 1e-4
+
+
+@pytest.mark.parametrize("spec", [synth.TINY, HD128_G4], ids=lambda s: s.name)
+def test_persistent_decode_multi_item_attention(hip_ctx, spec):
+    """More attention items than workgroups: each workgroup runs the item loop
+    of the attention phase several times, loading the next item's K rows into
+    registers and DMAing its V rows into the LDS buffer the current item has
+    just finished with.  Small grids (ALPACA_HIP_DECODE_WGS 4, 8, 16) and
+    item targets (ALPACA_HIP_DECODE_ITEMS 8, 24, 96) give 1-8 items per
+    workgroup with splits of 64, 128 and 256 positions; contexts sit on both
+    sides of those split lengths, including splits that hold only the current
+    position.  Each decode is held to the oracle (2e-3 + 1e-3) and to the
+    multi-kernel path (1e-4 of the logit peak).  Reference: the split-boundary
+    sweep of KernelTests.swift:123-144."""
+    c = spec.config
+    w = built(spec)
+    model = HIPLlamaModel(hip_ctx, c, w)
+    om = oracle_model(c, w)
+    cap = c.context_length  # 1024
+    prompt = synth.prompt_tokens(spec, cap)
+    contexts = (1, 65, 128, 129, 256, 257, 385, 512, 513, 769, 1023, cap)
+    with env(ALPACA_HIP_PERSISTENT_DECODE=0):
+        ref = model.make_session(capacity=cap, max_batch=512, gemm_precision="exact")
+    okv = orc.OracleKV(oracle_cfg(c), cap, rounds_f16=True)
+    want = {}
+    for p in contexts:
+        ref.reset()
+        okv.reset()
+        if p > 1:
+            ref.forward(prompt[: p - 1])
+            orc.forward(om, okv, prompt[: p - 1])
+        want[p] = (ref.decode(int(prompt[p - 1])), orc.forward(om, okv, [int(prompt[p - 1])]))
+    ref.close()
+    worst = 0.0
+    for wgs in (4, 8, 16):
+        for items in (8, 24, 96):
+            with env(ALPACA_HIP_DECODE_WGS=wgs, ALPACA_HIP_DECODE_ITEMS=items):
+                s = model.make_session(capacity=cap, max_batch=512, gemm_precision="exact")
+            for p in contexts:
+                s.reset()
+                if p > 1:
+                    s.forward(prompt[: p - 1])
+                g = s.decode(int(prompt[p - 1]))
+                r, e = want[p]
+                m = metrics(g, r)
+                worst = max(worst, m["max_rel_peak"])
+                assert m["max_rel_peak"] <= 1e-4, (wgs, items, p, m)
+                assert_close(g, e, 2e-3, 1e-3, f"{spec.name} wgs {wgs} items {items} context {p}")
+                assert s.length == p
+            s.close()
+    print(f"[metrics] {spec.name} multi-item attention: worst persistent vs multi-kernel peak-rel {worst:.2e}")

@@ -10,7 +10,7 @@ import pytest
 
 import oracle.oracle as orc
 from alpaca_amd.tensor import F16, Q4_0, Q8_0, encode
-from tests.helpers import assert_close, b64, fixture, metrics, splitmix_uniform
+from tests.helpers import assert_close, b64, env, fixture, metrics, splitmix_uniform
 
 pytestmark = pytest.mark.gpu
 
@@ -90,6 +90,44 @@ def test_fast_gemm_weights_enter_exactly(hip_ops, k, n, name, dt):
     assert gpu.shape == (k, n)
     bad = np.argwhere(gpu != deq.T)
     assert bad.size == 0, f"{name} K={k} N={n}: {len(bad)} weights differ, first at (k, n) = {bad[0]}"
+
+
+@pytest.mark.parametrize("name,dt", FORMATS)
+def test_gemm_tile_families_agree_at_large_grids(hip_ops, name, dt):
+    """M = 4096, K = 576, N = 1600 (C4's QKV width over a 4096-token prompt):
+    800 tiles of 128x64 are more than one round of resident workgroups, so the
+    default takes 128x128 tiles.  Every tile family (ALPACA_HIP_GEMM_TILE,
+    read per launch) accumulates each output over the same 32-weight blocks in
+    the same order, so the store, residual and SwiGLU epilogues must agree bit
+    for bit across 128x64, 128x128 and 256-row tiles.  The default is held to
+    the analytic fast-GEMM bound (KernelTests.swift:179-217), and one-hot
+    activation rows pin the weight path of every tile (Y[m] = W[:, m mod K]
+    exactly)."""
+    m, k, n = 4096, 576, 1600
+    w = encode(rand((n, k), 4242 + dt, 0.3), dt)
+    wu = encode(rand((n, k), 4343 + dt, 0.3), dt)
+    x = rand((m, k), 4244)
+    res = rand((m, n), 4245, 5)
+    onehot = np.zeros((m, k), np.float32)
+    onehot[np.arange(m), np.arange(m) % k] = 1.0
+    deq = orc.dequantize(dt, w.data, n * k).reshape(n, k)
+    outs = {}
+    for tile in (None, "128x64", "128x128", "256"):
+        with env(ALPACA_HIP_GEMM_TILE=tile):
+            outs[tile] = (hip_ops.linear(x, w, "fast"), hip_ops.linear_add(x, w, res, "fast"),
+                          hip_ops.gate_up_silu(x, w, wu, "fast"))
+            ident = hip_ops.linear(onehot, w, "fast")
+        bad = np.argwhere(ident != deq.T[np.arange(m) % k])
+        assert bad.size == 0, f"{name} tile {tile}: {len(bad)} weights differ, first at (m, n) = {bad[0]}"
+    for tile in ("128x64", "128x128", "256"):
+        for i, what in enumerate(("store", "residual", "swiglu")):
+            a, b = outs[tile][i], outs[None][i]
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{name} {what}: tile {tile} != default"
+    cpu = orc.linear(x, dt, w.data, n).astype(np.float64)
+    bound = np.abs(x.astype(np.float64)) @ np.abs(deq.astype(np.float64)).T / 1024 + 1e-5
+    err = np.abs(outs[None][0].astype(np.float64) - cpu)
+    print(f"[metrics] fast GEMM {name} M={m} K={k} N={n}: worst error / bound = {(err / bound).max():.3f}")
+    assert (err <= bound).all()
 
 
 def test_fused_gate_up_silu(hip_ops):  # KernelTests.swift:219-244

@@ -52,6 +52,37 @@ def test_fused_qkv_rope_is_bit_identical_to_unfused(hip_ctx, spec):
         tok = int(np.argmax(a))
 
 
+C4_LONG = replace(synth.C4, config=replace(synth.C4.config, layer_count=2, vocab_size=2048, context_length=4352),
+                  name="c4-shape-2l-4096")
+
+
+def test_fused_qkv_rope_with_large_tiles(hip_ctx):
+    """A 4096-token chunk at C4's layer shape: the QKV GEMM (N = 1600) has 800
+    tiles of 128x64, more than one round of resident workgroups, so it runs as
+    128x128 tiles with the RoPE epilogue (and the head-dim-64 RoPE staging).
+    Fused and unfused sessions agree bit for bit, and so do the tile families
+    forced through ALPACA_HIP_GEMM_TILE (read at every launch), since each
+    output accumulates the same blocks in the same order."""
+    spec = C4_LONG
+    model = HIPLlamaModel(hip_ctx, spec.config, built(spec))
+    prompt = synth.prompt_tokens(spec, 4096)
+    with env(ALPACA_HIP_FUSE_QKV_ROPE=0):
+        ref = model.make_session(capacity=4200, max_batch=4096, gemm_precision="fast")
+    fused = model.make_session(capacity=4200, max_batch=4096, gemm_precision="fast")
+    a, b = fused.forward(prompt), ref.forward(prompt)
+    assert np.array_equal(a, b), f"prefill logits differ: max |d| {np.abs(a - b).max():.3e}"
+    tok = int(np.argmax(a))
+    for step in range(2):
+        x, y = fused.decode(tok), ref.decode(tok)
+        assert np.array_equal(x, y), f"decode step {step} differs: max |d| {np.abs(x - y).max():.3e}"
+        tok = int(np.argmax(x))
+    for tile in ("128x64", "128x128"):
+        fused.reset()
+        with env(ALPACA_HIP_GEMM_TILE=tile):
+            t = fused.forward(prompt)
+        assert np.array_equal(t, a), f"tile {tile}: prefill logits differ: max |d| {np.abs(t - a).max():.3e}"
+
+
 # ------------------------------------------------------------------ prefill weight cache
 
 LAYER_MATS = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
