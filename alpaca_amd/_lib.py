@@ -152,6 +152,7 @@ SIGNATURES = {
     "ahip_op_argmax": (i, [vp, fp, i, ip]),
     "ahip_op_sample": (i, [vp, fp, i, C.c_float, i, C.c_float, C.c_double, ip]),
     "ahip_session_sample": (i, [vp, C.c_float, i, C.c_float, C.c_double, ip]),
+    "ahip_attention_decode_noalloc": (i, [vp, vp, vp, vp, i, i, i, i, i, i, vp, vp]),
     "ahip_quantize": (i, [i, fp, i64, vp]),
     "ahip_synth_uniform": (i, [C.c_uint64, C.c_uint64, i64, C.c_float, C.c_float, fp]),
     "ahip_synth_normal": (i, [C.c_uint64, C.c_uint64, i64, C.c_float, fp]),

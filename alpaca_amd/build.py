@@ -27,7 +27,7 @@ SOURCES = [("kernels_decode.hip", f"kernels_decode_{fmt}_hd{hd}",
            for fmt, hd in DECODE_VARIANTS]
 SOURCES += [(src, os.path.splitext(src)[0], []) for src in
             ("kernels_decode.hip", "kernels_misc.hip", "kernels_gemv.hip", "kernels_sample.hip", "runtime.cpp",
-             "gguf.cpp", "shim.cpp")]
+             "gguf.cpp", "shim.cpp", "noalloc.cpp")]
 # The prefill GEMMs scale each MFMA result on the VALU, and flash attention
 # rescales its output accumulators every key block; the VGPR form of the MFMA
 # keeps those results where the VALU reads them (the AGPR form adds a

@@ -19,5 +19,10 @@ struct ahip_stream {
     hipStream_t st = nullptr;
 };
 
+// Resolves, once per device and with that device current, the address of the
+// no-allocation entry point's scratch array (noalloc.cpp); called by
+// ahip_context_create.  Returns an ahip_status.
+int noalloc_scratch_init(int device);
+
 // Sets the thread-local message ahip_last_error() returns; returns `code`.
 int ahip_fail(int code, const std::string& msg);

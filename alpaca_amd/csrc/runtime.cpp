@@ -247,6 +247,7 @@ extern "C" int ahip_context_create(int device, ahip_context** out) {
     HIP_OR(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(AHIP_ERR_MODULE_LOAD, std::string("library is built for gfx950, device is ") + prop.gcnArchName);
+    if (int rc = noalloc_scratch_init(device)) return rc;
     auto* c = new ahip_context();
     c->device = device;
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {

@@ -330,6 +330,22 @@ int ahip_op_sample(ahip_context* ctx, const float* logits, int n, float temperat
                    double u, int32_t* token);
 int ahip_op_argmax(ahip_context* ctx, const float* logits, int n, int32_t* index);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, fixed serving loops, harnesses that
+ * forbid hipMalloc): the single-query case of ahip_op_attention (split-K
+ * attention over a KV cache, then the merge of the splits) on device buffers,
+ * allocating nothing.  q: [heads * head_dim] f32; k_cache / v_cache: the
+ * session layout [kv_heads][capacity][head_dim] in f16 (AHIP_KV_F16) or f32;
+ * rows 0..length-1 are visible; out: [heads * head_dim] f32.  Queued on
+ * `stream` (null: the context stream) without waiting.  The split partials go
+ * to a fixed 2.5 MiB device array per GPU (heads * splits * (head_dim + 2)
+ * floats, splits = ceil(length / max(128, ceil(capacity / 64) rounded up to
+ * 32))); larger shapes are AHIP_ERR_INVALID_ARGUMENT.  All calls on one GPU
+ * share that array: calls that overlap on one GPU race. */
+int ahip_attention_decode_noalloc(ahip_context* ctx, const float* q, const void* k_cache, const void* v_cache,
+                                  int kv_precision, int capacity, int heads, int kv_heads, int head_dim, int length,
+                                  float* out, ahip_stream* stream);
+
 /* Host block quantiser, Quantization.swift:39-73 (ggml quantize_row_*_ref):
  * count must be a multiple of 32; writes count/32 blocks into out. */
 int ahip_quantize(int dtype, const float* values, int64_t count, void* out);
