@@ -16,7 +16,7 @@ SHIM_CODE_OBJECT = os.path.join(HERE, "shim_kernels.hsaco")
 OK, NO_DEVICE, MODULE_LOAD, MISSING_KERNEL, ALLOC, COMMAND_FAILED, UNSUPPORTED, INVALID_ARGUMENT, BUSY, GGUF = range(10)
 F32, F16, Q8_0, Q4_0 = 0, 1, 2, 3
 KV_F16, KV_F32 = 0, 1
-GEMM_EXACT, GEMM_FAST = 0, 1
+GEMM_EXACT, GEMM_FAST, GEMM_FAST_F16 = 0, 1, 2
 
 STATUS_NAMES = {
     NO_DEVICE: "no device", MODULE_LOAD: "module load", MISSING_KERNEL: "missing kernel", ALLOC: "allocation",

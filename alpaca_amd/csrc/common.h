@@ -203,9 +203,11 @@ hipError_t launch_add(const float* a, const float* b, float* out, int64_t n, hip
 hipError_t launch_mul(const float* a, const float* b, float* out, int64_t n, hipStream_t st);
 hipError_t launch_silu(const float* x, float* out, int64_t n, hipStream_t st);
 hipError_t launch_silu_mul(const float* g, const float* u, float* out, int64_t n, hipStream_t st);
-hipError_t launch_f32_to_f16(const float* x, f16* out, int64_t n, hipStream_t st);
-hipError_t launch_rmsnorm(const float* x, const float* w, float* out_f32, f16* out_f16, int rows, int dim,
-                          float eps, hipStream_t st);
+// f16 outputs with a second-term pointer (lo) write hi = f16(v) and, when lo is
+// set, lo = f16(v - hi): the two-term activations of the MFMA prefill.
+hipError_t launch_f32_to_f16(const float* x, f16* out, f16* out_lo, int64_t n, hipStream_t st);
+hipError_t launch_rmsnorm(const float* x, const float* w, float* out_f32, f16* out_f16, f16* out_f16_lo, int rows,
+                          int dim, float eps, hipStream_t st);
 hipError_t launch_embed(const int32_t* tokens, int count, const DevMatrix& table, float* out, hipStream_t st);
 hipError_t launch_dequant(const DevMatrix& m, float* out, hipStream_t st);
 // f16 copy of a matrix (the prefill weight cache): f16(d*q) per weight, cols % 8 == 0.
@@ -222,8 +224,8 @@ hipError_t launch_argmax(const float* logits, int n, int32_t* chain_token, int32
 // place (q_f32) and/or written as f16 (q_f16); k rotated and v copied into the
 // caches at rows start..start+tokens-1.  k/v may be null (q-only RoPE).
 hipError_t launch_rope_store(float* qkv, int ld, int tokens, int heads, int kv_heads, int hd, int start,
-                             const float2* table, int interleaved, int write_q_f32, f16* q_f16, void* kcache,
-                             void* vcache, int kv_f16, int capacity, hipStream_t st);
+                             const float2* table, int interleaved, int write_q_f32, f16* q_f16, f16* q_f16_lo,
+                             void* kcache, void* vcache, int kv_f16, int capacity, hipStream_t st);
 
 // decode GEMV (kernels_gemv.hip)
 enum { GEMV_STORE = 0, GEMV_ADD = 1, GEMV_SWIGLU = 2, GEMV_QKV_ROPE = 3 };
@@ -256,10 +258,13 @@ hipError_t launch_gemv(const DevMatrix& w, const DevMatrix* w_up, const float* x
 
 // prefill GEMM (kernels_gemm.hip)
 enum { GEMM_STORE = 0, GEMM_ACC = 1, GEMM_SWIGLU = 2, GEMM_QKV_ROPE = 3 };
-// fast: x f16 [m][k] (row stride ldx); MFMA f16 with f32 accumulate.
-//   STORE/ACC write y f32 (row stride ldy); SWIGLU writes yh f16 (row stride ldy).
-hipError_t launch_gemm_mfma(const f16* x, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up, float* y,
-                            f16* yh, int ldy, int mode, hipStream_t st);
+// fast: x f16 [m][k] (row stride ldx); MFMA f16 with f32 accumulate.  With
+// xlo (the activations' second term, same layout) the activations enter as
+// x + xlo (two-term: float32-grade inputs at twice the MFMA work).
+//   STORE/ACC write y f32 (row stride ldy); SWIGLU writes yh f16 (row stride
+//   ldy), and with xlo its second term to yhlo.
+hipError_t launch_gemm_mfma(const f16* x, const f16* xlo, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up,
+                            float* y, f16* yh, f16* yhlo, int ldy, int mode, hipStream_t st);
 // The stacked [q|k|v] projection of m tokens at positions pos.. with the RoPE
 // (interleaved pairs) and KV-cache append in its epilogue: q rotated to qh f16
 // [m][heads*hd], k rotated and v copied to the f16 caches [kv_heads][capacity][hd].
@@ -268,11 +273,13 @@ hipError_t launch_gemm_mfma(const f16* x, int ldx, int m, const DevMatrix& w, co
 struct QkvRope {
     const float2* rope = nullptr;  // (cos, sin) [positions][hd/2]
     f16* qh = nullptr;
+    f16* qlo = nullptr;  // q's second term (two-term activations)
     f16* kc = nullptr;
     f16* vc = nullptr;
     int heads = 0, kv_heads = 0, hd = 0, pos = 0, capacity = 0;
 };
-hipError_t launch_gemm_qkv_rope(const f16* x, int ldx, int m, const DevMatrix& w, const QkvRope& o, hipStream_t st);
+hipError_t launch_gemm_qkv_rope(const f16* x, const f16* xlo, int ldx, int m, const DevMatrix& w, const QkvRope& o,
+                                hipStream_t st);
 // exact: x f32; float32 FMA in the reference's per-block order.  SWIGLU writes y f32.
 hipError_t launch_gemm_f32(const float* x, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up, float* y,
                            int ldy, int mode, hipStream_t st);
@@ -319,10 +326,13 @@ struct DecodeParams {
 // Phase-end stamps per launch: [0] start, 6 per layer (qkv, attention, merge,
 // wo, gate/up, down), then logits and the arg-max (workgroup 0 only).
 __host__ __device__ inline int decode_trace_points(int layers) { return 3 + 6 * layers; }
-// After those points, kDecodeAttnSubPoints stamps inside the attention item of
-// the last layer: entry, loads issued, q ready, current k/v ready, scores,
-// softmax, P.V, published.
-constexpr int kDecodeAttnSubPoints = 8;
+// After those points, kDecodeAttnSubPoints stamps inside the phases of the
+// last layer (the last value written wins): [0, 8) the attention item (entry,
+// loads issued, q ready, current k/v ready, scores, softmax, P.V, published);
+// then four per phase (entry, inputs arrived, inputs staged / normalised, rows
+// done) for QKV [8, 12), merge [12, 16), Wo [16, 20), gate/up [20, 24) and
+// down [24, 28).
+constexpr int kDecodeAttnSubPoints = 28;
 // Support, shared-memory size and launch of the persistent decode kernel.
 bool decode_kernel_supported(int fmt, int hd, int heads, int kv_heads);
 int decode_attention_max_splits(int capacity, int kv_heads, int target_items);
@@ -336,9 +346,12 @@ hipError_t launch_decode_step(int fmt, const DecodeParams& p, int grid, size_t l
 
 // attention (kernels_attention.hip).  Cache layout [kv_heads][capacity][hd].
 // q rows are [tokens][heads][hd] with row stride ldq (elements).
-hipError_t launch_flash_attention(const f16* q, int ldq, const f16* kc, const f16* vc, int capacity, int tokens,
-                                  int heads, int kv_heads, int hd, int start, float* out_f32, f16* out_f16,
-                                  hipStream_t st);
+// q (and with qlo its second term: two-term Q and P, float32-grade scores and
+// P.V) f16 [tokens][heads*hd]; writes out_f32, or out_f16 (with out_f16_lo the
+// second term when qlo is set).
+hipError_t launch_flash_attention(const f16* q, const f16* qlo, int ldq, const f16* kc, const f16* vc, int capacity,
+                                  int tokens, int heads, int kv_heads, int hd, int start, float* out_f32, f16* out_f16,
+                                  f16* out_f16_lo, hipStream_t st);
 // Generic online-softmax attention, any hd <= 256, f16 or f32 cache, keys
 // split into `splits` ranges merged by a second kernel when splits > 1.
 int attention_splits(int length, int heads, int tokens);

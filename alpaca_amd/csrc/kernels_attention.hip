@@ -16,7 +16,11 @@
 // so each lane owns one query column: the online-softmax max/sum need only
 // two cross-lane shuffles, and the probabilities already sit in the B-operand
 // layout of O^T += V^T P^T (the key order inside a 32-key MFMA step is
-// permuted identically on both operands).  P and V enter MFMA as f16;
+// permuted identically on both operands).  V enters MFMA as f16 (it is f16
+// in the cache); Q and P enter either as one f16 term each, or (TT, the
+// default prefill) as two, hi = f16(x) and lo = f16(x - hi), which carry them
+// to ~2^-22 so that scores and P.V keep float32 accuracy at twice the MFMA
+// work (P times 2^14 then, so that lo stays out of the f16 subnormals);
 // accumulation and the softmax statistics are float32.
 //
 // attn_generic_kernel: one wave per (query, head, key split) with an online
@@ -30,6 +34,7 @@ namespace {
 
 struct FlashArgs {
     const f16* q;
+    const f16* qlo;  // second term of q (TT)
     int ldq;
     const f16* kc;
     const f16* vc;
@@ -37,6 +42,7 @@ struct FlashArgs {
     float scale_log2;
     float* out32;
     f16* out16;
+    f16* out16lo;  // second term of the f16 output (TT)
 };
 
 constexpr int BQ = 64, BKV = 64;
@@ -72,7 +78,7 @@ __device__ __forceinline__ f16x4 lds_read_tr(const uint8_t* p) {
 // halving the sequential walk of the longest (causal) query blocks; the halves
 // merge at the end.  It costs LDS (one workgroup per CU), so the launcher uses
 // it only when one-set workgroups would not fill the chip.
-template <int HD, int NSET, bool OUT16>
+template <int HD, int NSET, bool OUT16, bool TT>
 __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
     static_assert(NSET == 1 || (NSET == 2 && HD == 64), "two wave-sets fit LDS at head dim 64 only");
     constexpr int KS = HD / 32, DT = HD / 16;
@@ -107,9 +113,16 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
     uint8_t* const st1 = set ? sB1 : sA1;
     uint8_t* const st2 = set ? sB2 : sA2;
 
-    f16x8 qf[KS];
+    // P enters the MFMA scaled by 2^14 in the two-term form (lo stays out of the
+    // f16 subnormals); the output's normalisation undoes it.
+    constexpr float kPScale = TT ? 16384.f : 1.f;
+    f16x8 qf[KS], ql[TT ? KS : 1];
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++) qf[ks] = *(const f16x8*)(a.q + (int64_t)qc * a.ldq + h * HD + 32 * ks + 8 * g);
+    for (int ks = 0; ks < KS; ks++) {
+        const int64_t qo = (int64_t)qc * a.ldq + h * HD + 32 * ks + 8 * g;
+        qf[ks] = *(const f16x8*)(a.q + qo);
+        if constexpr (TT) ql[ks] = *(const f16x8*)(a.qlo + qo);
+    }
 
     const int last_q = (qb + 1) * BQ < a.T ? (qb + 1) * BQ : a.T;
     const int kend = a.start + last_q;  // keys [0, kend) cover every query of this block
@@ -156,6 +169,7 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
             for (int ks = 0; ks < KS; ks++) {
                 const f16x8 kf = *(const f16x8*)(Kt + r * ROWB + (((4 * ks + g) ^ kv_swz(r)) * 16));
                 sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], sacc[t], 0, 0, 0);
+                if constexpr (TT) sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[ks], sacc[t], 0, 0, 0);
             }
         }
         // Masking only where some key of the block lies past some query of the wave.
@@ -179,15 +193,18 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
         // v_exp_f32 without the library's denormal-result path: values below
         // 2^-126 become 0, as they do anyway once P is rounded to f16.
         const float alpha = __builtin_amdgcn_exp2f(m - mref);
-        // The row sum takes the float32 probabilities; P enters the MFMA as f16.
+        // The row sum takes the float32 probabilities; P enters the MFMA as f16
+        // (hi, and lo with two terms).
         float ps = 0.f;
-        f16 ph[4][4];
+        f16 ph[4][4], pl[TT ? 4 : 1][4];
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const float e = __builtin_amdgcn_exp2f(fmaf(sacc[t][r], a.scale_log2, -mref));
-                ph[t][r] = (f16)e;
+                const float es = e * kPScale;
+                ph[t][r] = (f16)es;
+                if constexpr (TT) pl[t][r] = (f16)(es - (float)ph[t][r]);
                 ps += e;
             }
         lsum = lsum * alpha + ps;
@@ -199,6 +216,10 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
         for (int s = 0; s < 2; s++) {
             const f16x8 pf = {ph[2 * s][0], ph[2 * s][1], ph[2 * s][2], ph[2 * s][3],
                               ph[2 * s + 1][0], ph[2 * s + 1][1], ph[2 * s + 1][2], ph[2 * s + 1][3]};
+            f16x8 plf;
+            if constexpr (TT)
+                plf = f16x8{pl[2 * s][0], pl[2 * s][1], pl[2 * s][2], pl[2 * s][3],
+                            pl[2 * s + 1][0], pl[2 * s + 1][1], pl[2 * s + 1][2], pl[2 * s + 1][3]};
             const int ra = 32 * s + 4 * g + (c16 >> 2), rb = ra + 16;
 #pragma unroll
             for (int d = 0; d < DT; d++) {
@@ -207,6 +228,7 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
                 const f16x4 hi = lds_read_tr(Vt + rb * ROWB + ((cb ^ kv_swz(rb)) * 16) + hb);
                 const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 oacc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, oacc[d], 0, 0, 0);
+                if constexpr (TT) oacc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, plf, oacc[d], 0, 0, 0);
             }
         }
         m = mn;
@@ -275,15 +297,18 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
             for (int r = 0; r < 4; r++) oacc[d][r] = oacc[d][r] * a0 + xo[(d * 4 + r) * 64 + lane] * a1;
     }
     if (qi >= a.T) return;
-    const float inv = 1.0f / lsum;
+    const float inv = (1.0f / lsum) * (1.0f / kPScale);
     // oacc[d][r] = O(query qi, dim 16d + 4g + r)
 #pragma unroll
     for (int d = 0; d < DT; d++) {
         const int64_t o = ((int64_t)qi * a.H + h) * HD + 16 * d + 4 * g;
         if (OUT16) {
-            const f16x4 v = {(f16)(oacc[d][0] * inv), (f16)(oacc[d][1] * inv), (f16)(oacc[d][2] * inv),
-                             (f16)(oacc[d][3] * inv)};
+            const float o0 = oacc[d][0] * inv, o1 = oacc[d][1] * inv, o2 = oacc[d][2] * inv, o3 = oacc[d][3] * inv;
+            const f16x4 v = {(f16)o0, (f16)o1, (f16)o2, (f16)o3};
             *(f16x4*)(a.out16 + o) = v;
+            if constexpr (TT)
+                *(f16x4*)(a.out16lo + o) = f16x4{(f16)(o0 - (float)v[0]), (f16)(o1 - (float)v[1]),
+                                                 (f16)(o2 - (float)v[2]), (f16)(o3 - (float)v[3])};
         } else {
             *(float4*)(a.out32 + o) = make_float4(oacc[d][0] * inv, oacc[d][1] * inv, oacc[d][2] * inv,
                                                   oacc[d][3] * inv);
@@ -522,12 +547,36 @@ hipError_t decode_dispatch(int G, dim3 grid, hipStream_t st, const float* q, con
 
 }  // namespace
 
-hipError_t launch_flash_attention(const f16* q, int ldq, const f16* kc, const f16* vc, int capacity, int tokens,
-                                  int heads, int kv_heads, int hd, int start, float* out_f32, f16* out_f16,
-                                  hipStream_t st) {
+template <bool TT>
+hipError_t flash_dispatch(const FlashArgs& a, dim3 grid, int hd, bool out16, hipStream_t st) {
+    // One-set workgroups (48 KB of LDS at head dim 64) run three per CU: below
+    // three per CU the causal critical path dominates and two sets win.
+    const bool two_sets = (int64_t)grid.x * grid.y < 3 * 256;
+    if (hd == 64) {
+        if (two_sets) {
+            if (out16) flash_attn_kernel<64, 2, true, TT><<<grid, 512, 0, st>>>(a);
+            else flash_attn_kernel<64, 2, false, TT><<<grid, 512, 0, st>>>(a);
+        } else {
+            if (out16) flash_attn_kernel<64, 1, true, TT><<<grid, 256, 0, st>>>(a);
+            else flash_attn_kernel<64, 1, false, TT><<<grid, 256, 0, st>>>(a);
+        }
+    } else if (hd == 128) {
+        if (out16) flash_attn_kernel<128, 1, true, TT><<<grid, 256, 0, st>>>(a);
+        else flash_attn_kernel<128, 1, false, TT><<<grid, 256, 0, st>>>(a);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_flash_attention(const f16* q, const f16* qlo, int ldq, const f16* kc, const f16* vc, int capacity,
+                                  int tokens, int heads, int kv_heads, int hd, int start, float* out_f32, f16* out_f16,
+                                  f16* out_f16_lo, hipStream_t st) {
     if (tokens <= 0) return hipSuccess;
+    if (qlo && out_f16 && !out_f16_lo) return hipErrorInvalidValue;  // two-term in, two-term out
     FlashArgs a;
     a.q = q;
+    a.qlo = qlo;
     a.ldq = ldq;
     a.kc = kc;
     a.vc = vc;
@@ -539,25 +588,9 @@ hipError_t launch_flash_attention(const f16* q, int ldq, const f16* kc, const f1
     a.scale_log2 = 1.4426950408889634f / sqrtf((float)hd);
     a.out32 = out_f32;
     a.out16 = out_f16;
+    a.out16lo = out_f16_lo;
     dim3 grid(heads, (tokens + BQ - 1) / BQ);
-    // One-set workgroups (48 KB of LDS at head dim 64) run three per CU: below
-    // three per CU the causal critical path dominates and two sets win.
-    const bool two_sets = (int64_t)grid.x * grid.y < 3 * 256;
-    if (hd == 64) {
-        if (two_sets) {
-            if (out_f16) flash_attn_kernel<64, 2, true><<<grid, 512, 0, st>>>(a);
-            else flash_attn_kernel<64, 2, false><<<grid, 512, 0, st>>>(a);
-        } else {
-            if (out_f16) flash_attn_kernel<64, 1, true><<<grid, 256, 0, st>>>(a);
-            else flash_attn_kernel<64, 1, false><<<grid, 256, 0, st>>>(a);
-        }
-    } else if (hd == 128) {
-        if (out_f16) flash_attn_kernel<128, 1, true><<<grid, 256, 0, st>>>(a);
-        else flash_attn_kernel<128, 1, false><<<grid, 256, 0, st>>>(a);
-    } else {
-        return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
+    return qlo ? flash_dispatch<true>(a, grid, hd, out_f16, st) : flash_dispatch<false>(a, grid, hd, out_f16, st);
 }
 
 // Splits for the generic kernel: decode spreads the context over >= 64-key

@@ -6,13 +6,18 @@
 // KernelEncoder.swift:192-280.  CPU semantics: CPUOps.linear / dot
 // (CPUOps.swift:77-139).
 //
-// Fast path (f16 MFMA): f16 activations; quantised weights enter as their
-// integer quants in f16 (exact) with the per-block f16 scale kept in float32;
-// one v_mfma_f32_16x16x32_f16 covers one 32-weight block and its result is
-// scaled by d before accumulation, so the only rounding on the inputs is the
-// activations' (float32 -> f16).  (Rounding half(d*q) as the reference's
+// Fast path (f16 MFMA): quantised weights enter as their integer quants in f16
+// (exact) with the per-block f16 scale kept in float32; one
+// v_mfma_f32_16x16x32_f16 covers one 32-weight block and its result is scaled
+// by d before accumulation.  The activations enter either as one f16 term
+// (TT = false: the only input rounding is float32 -> f16, 2^-11 relative) or
+// as two, hi = f16(x) and lo = f16(x - hi) (TT = true), which carry x to
+// ~2^-22: both terms are multiplied by the same exact quants and summed in the
+// block's float32 result before the scaling, so the product keeps float32
+// accuracy at twice the MFMA work.  (Rounding half(d*q) as the reference's
 // tensor-op path does moves C1 prefill logits past the 2e-3 bound against the
-// CPU reference; exact quants keep them at 1.6e-3.)
+// CPU reference; single-term activations keep C1 inside it but not the larger
+// configurations.)
 //   dgemm_kernel: global -> LDS DMA, three stages in flight (the default).
 //   gemm_mfma_kernel: register-staged, double-buffered; shapes the DMA kernel
 //   does not take.
@@ -38,10 +43,12 @@ constexpr int LDT = BK + 8;  // LDS row pitch in halves (144 B: staggers banks)
 
 struct GemmArgs {
     const f16* x;
+    const f16* xlo = nullptr;  // the activations' second term (two-term kernels)
     int ldx, M;
     DevMatrix w, u;
     float* y;
     f16* yh;
+    f16* yhlo = nullptr;  // f16 outputs' second term (two-term kernels)
     int ldy;
     QkvRope qkv;  // GEMM_QKV_ROPE only (yh = qkv.qh, ldy = heads * hd)
 };
@@ -100,7 +107,7 @@ __device__ __forceinline__ void b_store(const BUnit<FMT>& u, int k, f16* dst, fl
     if (FMT != DT_F16 && (k & 16) == 0) *dscale = u.d;
 }
 
-template <int FMT, int BM, int BN, int MODE>
+template <int FMT, int BM, int BN, int MODE, bool TT>
 __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmArgs p) {
     constexpr int NB = MODE == GEMM_SWIGLU ? 2 : 1;
     constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16;
@@ -110,6 +117,7 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmArgs p) {
 
     constexpr bool kQuant = FMT != DT_F16;
     __shared__ __attribute__((aligned(16))) f16 As[2][BM][LDT];
+    __shared__ __attribute__((aligned(16))) f16 Al[TT ? 2 : 1][TT ? BM : 1][LDT];  // second term
     __shared__ __attribute__((aligned(16))) f16 Bs[2][NB][BN][LDT];
     __shared__ float Ds[2][NB][BN][BK / 32];  // block scales of the stage
 
@@ -119,7 +127,7 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmArgs p) {
     const int wm = wave >> 1, wn = wave & 1;
     const int nk = (K + BK - 1) / BK;
 
-    int4 ra[SA];
+    int4 ra[SA], rl[TT ? SA : 1];
     BUnit<FMT> rb[NB][UB];
 
     auto gload = [&](int kt) {
@@ -127,9 +135,13 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmArgs p) {
 #pragma unroll
         for (int i = 0; i < SA; i++) {
             const int seg = tid + 256 * i, r = seg >> 3, c = (seg & 7) * 8;
-            int4 v = {0, 0, 0, 0};
-            if (m0 + r < M && k0 + c < K) v = *(const int4*)(p.x + (int64_t)(m0 + r) * p.ldx + k0 + c);
+            int4 v = {0, 0, 0, 0}, vl = {0, 0, 0, 0};
+            if (m0 + r < M && k0 + c < K) {
+                v = *(const int4*)(p.x + (int64_t)(m0 + r) * p.ldx + k0 + c);
+                if constexpr (TT) vl = *(const int4*)(p.xlo + (int64_t)(m0 + r) * p.ldx + k0 + c);
+            }
             ra[i] = v;
+            if constexpr (TT) rl[i] = vl;
         }
 #pragma unroll
         for (int mat = 0; mat < NB; mat++)
@@ -150,6 +162,7 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmArgs p) {
         for (int i = 0; i < SA; i++) {
             const int seg = tid + 256 * i, r = seg >> 3, c = (seg & 7) * 8;
             *(int4*)&As[buf][r][c] = ra[i];
+            if constexpr (TT) *(int4*)&Al[buf][r][c] = rl[i];
         }
 #pragma unroll
         for (int mat = 0; mat < NB; mat++)
@@ -176,10 +189,12 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmArgs p) {
         if (kt + 1 < nk) gload(kt + 1);
 #pragma unroll
         for (int kk = 0; kk < BK / 32; kk++) {
-            f16x8 af[TM];
+            f16x8 af[TM], al[TT ? TM : 1];
 #pragma unroll
-            for (int i = 0; i < TM; i++)
+            for (int i = 0; i < TM; i++) {
                 af[i] = *(const f16x8*)&As[cur][wm * WM + 16 * i + (lane & 15)][32 * kk + 8 * (lane >> 4)];
+                if constexpr (TT) al[i] = *(const f16x8*)&Al[cur][wm * WM + 16 * i + (lane & 15)][32 * kk + 8 * (lane >> 4)];
+            }
 #pragma unroll
             for (int mat = 0; mat < NB; mat++)
 #pragma unroll
@@ -192,15 +207,19 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmArgs p) {
                         const float d = Ds[cur][mat][br][kk];
 #pragma unroll
                         for (int i = 0; i < TM; i++) {
-                            const f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                            f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                            if constexpr (TT) t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bf, t, 0, 0, 0);
                             acc[mat][i][j] += d * t;
                         }
                         // keep one column tile of block results live at a time (register budget)
                         __builtin_amdgcn_sched_barrier(0);
                     } else {
 #pragma unroll
-                        for (int i = 0; i < TM; i++)
+                        for (int i = 0; i < TM; i++) {
                             acc[mat][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, acc[mat][i][j], 0, 0, 0);
+                            if constexpr (TT)
+                                acc[mat][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bf, acc[mat][i][j], 0, 0, 0);
+                        }
                     }
                 }
         }
@@ -226,24 +245,27 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmArgs p) {
                     p.y[o] += acc[0][i][j][r];
                 } else {
                     const float g = acc[0][i][j][r], u = acc[NB - 1][i][j][r];
-                    p.yh[o] = (f16)((g / (1.0f + __expf(-g))) * u);
+                    const float v = (g / (1.0f + __expf(-g))) * u;
+                    const f16 hv = (f16)v;
+                    p.yh[o] = hv;
+                    if constexpr (TT) p.yhlo[o] = (f16)(v - (float)hv);
                 }
             }
         }
 }
 
-template <int FMT, int BM, int BN>
+template <int FMT, int BM, int BN, bool TT>
 hipError_t run_mfma(const GemmArgs& a, int mode, hipStream_t st) {
     dim3 grid((a.M + BM - 1) / BM, (a.w.rows + BN - 1) / BN);
-    if (mode == GEMM_STORE) gemm_mfma_kernel<FMT, BM, BN, GEMM_STORE><<<grid, 256, 0, st>>>(a);
-    else if (mode == GEMM_ACC) gemm_mfma_kernel<FMT, BM, BN, GEMM_ACC><<<grid, 256, 0, st>>>(a);
+    if (mode == GEMM_STORE) gemm_mfma_kernel<FMT, BM, BN, GEMM_STORE, TT><<<grid, 256, 0, st>>>(a);
+    else if (mode == GEMM_ACC) gemm_mfma_kernel<FMT, BM, BN, GEMM_ACC, TT><<<grid, 256, 0, st>>>(a);
     return hipGetLastError();
 }
 
-template <int FMT, int BM, int BN>
+template <int FMT, int BM, int BN, bool TT>
 hipError_t run_mfma_swiglu(const GemmArgs& a, hipStream_t st) {
     dim3 grid((a.M + BM - 1) / BM, (a.w.rows + BN - 1) / BN);
-    gemm_mfma_kernel<FMT, BM, BN, GEMM_SWIGLU><<<grid, 256, 0, st>>>(a);
+    gemm_mfma_kernel<FMT, BM, BN, GEMM_SWIGLU, TT><<<grid, 256, 0, st>>>(a);
     return hipGetLastError();
 }
 
@@ -251,16 +273,21 @@ hipError_t run_mfma_swiglu(const GemmArgs& a, hipStream_t st) {
 // otherwise 128 tokens x 64 rows (quantised formats keep two waves per SIMD
 // there: the per-block scaling holds a second set of MFMA results in
 // registers), and 128x128 for F16 weights when the grid covers the chip twice.
-template <int FMT>
+template <int FMT, bool TT>
 hipError_t pick_tile(const GemmArgs& a, int mode, hipStream_t st) {
     const int M = a.M, N = a.w.rows;
-    if (mode == GEMM_SWIGLU) return run_mfma_swiglu<FMT, 64, 64>(a, st);
-    if (M <= 64) return run_mfma<FMT, 64, 64>(a, mode, st);
+    if (mode == GEMM_SWIGLU) return run_mfma_swiglu<FMT, 64, 64, TT>(a, st);
+    if (M <= 64) return run_mfma<FMT, 64, 64, TT>(a, mode, st);
     const long big = (long)((M + 127) / 128) * ((N + 127) / 128);
     if constexpr (FMT == DT_F16) {
-        if (big >= 512) return run_mfma<FMT, 128, 128>(a, mode, st);
+        if (big >= 512) return run_mfma<FMT, 128, 128, TT>(a, mode, st);
     }
-    return run_mfma<FMT, 128, 64>(a, mode, st);
+    return run_mfma<FMT, 128, 64, TT>(a, mode, st);
+}
+
+template <int FMT>
+hipError_t pick_tile_terms(const GemmArgs& a, int mode, hipStream_t st) {
+    return a.xlo ? pick_tile<FMT, true>(a, mode, st) : pick_tile<FMT, false>(a, mode, st);
 }
 
 // ------------------------------------------------------------------ exact path
@@ -421,11 +448,14 @@ hipError_t run_f32(const GemmF32Args& a, int mode, hipStream_t st) {
 
 // Register-staged kernel: shapes the LDS-DMA kernel does not take (K not a
 // multiple of 64, activation rows not 16-byte aligned).
-static hipError_t launch_gemm_mfma_staged(const f16* x, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up,
-                                         float* y, f16* yh, int ldy, int mode, hipStream_t st) {
+static hipError_t launch_gemm_mfma_staged(const f16* x, const f16* xlo, int ldx, int m, const DevMatrix& w,
+                                         const DevMatrix* w_up, float* y, f16* yh, f16* yhlo, int ldy, int mode,
+                                         hipStream_t st) {
     if (m <= 0) return hipSuccess;
     GemmArgs a;
     a.x = x;
+    a.xlo = xlo;
+    a.yhlo = yhlo;
     a.ldx = ldx;
     a.M = m;
     a.w = w;
@@ -434,9 +464,9 @@ static hipError_t launch_gemm_mfma_staged(const f16* x, int ldx, int m, const De
     a.yh = yh;
     a.ldy = ldy;
     switch (w.dtype) {
-    case DT_Q8_0: return pick_tile<DT_Q8_0>(a, mode, st);
-    case DT_Q4_0: return pick_tile<DT_Q4_0>(a, mode, st);
-    default: return pick_tile<DT_F16>(a, mode, st);
+    case DT_Q8_0: return pick_tile_terms<DT_Q8_0>(a, mode, st);
+    case DT_Q4_0: return pick_tile_terms<DT_Q4_0>(a, mode, st);
+    default: return pick_tile_terms<DT_F16>(a, mode, st);
     }
 }
 
@@ -507,28 +537,30 @@ __device__ __forceinline__ int swz_a(int r) { return (r & 7) ^ ((r >> 1) & 4); }
 __device__ __forceinline__ int swz_q8(int r) { return (r >> 2) & 3; }
 __device__ __forceinline__ int swz_q4(int r) { return (r >> 3) & 1; }
 
-// Byte layout of one stage buffer: A rows, then each matrix's weight rows,
-// then each matrix's scales.
-template <int FMT, int BM, int BN, int NB>
+// Byte layout of one stage buffer: A rows (the second term's A rows after
+// them, two-term kernels), then each matrix's weight rows, then each matrix's
+// scales.
+template <int FMT, int BM, int BN, int NB, bool TT>
 struct DStage {
     static constexpr int BROW = FMT == DT_Q8_0 ? 64 : FMT == DT_Q4_0 ? 32 : 128;  // weight bytes per row
     static constexpr int SROW = FMT == DT_F16 ? 0 : 4;                             // scale bytes per row
-    static constexpr int B_OFF = BM * DBK * 2;
+    static constexpr int A_LO = BM * DBK * 2;
+    static constexpr int B_OFF = BM * DBK * 2 * (TT ? 2 : 1);
     static constexpr int S_OFF = B_OFF + NB * BN * BROW;
     static constexpr int BYTES = S_OFF + NB * BN * SROW + 16;
 };
 
-template <int FMT, int BM, int BN, int WM, int WN, int MODE>
+template <int FMT, int BM, int BN, int WM, int WN, int MODE, bool TT>
 struct DGemm {
     static constexpr int NB = MODE == GEMM_SWIGLU ? 2 : 1;
     static constexpr int TM = WM / 16, TN = WN / 16;
     static_assert((BM / WM) * (BN / WN) == 4, "four waves");
-    // DMA instructions per wave per stage
-    static constexpr int A_I = BM / 32;  // 8 rows of 128 B per instruction, 4 waves
+    // DMA instructions per wave per stage (A rows: 8 of 128 B per instruction, 4 waves; twice with two terms)
+    static constexpr int A_I = BM / 32;
     static constexpr bool Q4_16 = (BN / 32) % 4 == 0;
     static constexpr int B_I = FMT == DT_Q8_0 ? BN / 64 : FMT == DT_Q4_0 ? (Q4_16 ? BN / 128 : BN / 32) : BN / 32;
     static constexpr int S_I = FMT == DT_F16 ? 0 : 1;  // a quarter of the tile's scale pairs per wave
-    static constexpr int PER = A_I + NB * (B_I + S_I);
+    static constexpr int PER = A_I * (TT ? 2 : 1) + NB * (B_I + S_I);
     static_assert(BM % 32 == 0 && BN % 64 == 0, "tile shape");
 };
 
@@ -600,7 +632,7 @@ __device__ __forceinline__ void acc_epilogue(const GemmArgs& p, const f32x4 (&ac
 // odd lane (b = own, a = partner) b*c + a*s == a*s + b*c, so q/k are bit for
 // bit those of rope_store_kernel (CPUOps.rope, CPUOps.swift:184-212;
 // KVCache.write, KVCache.swift:44-63).  smem holds at least BM * hd/2 float2.
-template <int BM, int TM, int TN>
+template <int BM, int TM, int TN, bool TT>
 __device__ __forceinline__ void qkv_rope_epilogue(const GemmArgs& p, const f32x4 (&acc)[TM][TN], uint8_t* smem,
                                                   int m0, int mb, int nb, int M, int N, int lane) {
 #pragma clang fp contract(off)
@@ -634,9 +666,11 @@ __device__ __forceinline__ void qkv_rope_epilogue(const GemmArgs& p, const f32x4
         const int h = cn0 / hd, d = cn0 - h * hd + (lane & 15);
         // element (m, column) lives at dst + m * stride (a 32-bit offset: m < M, stride <= heads * hd)
         f16* dst;
+        f16* dlo = nullptr;  // q's second term (two-term kernels)
         int stride;
         if (region == 0) {
             dst = p.yh + g0 + (lane & 15);
+            if constexpr (TT) dlo = p.yhlo + g0 + (lane & 15);
             stride = p.ldy;
         } else {
             dst = (region == 1 ? o.kc : o.vc) + ((int64_t)h * o.capacity + o.pos) * hd + d;
@@ -661,7 +695,11 @@ __device__ __forceinline__ void qkv_rope_epilogue(const GemmArgs& p, const f32x4
                         const float t1 = out * cs.x, t2 = pv[r] * (odd ? cs.y : -cs.y);
                         out = t1 + t2;
                     }
-                    if (FULL || m < M) dst[m * stride] = (f16)out;
+                    if (FULL || m < M) {
+                        const f16 ho = (f16)out;
+                        dst[m * stride] = ho;
+                        if (TT && region == 0) dlo[m * stride] = (f16)(out - (float)ho);
+                    }
                 }
             }
         };
@@ -677,10 +715,10 @@ __device__ __forceinline__ void qkv_rope_epilogue(const GemmArgs& p, const f32x4
 
 // RH: for GEMM_QKV_ROPE, the largest head dim the RoPE staging holds (64 or
 // 128); 0 for the other modes.
-template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH>
+template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH, bool TT>
 __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
-    using G = DGemm<FMT, BM, BN, WM, WN, MODE>;
-    using L = DStage<FMT, BM, BN, G::NB>;
+    using G = DGemm<FMT, BM, BN, WM, WN, MODE, TT>;
+    using L = DStage<FMT, BM, BN, G::NB, TT>;
     constexpr int NB = G::NB, TM = G::TM, TN = G::TN, PER = G::PER;
     // The stage buffers, in one array that the GEMM_QKV_ROPE epilogue reuses
     // for the tile's RoPE rows (BM positions x RH/2 pairs of 8 bytes: 32 KB at
@@ -711,7 +749,9 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
 #pragma unroll
         for (int i = 0; i < G::A_I; i++) {
             const int r0 = (i * 4 + wave) * 8, r = r0 + (lane >> 3), c = (lane & 7) ^ swz_a(r);
-            dma16(p.x + (int64_t)min(m0 + r, M - 1) * p.ldx + k0 + c * 8, sg + r0 * DBK * 2);
+            const int64_t off = (int64_t)min(m0 + r, M - 1) * p.ldx + k0 + c * 8;
+            dma16(p.x + off, sg + r0 * DBK * 2);
+            if constexpr (TT) dma16(p.xlo + off, sg + L::A_LO + r0 * DBK * 2);
         }
 #pragma unroll
         for (int mat = 0; mat < NB; mat++) {
@@ -758,7 +798,7 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
     // is scaled by the block's d before it is accumulated.  The MFMAs of column
     // j+1 are issued before the scaling of column j, so the VALU work of one
     // column runs under the MFMAs of the next instead of waiting on them.
-    auto compute_block_quant = [&](const uint8_t* sg, int kk, const f16x8 (&af)[TM]) {
+    auto compute_block_quant = [&](const uint8_t* sg, int kk, const f16x8 (&af)[TM], const f16x8 (&al)[TT ? TM : 1]) {
         f16x8 bf[NB * TN];
         float d[NB * TN];
 #pragma unroll
@@ -784,13 +824,19 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
         }
         f32x4 prev[TM], cur[TM];
         const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        // the block's product: both activation terms times the exact quants, summed in float32
+        auto block = [&](int i, const f16x8& b) {
+            f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], b, zero, 0, 0, 0);
+            if constexpr (TT) t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b, t, 0, 0, 0);
+            return t;
+        };
 #pragma unroll
-        for (int i = 0; i < TM; i++) prev[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[0], zero, 0, 0, 0);
+        for (int i = 0; i < TM; i++) prev[i] = block(i, bf[0]);
 #pragma unroll
         for (int c = 1; c <= NB * TN; c++) {
             if (c < NB * TN) {
 #pragma unroll
-                for (int i = 0; i < TM; i++) cur[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[c], zero, 0, 0, 0);
+                for (int i = 0; i < TM; i++) cur[i] = block(i, bf[c]);
             }
             const int pc = c - 1, mat = pc / TN, j = pc % TN;
 #pragma unroll
@@ -802,11 +848,13 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
     auto compute = [&](const uint8_t* sg) {
 #pragma unroll
         for (int kk = 0; kk < 2; kk++) {
-            f16x8 af[TM];
+            f16x8 af[TM], al[TT ? TM : 1];
 #pragma unroll
             for (int i = 0; i < TM; i++) {
                 const int r = wm * WM + 16 * i + (lane & 15);
-                af[i] = *(const f16x8*)(sg + r * DBK * 2 + ((4 * kk + jj) ^ swz_a(r)) * 16);
+                const int o = r * DBK * 2 + ((4 * kk + jj) ^ swz_a(r)) * 16;
+                af[i] = *(const f16x8*)(sg + o);
+                if constexpr (TT) al[i] = *(const f16x8*)(sg + L::A_LO + o);
             }
 #pragma unroll
             for (int mat = 0; mat < NB; mat++)
@@ -817,11 +865,14 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
                     if constexpr (FMT == DT_F16) {
                         const f16x8 bf = *(const f16x8*)(bq + r * 128 + ((4 * kk + jj) ^ swz_a(r)) * 16);
 #pragma unroll
-                        for (int i = 0; i < TM; i++)
+                        for (int i = 0; i < TM; i++) {
                             acc[mat][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, acc[mat][i][j], 0, 0, 0);
+                            if constexpr (TT)
+                                acc[mat][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bf, acc[mat][i][j], 0, 0, 0);
+                        }
                     }
                 }
-            if constexpr (FMT != DT_F16) compute_block_quant(sg, kk, af);
+            if constexpr (FMT != DT_F16) compute_block_quant(sg, kk, af, al);
         }
     };
 
@@ -859,7 +910,7 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
     // No DMA may still be writing this workgroup's LDS when its waves end.
     wait_stage_barrier<0>();
     if constexpr (MODE == GEMM_QKV_ROPE) {
-        qkv_rope_epilogue<BM, TM, TN>(p, acc[0], smem, m0, m0 + wm * WM, n0 + wn * WN, M, N, lane);
+        qkv_rope_epilogue<BM, TM, TN, TT>(p, acc[0], smem, m0, m0 + wm * WM, n0 + wn * WN, M, N, lane);
         return;
     }
     if constexpr (MODE == GEMM_ACC) {
@@ -885,16 +936,19 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
                     p.y[o] += acc[0][i][j][r];
                 } else {
                     const float g = acc[0][i][j][r], u = acc[NB - 1][i][j][r];
-                    p.yh[o] = (f16)((g / (1.0f + __expf(-g))) * u);
+                    const float v = (g / (1.0f + __expf(-g))) * u;
+                    const f16 hv = (f16)v;
+                    p.yh[o] = hv;
+                    if constexpr (TT) p.yhlo[o] = (f16)(v - (float)hv);
                 }
             }
         }
 }
 
-template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH>
+template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH, bool TT>
 hipError_t run_dgemm(const GemmArgs& a, hipStream_t st) {
     const int tiles = ((a.M + BM - 1) / BM) * ((a.w.rows + BN - 1) / BN);
-    dgemm_kernel<FMT, BM, BN, WM, WN, MODE, RH><<<tiles, 256, 0, st>>>(a);
+    dgemm_kernel<FMT, BM, BN, WM, WN, MODE, RH, TT><<<tiles, 256, 0, st>>>(a);
     return hipGetLastError();
 }
 
@@ -925,11 +979,11 @@ int device_cus() {
 
 // Resident workgroups per CU of one instantiation (registers and LDS as
 // compiled), asked once per process.
-template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH>
+template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH, bool TT>
 int resident_per_cu() {
     static const int v = [] {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, dgemm_kernel<FMT, BM, BN, WM, WN, MODE, RH>, 256, 0) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, dgemm_kernel<FMT, BM, BN, WM, WN, MODE, RH, TT>, 256, 0) !=
                 hipSuccess || n < 1) {
             hipGetLastError();
             return 1;
@@ -940,7 +994,7 @@ int resident_per_cu() {
 }
 
 // Tile choice, counted in rounds of resident workgroups over the device's CUs.
-template <int FMT, int MODE, int RH>
+template <int FMT, int MODE, int RH, bool TT>
 hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
     const int M = a.M, N = a.w.rows;
     auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
@@ -951,40 +1005,52 @@ hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
     // two LDS stages) are kept while their grid fits in one round of the
     // workgroups the device holds at once; past it (a near-empty second round,
     // e.g. a 1600-column QKV over 4096 rows) 128x128 tiles are faster.
+    // (The 256-row tiles do not fit LDS with two activation terms.)
     if constexpr (MODE == GEMM_SWIGLU) {
-        if (f == 1) return run_dgemm<FMT, 256, 64, 128, 32, MODE, RH>(a, st);
-        return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH>(a, st);
+        if constexpr (!TT)
+            if (f == 1) return run_dgemm<FMT, 256, 64, 128, 32, MODE, RH, TT>(a, st);
+        return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH, TT>(a, st);
     } else {
-        if (f == 1) return run_dgemm<FMT, 256, 128, 128, 64, MODE, RH>(a, st);
-        const int slots = resident_per_cu<FMT, 128, 64, 64, 32, MODE, RH>() * device_cus();
-        if (f == 2 || (f == 0 && tiles(128, 64) > slots)) return run_dgemm<FMT, 128, 128, 64, 64, MODE, RH>(a, st);
-        return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH>(a, st);
+        if constexpr (!TT)
+            if (f == 1) return run_dgemm<FMT, 256, 128, 128, 64, MODE, RH, TT>(a, st);
+        const int slots = resident_per_cu<FMT, 128, 64, 64, 32, MODE, RH, TT>() * device_cus();
+        if (f == 2 || (f == 0 && tiles(128, 64) > slots)) return run_dgemm<FMT, 128, 128, 64, 64, MODE, RH, TT>(a, st);
+        return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH, TT>(a, st);
     }
+}
+
+template <int FMT, bool TT>
+hipError_t dgemm_mode_terms(const GemmArgs& a, int mode, hipStream_t st) {
+    if (mode == GEMM_STORE) return pick_dgemm<FMT, GEMM_STORE, 0, TT>(a, st);
+    if (mode == GEMM_ACC) return pick_dgemm<FMT, GEMM_ACC, 0, TT>(a, st);
+    if (mode == GEMM_QKV_ROPE) {
+        if (a.qkv.hd <= 64) return pick_dgemm<FMT, GEMM_QKV_ROPE, 64, TT>(a, st);
+        return pick_dgemm<FMT, GEMM_QKV_ROPE, 128, TT>(a, st);
+    }
+    return pick_dgemm<FMT, GEMM_SWIGLU, 0, TT>(a, st);
 }
 
 template <int FMT>
 hipError_t dgemm_mode(const GemmArgs& a, int mode, hipStream_t st) {
-    if (mode == GEMM_STORE) return pick_dgemm<FMT, GEMM_STORE, 0>(a, st);
-    if (mode == GEMM_ACC) return pick_dgemm<FMT, GEMM_ACC, 0>(a, st);
-    if (mode == GEMM_QKV_ROPE) {
-        if (a.qkv.hd <= 64) return pick_dgemm<FMT, GEMM_QKV_ROPE, 64>(a, st);
-        return pick_dgemm<FMT, GEMM_QKV_ROPE, 128>(a, st);
-    }
-    return pick_dgemm<FMT, GEMM_SWIGLU, 0>(a, st);
+    return a.xlo ? dgemm_mode_terms<FMT, true>(a, mode, st) : dgemm_mode_terms<FMT, false>(a, mode, st);
 }
 
 }  // namespace
 
-hipError_t launch_gemm_mfma(const f16* x, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up, float* y,
-                            f16* yh, int ldy, int mode, hipStream_t st) {
+hipError_t launch_gemm_mfma(const f16* x, const f16* xlo, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up,
+                            float* y, f16* yh, f16* yhlo, int ldy, int mode, hipStream_t st) {
     if (m <= 0) return hipSuccess;
+    if (mode == GEMM_SWIGLU && xlo && !yhlo) return hipErrorInvalidValue;  // two-term in, two-term out
     // The DMA kernel needs 64-wide K stages, 16-byte aligned activation rows and,
     // for quantised weights, the stage-major scales.
     const bool quant = w.dtype != DT_F16;
-    if (w.cols % DBK || ldx % 8 || ((uintptr_t)x & 15) || (quant && (!w.s2 || (w_up && !w_up->s2))))
-        return launch_gemm_mfma_staged(x, ldx, m, w, w_up, y, yh, ldy, mode, st);
+    if (w.cols % DBK || ldx % 8 || ((uintptr_t)x & 15) || ((uintptr_t)xlo & 15) ||
+        (quant && (!w.s2 || (w_up && !w_up->s2))))
+        return launch_gemm_mfma_staged(x, xlo, ldx, m, w, w_up, y, yh, yhlo, ldy, mode, st);
     GemmArgs a;
     a.x = x;
+    a.xlo = xlo;
+    a.yhlo = yhlo;
     a.ldx = ldx;
     a.M = m;
     a.w = w;
@@ -999,16 +1065,20 @@ hipError_t launch_gemm_mfma(const f16* x, int ldx, int m, const DevMatrix& w, co
     }
 }
 
-hipError_t launch_gemm_qkv_rope(const f16* x, int ldx, int m, const DevMatrix& w, const QkvRope& o, hipStream_t st) {
+hipError_t launch_gemm_qkv_rope(const f16* x, const f16* xlo, int ldx, int m, const DevMatrix& w, const QkvRope& o,
+                                hipStream_t st) {
     if (m <= 0) return hipSuccess;
     const bool quant = w.dtype != DT_F16;
     // the pipelined kernel's conditions (as in launch_gemm_mfma); RoPE pairs and
-    // 16-column lane groups must not straddle a head
-    if (w.cols % DBK || ldx % 8 || ((uintptr_t)x & 15) || (quant && !w.s2) || o.hd % 16 || o.hd > 128 || o.heads <= 0 ||
-        o.kv_heads <= 0 || w.rows != (o.heads + 2 * o.kv_heads) * o.hd || !o.rope || !o.qh || !o.kc || !o.vc)
+    // 16-column lane groups must not straddle a head; two-term in, two-term q out
+    if (w.cols % DBK || ldx % 8 || ((uintptr_t)x & 15) || ((uintptr_t)xlo & 15) || (quant && !w.s2) || o.hd % 16 ||
+        o.hd > 128 || o.heads <= 0 || o.kv_heads <= 0 || w.rows != (o.heads + 2 * o.kv_heads) * o.hd || !o.rope ||
+        !o.qh || !o.kc || !o.vc || (xlo && !o.qlo))
         return hipErrorNotSupported;
     GemmArgs a;
     a.x = x;
+    a.xlo = xlo;
+    a.yhlo = o.qlo;
     a.ldx = ldx;
     a.M = m;
     a.w = w;

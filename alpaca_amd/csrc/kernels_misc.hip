@@ -34,15 +34,22 @@ __global__ void silu_mul_kernel(const float* g, const float* u, float* o, int64_
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
         o[i] = silu_f(g[i]) * u[i];
 }
-__global__ void f32_to_f16_kernel(const float* x, f16* o, int64_t n) {
+// hi = f16(v) to o, and with ol the remainder lo = f16(v - hi): hi + lo holds v
+// to ~2^-22 relative (the two-term activations of the MFMA prefill).
+__device__ __forceinline__ void store_terms(f16* o, f16* ol, int64_t i, float v) {
+    const f16 h = (f16)v;
+    o[i] = h;
+    if (ol) ol[i] = (f16)(v - (float)h);
+}
+__global__ void f32_to_f16_kernel(const float* x, f16* o, f16* ol, int64_t n) {
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-        o[i] = (f16)x[i];
+        store_terms(o, ol, i, x[i]);
 }
 
 // CPUOps.rmsNorm (CPUOps.swift:144-159): y = x * (1/sqrt(mean(x^2) + eps)) * w,
 // one block per row, optionally writing f16 for the MFMA GEMM.
 __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const float* x, const float* w, float* of, f16* oh,
-                                                         int dim, float eps) {
+                                                         f16* ol, int dim, float eps) {
     __shared__ float red[16];
     const float* xr = x + (int64_t)blockIdx.x * dim;
     float ss = 0.f;
@@ -52,7 +59,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const float* x, const f
     for (int i = threadIdx.x; i < dim; i += kBlock) {
         float y = (xr[i] * scale) * w[i];
         if (of) of[(int64_t)blockIdx.x * dim + i] = y;
-        if (oh) oh[(int64_t)blockIdx.x * dim + i] = (f16)y;
+        if (oh) store_terms(oh, ol, (int64_t)blockIdx.x * dim + i, y);
     }
 }
 
@@ -61,7 +68,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const float* x, const f
 // 8-byte f16 stores, and no block barrier.
 constexpr int kNormV4 = 8;
 __global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(const float* x, const float* w, float* of, f16* oh,
-                                                              int rows, int dim, float eps) {
+                                                              f16* ol, int rows, int dim, float eps) {
     const int row = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= rows) return;  // whole waves leave together
     const int n4 = dim >> 2;
@@ -90,7 +97,11 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(const float* x, co
         if (of) ((float4*)(of + (int64_t)row * dim))[i] = y;
         if (oh) {
             typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-            ((h4*)(oh + (int64_t)row * dim))[i] = h4{(f16)y.x, (f16)y.y, (f16)y.z, (f16)y.w};
+            const h4 hi = {(f16)y.x, (f16)y.y, (f16)y.z, (f16)y.w};
+            ((h4*)(oh + (int64_t)row * dim))[i] = hi;
+            if (ol)
+                ((h4*)(ol + (int64_t)row * dim))[i] = h4{(f16)(y.x - (float)hi[0]), (f16)(y.y - (float)hi[1]),
+                                                         (f16)(y.z - (float)hi[2]), (f16)(y.w - (float)hi[3])};
         }
     }
 }
@@ -184,7 +195,8 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, int n
 template <typename KV>
 __global__ __launch_bounds__(kBlock) void rope_store_kernel(float* qkv, int ld, int heads, int kv_heads, int hd,
                                                             int start, const float2* table, int interleaved,
-                                                            int write_q, f16* q16, KV* kc, KV* vc, int capacity) {
+                                                            int write_q, f16* q16, f16* q16lo, KV* kc, KV* vc,
+                                                            int capacity) {
 #pragma clang fp contract(off)
     int t = blockIdx.x;
     int half = hd / 2;
@@ -203,9 +215,9 @@ __global__ __launch_bounds__(kBlock) void rope_store_kernel(float* qkv, int ld, 
             float ra = ac - bs, rb = as + bc;
             if (write_q) { p[ia] = ra; p[ib] = rb; }
             if (q16) {
-                f16* o = q16 + ((int64_t)t * heads + y) * hd;
-                o[ia] = (f16)ra;
-                o[ib] = (f16)rb;
+                const int64_t o = ((int64_t)t * heads + y) * hd;
+                store_terms(q16, q16lo, o + ia, ra);
+                store_terms(q16, q16lo, o + ib, rb);
             }
         } else {
             int h = y - heads;
@@ -240,17 +252,17 @@ hipError_t launch_silu_mul(const float* g, const float* u, float* out, int64_t n
     if (n > 0) silu_mul_kernel<<<grid_for(n), kBlock, 0, st>>>(g, u, out, n);
     return hipGetLastError();
 }
-hipError_t launch_f32_to_f16(const float* x, f16* out, int64_t n, hipStream_t st) {
-    if (n > 0) f32_to_f16_kernel<<<grid_for(n), kBlock, 0, st>>>(x, out, n);
+hipError_t launch_f32_to_f16(const float* x, f16* out, f16* out_lo, int64_t n, hipStream_t st) {
+    if (n > 0) f32_to_f16_kernel<<<grid_for(n), kBlock, 0, st>>>(x, out, out_lo, n);
     return hipGetLastError();
 }
-hipError_t launch_rmsnorm(const float* x, const float* w, float* of, f16* oh, int rows, int dim, float eps,
+hipError_t launch_rmsnorm(const float* x, const float* w, float* of, f16* oh, f16* ol, int rows, int dim, float eps,
                           hipStream_t st) {
     if (rows <= 0) return hipSuccess;
     const bool vec = dim % 4 == 0 && dim <= 64 * 4 * kNormV4 && !((uintptr_t)x & 15) && !((uintptr_t)w & 15) &&
-                     !((uintptr_t)of & 15) && !((uintptr_t)oh & 7);
-    if (vec) rmsnorm_rows_kernel<<<(rows + 3) / 4, kBlock, 0, st>>>(x, w, of, oh, rows, dim, eps);
-    else rmsnorm_kernel<<<rows, kBlock, 0, st>>>(x, w, of, oh, dim, eps);
+                     !((uintptr_t)of & 15) && !((uintptr_t)oh & 7) && !((uintptr_t)ol & 7);
+    if (vec) rmsnorm_rows_kernel<<<(rows + 3) / 4, kBlock, 0, st>>>(x, w, of, oh, ol, rows, dim, eps);
+    else rmsnorm_kernel<<<rows, kBlock, 0, st>>>(x, w, of, oh, ol, dim, eps);
     return hipGetLastError();
 }
 hipError_t launch_embed(const int32_t* tokens, int count, const DevMatrix& table, float* out, hipStream_t st) {
@@ -275,16 +287,16 @@ hipError_t launch_argmax(const float* logits, int n, int32_t* chain, int32_t* em
     return hipGetLastError();
 }
 hipError_t launch_rope_store(float* qkv, int ld, int tokens, int heads, int kv_heads, int hd, int start,
-                             const float2* table, int interleaved, int write_q_f32, f16* q_f16, void* kcache,
-                             void* vcache, int kv_f16, int capacity, hipStream_t st) {
+                             const float2* table, int interleaved, int write_q_f32, f16* q_f16, f16* q_f16_lo,
+                             void* kcache, void* vcache, int kv_f16, int capacity, hipStream_t st) {
     if (tokens <= 0) return hipSuccess;
     if (kv_f16)
         rope_store_kernel<f16><<<tokens, kBlock, 0, st>>>(qkv, ld, heads, kv_heads, hd, start, table, interleaved,
-                                                          write_q_f32, q_f16, (f16*)kcache, (f16*)vcache,
+                                                          write_q_f32, q_f16, q_f16_lo, (f16*)kcache, (f16*)vcache,
                                                           capacity);
     else
         rope_store_kernel<float><<<tokens, kBlock, 0, st>>>(qkv, ld, heads, kv_heads, hd, start, table,
-                                                            interleaved, write_q_f32, q_f16, (float*)kcache,
+                                                            interleaved, write_q_f32, q_f16, q_f16_lo, (float*)kcache,
                                                             (float*)vcache, capacity);
     return hipGetLastError();
 }

@@ -58,6 +58,12 @@ static int fail(int code, const std::string& msg) {
 
 extern "C" const char* ahip_last_error(void) { return g_err.c_str(); }
 
+// Kernel launches report their failure through hipGetLastError(), which also
+// returns an error left by an earlier, unrelated HIP call of this thread
+// (a failed teardown call, say).  Entry points that launch work start from a
+// clean state.
+static inline void drop_stale_error() { (void)hipGetLastError(); }
+
 // For the library's other host sources (gguf.cpp).
 int ahip_fail(int code, const std::string& msg) { return fail(code, msg); }
 
@@ -264,6 +270,7 @@ extern "C" int ahip_context_destroy(ahip_context* c) {
     hipStreamSynchronize(c->stream);
     hipStreamDestroy(c->stream);
     delete c;
+    drop_stale_error();
     return AHIP_OK;
 }
 
@@ -410,6 +417,10 @@ static std::vector<float2> rope_table(int positions, int hd, float theta) {
 // ------------------------------------------------------------------ model
 
 struct ahip_model {
+    // The creator's reference plus one per live session: a model outlives its
+    // sessions (MetalLlamaSession holds its MetalLlamaModel), whatever order the
+    // caller destroys them in.
+    std::atomic<int> refs{1};
     ahip_context* ctx = nullptr;
     int device = 0;  // kept so destruction never touches a destroyed context
     ahip_llama_config c{};
@@ -457,6 +468,7 @@ int ahip_validate_config(const ahip_llama_config* c) { return validate_config(c)
 extern "C" int ahip_model_create(ahip_context* ctx, const ahip_llama_config* config, const ahip_tensor_desc* tensors,
                                  int count, int prefill_weight_cache, ahip_model** out) {
     if (!ctx || !out || (count && !tensors)) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
+    drop_stale_error();
     if (int rc = validate_config(config)) return rc;
     const ahip_llama_config& c = *config;
     std::map<std::string, const ahip_tensor_desc*> byname;
@@ -560,10 +572,16 @@ extern "C" int ahip_model_create(ahip_context* ctx, const ahip_llama_config* con
     return AHIP_OK;
 }
 
-extern "C" int ahip_model_destroy(ahip_model* m) {
-    if (!m) return AHIP_OK;
+static void model_release(ahip_model* m) {
+    if (m->refs.fetch_sub(1) != 1) return;
     hipSetDevice(m->device);
     delete m;
+    drop_stale_error();
+}
+
+extern "C" int ahip_model_destroy(ahip_model* m) {
+    if (!m) return AHIP_OK;
+    model_release(m);
     return AHIP_OK;
 }
 
@@ -599,8 +617,9 @@ static SessionSizes session_sizes(const ahip_llama_config& c, int capacity, int 
     s.ffn = B * c.feed_forward_size;
     s.partials = (int64_t)c.head_count * kMaxSplits * (c.head_dim + 2);
     s.logits = c.vocab_size;
+    // the f16 activation buffers hold two planes (the two-term activations' hi and lo)
     s.total = 2 * c.layer_count * s.kv_per_layer + 4 * (2 * s.x + s.qkv + s.ctx + s.ffn + s.partials + s.logits) +
-              2 * (s.x + s.q16 + s.ctx + s.ffn) + 4 * ((int64_t)capacity + 9 + capacity);
+              4 * (s.x + s.q16 + s.ctx + s.ffn) + 4 * ((int64_t)capacity + 9 + capacity);
     return s;
 }
 
@@ -620,7 +639,12 @@ struct StageMark {
 struct ahip_session {
     ahip_model* m = nullptr;
     int capacity = 0, max_batch = 0, kv_f16 = 1, fast = 1;
+    int two_term = 1;  // fast prefill with two-term activations (AHIP_GEMM_FAST); 0: one f16 term (FAST_F16)
     int fuse_qkv_rope = 1;  // ALPACA_HIP_FUSE_QKV_ROPE at creation; 0: RoPE + KV append as their own kernel
+    // Numerics diagnostics, read at creation: ALPACA_HIP_PREFILL_ATTENTION=generic runs the fast prefill's
+    // attention as the float32 kernel the exact prefill uses; ALPACA_HIP_PREFILL_GEMM=f32 its projections as
+    // the exact float32 GEMMs.
+    int prefill_generic_attention = 0, prefill_f32_gemm = 0;
     bool logits_ready = false;  // `logits` holds the last forward's logits (for ahip_session_sample)
     DevBuf sample_idx, sample_p, sample_out;  // sampler scratch, allocated on first use
     hipStream_t stream = nullptr;
@@ -973,9 +997,11 @@ static int pdec_check(ahip_session* s) {
 extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, int kv_precision, int gemm_precision,
                                    ahip_session** out) {
     if (!m || !out) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
+    drop_stale_error();
     if (capacity <= 0 || max_batch <= 0) return fail(AHIP_ERR_INVALID_ARGUMENT, "capacity and maxBatch must be positive");
     if (kv_precision != AHIP_KV_F16 && kv_precision != AHIP_KV_F32) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad kv precision");
-    if (gemm_precision != AHIP_GEMM_EXACT && gemm_precision != AHIP_GEMM_FAST) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad gemm precision");
+    if (gemm_precision != AHIP_GEMM_EXACT && gemm_precision != AHIP_GEMM_FAST && gemm_precision != AHIP_GEMM_FAST_F16)
+        return fail(AHIP_ERR_INVALID_ARGUMENT, "bad gemm precision");
     const ahip_llama_config& c = m->c;
     capacity = std::min(capacity, c.context_length);
     max_batch = std::min(max_batch, capacity);
@@ -985,8 +1011,15 @@ extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, i
     s->capacity = capacity;
     s->max_batch = max_batch;
     s->kv_f16 = kv_precision == AHIP_KV_F16;
-    s->fast = gemm_precision == AHIP_GEMM_FAST;
+    s->fast = gemm_precision != AHIP_GEMM_EXACT;
+    s->two_term = gemm_precision == AHIP_GEMM_FAST;
     s->fuse_qkv_rope = env_int("ALPACA_HIP_FUSE_QKV_ROPE", 1) != 0;
+    {
+        const char* a = std::getenv("ALPACA_HIP_PREFILL_ATTENTION");
+        const char* g = std::getenv("ALPACA_HIP_PREFILL_GEMM");
+        s->prefill_generic_attention = a && !std::strcmp(a, "generic");
+        s->prefill_f32_gemm = g && !std::strcmp(g, "f32");
+    }
     HIP_OR(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate");
     const SessionSizes z = session_sizes(c, capacity, max_batch, s->kv_f16);
     for (int l = 0; l < c.layer_count; l++) {
@@ -996,8 +1029,8 @@ extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, i
         if (int rc = s->vc.back()->alloc(z.kv_per_layer)) return rc;
     }
     struct A { DevBuf* b; int64_t n; };
-    for (A a : {A{&s->x, z.x * 4}, A{&s->xn, z.x * 4}, A{&s->xh, z.x * 2}, A{&s->qkv, z.qkv * 4}, A{&s->qh, z.q16 * 2},
-                A{&s->ctx, z.ctx * 4}, A{&s->ctxh, z.ctx * 2}, A{&s->ffn, z.ffn * 4}, A{&s->ffnh, z.ffn * 2},
+    for (A a : {A{&s->x, z.x * 4}, A{&s->xn, z.x * 4}, A{&s->xh, z.x * 4}, A{&s->qkv, z.qkv * 4}, A{&s->qh, z.q16 * 4},
+                A{&s->ctx, z.ctx * 4}, A{&s->ctxh, z.ctx * 4}, A{&s->ffn, z.ffn * 4}, A{&s->ffnh, z.ffn * 4},
                 A{&s->partials, z.partials * 4}, A{&s->logits, z.logits * 4}, A{&s->tokens, (int64_t)capacity * 4},
                 A{&s->chain, 64}, A{&s->dpos, 64}})
         if (int rc = a.b->alloc(a.n)) return rc;
@@ -1015,6 +1048,7 @@ extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, i
     if (int rc = setup_persistent_decode(s.get())) return rc;
     HIP_OR(hipEventCreate(&s->ev_begin), "hipEventCreate");
     HIP_OR(hipEventCreate(&s->ev_end), "hipEventCreate");
+    m->refs.fetch_add(1);
     *out = s.release();
     return AHIP_OK;
 }
@@ -1030,7 +1064,10 @@ extern "C" int ahip_session_destroy(ahip_session* s) {
             order.last_stream = nullptr;
         }
     }
+    ahip_model* m = s->m;
     delete s;
+    drop_stale_error();
+    model_release(m);
     return AHIP_OK;
 }
 
@@ -1125,8 +1162,14 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
     const float2* rope = m->rope.as<float2>();
     s->stage("embed");
     LAUNCH(launch_embed(dtok, n, m->embed.m, x, st));
-    const bool mfma = s->fast && n >= 16;
-    const bool flash = mfma && s->kv_f16 && (hd == 64 || hd == 128);
+    const bool mfma = s->fast && n >= 16 && !s->prefill_f32_gemm;
+    const bool flash = s->fast && n >= 16 && !s->prefill_generic_attention && s->kv_f16 && (hd == 64 || hd == 128);
+    // Second-term planes of the f16 activation buffers (two-term prefill), after the first planes.
+    const int64_t B = s->max_batch;
+    f16* xhlo = s->two_term ? s->xh.as<f16>() + B * H : nullptr;
+    f16* qhlo = s->two_term ? s->qh.as<f16>() + B * QW : nullptr;
+    f16* ctxhlo = s->two_term ? s->ctxh.as<f16>() + B * QW : nullptr;
+    f16* ffnhlo = s->two_term ? s->ffnh.as<f16>() + B * F : nullptr;
     for (int li = 0; li < c.layer_count; li++) {
         ahip_model::Layer& L = *m->layers[li];
         void* kc = s->kc[li]->p;
@@ -1136,7 +1179,7 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
         } else if (mfma) {
             f16* xh = s->xh.as<f16>();
             s->stage("rmsnorm");
-            LAUNCH(launch_rmsnorm(x, L.attn_norm.as<float>(), nullptr, xh, n, H, c.rms_norm_eps, st));
+            LAUNCH(launch_rmsnorm(x, L.attn_norm.as<float>(), nullptr, xh, xhlo, n, H, c.rms_norm_eps, st));
             s->stage("qkv projections");
             hipError_t fused = hipErrorNotSupported;
             if (flash && s->fuse_qkv_rope) {
@@ -1144,6 +1187,7 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
                 QkvRope o;
                 o.rope = rope;
                 o.qh = s->qh.as<f16>();
+                o.qlo = qhlo;
                 o.kc = (f16*)kc;
                 o.vc = (f16*)vc;
                 o.heads = c.head_count;
@@ -1151,51 +1195,61 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
                 o.hd = hd;
                 o.pos = pos;
                 o.capacity = s->capacity;
-                fused = launch_gemm_qkv_rope(xh, H, n, L.pre(L.qkv, L.qkv16), o, st);
+                fused = launch_gemm_qkv_rope(xh, xhlo, H, n, L.pre(L.qkv, L.qkv16), o, st);
                 if (fused != hipErrorNotSupported) LAUNCH(fused);
             }
             if (fused == hipErrorNotSupported) {
-                LAUNCH(launch_gemm_mfma(xh, H, n, L.pre(L.qkv, L.qkv16), nullptr, qkv, nullptr, LDQKV, GEMM_STORE, st));
+                LAUNCH(launch_gemm_mfma(xh, xhlo, H, n, L.pre(L.qkv, L.qkv16), nullptr, qkv, nullptr, nullptr, LDQKV,
+                                        GEMM_STORE, st));
                 s->stage("rope + kv store");
                 LAUNCH(launch_rope_store(qkv, LDQKV, n, c.head_count, c.kv_head_count, hd, pos, rope, 1,
-                                         flash ? 0 : 1, flash ? s->qh.as<f16>() : nullptr, kc, vc, s->kv_f16,
-                                         s->capacity, st));
+                                         flash ? 0 : 1, flash ? s->qh.as<f16>() : nullptr, flash ? qhlo : nullptr, kc,
+                                         vc, s->kv_f16, s->capacity, st));
             }
             s->stage("attention");
             if (flash) {
-                LAUNCH(launch_flash_attention(s->qh.as<f16>(), QW, (const f16*)kc, (const f16*)vc, s->capacity, n,
-                                              c.head_count, c.kv_head_count, hd, pos, nullptr, s->ctxh.as<f16>(), st));
+                LAUNCH(launch_flash_attention(s->qh.as<f16>(), qhlo, QW, (const f16*)kc, (const f16*)vc, s->capacity,
+                                              n, c.head_count, c.kv_head_count, hd, pos, nullptr, s->ctxh.as<f16>(),
+                                              ctxhlo, st));
             } else {
                 LAUNCH(launch_attention_generic(qkv, LDQKV, kc, vc, s->kv_f16, s->capacity, n, c.head_count,
                                                 c.kv_head_count, hd, pos, 1, nullptr, s->ctx.as<float>(), st));
-                LAUNCH(launch_f32_to_f16(s->ctx.as<float>(), s->ctxh.as<f16>(), (int64_t)n * QW, st));
+                LAUNCH(launch_f32_to_f16(s->ctx.as<float>(), s->ctxh.as<f16>(), ctxhlo, (int64_t)n * QW, st));
             }
             s->stage("attn out projection (+residual)");
-            LAUNCH(launch_gemm_mfma(s->ctxh.as<f16>(), QW, n, L.pre(L.wo, L.wo16), nullptr, x, nullptr, H, GEMM_ACC, st));
+            LAUNCH(launch_gemm_mfma(s->ctxh.as<f16>(), ctxhlo, QW, n, L.pre(L.wo, L.wo16), nullptr, x, nullptr, nullptr,
+                                    H, GEMM_ACC, st));
             s->stage("rmsnorm");
-            LAUNCH(launch_rmsnorm(x, L.ffn_norm.as<float>(), nullptr, xh, n, H, c.rms_norm_eps, st));
+            LAUNCH(launch_rmsnorm(x, L.ffn_norm.as<float>(), nullptr, xh, xhlo, n, H, c.rms_norm_eps, st));
             s->stage("ffn gate+up+silu");
-            LAUNCH(launch_gemm_mfma(xh, H, n, L.pre(L.gate, L.gate16), &L.pre(L.up, L.up16), nullptr, s->ffnh.as<f16>(),
-                                    F, GEMM_SWIGLU, st));
+            LAUNCH(launch_gemm_mfma(xh, xhlo, H, n, L.pre(L.gate, L.gate16), &L.pre(L.up, L.up16), nullptr,
+                                    s->ffnh.as<f16>(), ffnhlo, F, GEMM_SWIGLU, st));
             s->stage("ffn down (+residual)");
-            LAUNCH(launch_gemm_mfma(s->ffnh.as<f16>(), F, n, L.pre(L.down, L.down16), nullptr, x, nullptr, H, GEMM_ACC,
-                                    st));
+            LAUNCH(launch_gemm_mfma(s->ffnh.as<f16>(), ffnhlo, F, n, L.pre(L.down, L.down16), nullptr, x, nullptr,
+                                    nullptr, H, GEMM_ACC, st));
         } else {
             float* xn = s->xn.as<float>();
             s->stage("rmsnorm");
-            LAUNCH(launch_rmsnorm(x, L.attn_norm.as<float>(), xn, nullptr, n, H, c.rms_norm_eps, st));
+            LAUNCH(launch_rmsnorm(x, L.attn_norm.as<float>(), xn, nullptr, nullptr, n, H, c.rms_norm_eps, st));
             s->stage("qkv projections");
             LAUNCH(launch_gemm_f32(xn, H, n, L.qkv.m, nullptr, qkv, LDQKV, GEMM_STORE, st));
             s->stage("rope + kv store");
-            LAUNCH(launch_rope_store(qkv, LDQKV, n, c.head_count, c.kv_head_count, hd, pos, rope, 1, 1, nullptr, kc,
-                                     vc, s->kv_f16, s->capacity, st));
+            LAUNCH(launch_rope_store(qkv, LDQKV, n, c.head_count, c.kv_head_count, hd, pos, rope, 1, flash ? 0 : 1,
+                                     flash ? s->qh.as<f16>() : nullptr, flash ? qhlo : nullptr, kc, vc, s->kv_f16,
+                                     s->capacity, st));
             s->stage("attention");
-            LAUNCH(launch_attention_generic(qkv, LDQKV, kc, vc, s->kv_f16, s->capacity, n, c.head_count,
-                                            c.kv_head_count, hd, pos, 1, nullptr, s->ctx.as<float>(), st));
+            if (flash) {
+                LAUNCH(launch_flash_attention(s->qh.as<f16>(), qhlo, QW, (const f16*)kc, (const f16*)vc, s->capacity,
+                                              n, c.head_count, c.kv_head_count, hd, pos, s->ctx.as<float>(), nullptr,
+                                              nullptr, st));
+            } else {
+                LAUNCH(launch_attention_generic(qkv, LDQKV, kc, vc, s->kv_f16, s->capacity, n, c.head_count,
+                                                c.kv_head_count, hd, pos, 1, nullptr, s->ctx.as<float>(), st));
+            }
             s->stage("attn out projection (+residual)");
             LAUNCH(launch_gemm_f32(s->ctx.as<float>(), QW, n, L.wo.m, nullptr, x, H, GEMM_ACC, st));
             s->stage("rmsnorm");
-            LAUNCH(launch_rmsnorm(x, L.ffn_norm.as<float>(), xn, nullptr, n, H, c.rms_norm_eps, st));
+            LAUNCH(launch_rmsnorm(x, L.ffn_norm.as<float>(), xn, nullptr, nullptr, n, H, c.rms_norm_eps, st));
             s->stage("ffn gate+up+silu");
             LAUNCH(launch_gemm_f32(xn, H, n, L.gate.m, &L.up.m, s->ffn.as<float>(), F, GEMM_SWIGLU, st));
             s->stage("ffn down (+residual)");
@@ -1219,6 +1273,7 @@ static int validate_tokens(const ahip_session* s, const int32_t* tokens, int n) 
 }
 
 extern "C" int ahip_session_forward(ahip_session* s, const int32_t* tokens, int n, const float** logits) {
+    drop_stale_error();
     if (!s || !logits) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
     BusyGuard guard(s);
     if (!guard.ok) return fail(AHIP_ERR_BUSY, "session is already executing a forward pass");
@@ -1325,6 +1380,7 @@ static bool capture_greedy_graph(ahip_session* s) {
 extern "C" int ahip_session_decode_greedy(ahip_session* s, int32_t start, int max_steps, int depth, ahip_emit_fn emit,
                                           void* user, int* fed_out) {
     if (!s || !emit || !fed_out) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
+    drop_stale_error();
     BusyGuard guard(s);
     if (!guard.ok) return fail(AHIP_ERR_BUSY, "session is already executing a forward pass");
     *fed_out = 0;
@@ -1446,6 +1502,7 @@ static int run_sample(const float* dlogits, int n, float temperature, int top_k,
 extern "C" int ahip_session_sample(ahip_session* s, float temperature, int top_k, float top_p, double u,
                                    int32_t* token) {
     if (!s || !token) return fail(AHIP_ERR_INVALID_ARGUMENT, "null argument");
+    drop_stale_error();
     if (int rc = check_sampling(temperature, top_k, top_p, u)) return rc;
     BusyGuard guard(s);
     if (!guard.ok) return fail(AHIP_ERR_BUSY, "session is already executing a forward pass");
@@ -1535,6 +1592,7 @@ int check_matrix(int dtype, int k) {
 template <typename F>
 int with_ctx(ahip_context* ctx, F f) {
     if (!ctx) return fail(AHIP_ERR_INVALID_ARGUMENT, "null context");
+    drop_stale_error();
     HIP_OR(hipSetDevice(ctx->device), "hipSetDevice");
     return f(ctx->stream);
 }
@@ -1579,7 +1637,7 @@ extern "C" int ahip_op_rmsnorm(ahip_context* ctx, const float* x, const float* w
         if (int rc = upload(dx, x, (size_t)rows * dim * 4, st)) return rc;
         if (int rc = upload(dw, w, (size_t)dim * 4, st)) return rc;
         if (int rc = dout.alloc((size_t)rows * dim * 4)) return rc;
-        LAUNCH(launch_rmsnorm(dx.as<float>(), dw.as<float>(), dout.as<float>(), nullptr, rows, dim, eps, st));
+        LAUNCH(launch_rmsnorm(dx.as<float>(), dw.as<float>(), dout.as<float>(), nullptr, nullptr, rows, dim, eps, st));
         return download(out, dout, (size_t)rows * dim * 4, st);
     });
 }
@@ -1595,7 +1653,8 @@ static int op_project(ahip_context* ctx, const float* x, int m, int k, int dtype
                       int n, int precision, float* y, int mode) {
     if (m <= 0 || n <= 0 || !x || !w || !y || (mode == GEMM_SWIGLU && !wu))
         return fail(AHIP_ERR_INVALID_ARGUMENT, "linear shapes");
-    if (precision != AHIP_GEMM_EXACT && precision != AHIP_GEMM_FAST) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad precision");
+    if (precision != AHIP_GEMM_EXACT && precision != AHIP_GEMM_FAST && precision != AHIP_GEMM_FAST_F16)
+        return fail(AHIP_ERR_INVALID_ARGUMENT, "bad precision");
     if (int rc = check_matrix(dtype, k)) return rc;
     return with_ctx(ctx, [&](hipStream_t st) -> int {
         OwnedMatrix W, U;
@@ -1613,19 +1672,26 @@ static int op_project(ahip_context* ctx, const float* x, int m, int k, int dtype
         if (m == 1) {
             const int gm = mode == GEMM_STORE ? GEMV_STORE : mode == GEMM_ACC ? GEMV_ADD : GEMV_SWIGLU;
             LAUNCH(launch_gemv(W.m, up, dx.as<float>(), nullptr, 0.f, dy.as<float>(), gm, st));
-        } else if (precision == AHIP_GEMM_FAST && m >= 16) {
+        } else if (precision != AHIP_GEMM_EXACT && m >= 16) {
+            // f16 activations: two planes (hi, lo) for the two-term default, one for FAST_F16
+            const bool tt = precision == AHIP_GEMM_FAST;
             DevBuf xh, yh;
-            if (int rc = xh.alloc((size_t)m * k * 2)) return rc;
-            LAUNCH(launch_f32_to_f16(dx.as<float>(), xh.as<f16>(), (int64_t)m * k, st));
+            if (int rc = xh.alloc((size_t)m * k * 2 * (tt ? 2 : 1))) return rc;
+            f16* xlo = tt ? xh.as<f16>() + (size_t)m * k : nullptr;
+            LAUNCH(launch_f32_to_f16(dx.as<float>(), xh.as<f16>(), xlo, (int64_t)m * k, st));
             if (mode == GEMM_SWIGLU) {
-                if (int rc = yh.alloc((size_t)m * n * 2)) return rc;
-                LAUNCH(launch_gemm_mfma(xh.as<f16>(), k, m, W.m, up, nullptr, yh.as<f16>(), n, mode, st));
-                std::vector<uint16_t> h((size_t)m * n);
+                if (int rc = yh.alloc((size_t)m * n * 2 * (tt ? 2 : 1))) return rc;
+                f16* ylo = tt ? yh.as<f16>() + (size_t)m * n : nullptr;
+                LAUNCH(launch_gemm_mfma(xh.as<f16>(), xlo, k, m, W.m, up, nullptr, yh.as<f16>(), ylo, n, mode, st));
+                // the result as the next GEMM takes it: hi + lo (two-term) or hi
+                std::vector<uint16_t> h((size_t)m * n * (tt ? 2 : 1));
                 if (int rc = download(h.data(), yh, h.size() * 2, st)) return rc;
-                for (size_t i = 0; i < h.size(); i++) y[i] = f16_bits_to_f32(h[i]);
+                for (size_t i = 0; i < (size_t)m * n; i++)
+                    y[i] = f16_bits_to_f32(h[i]) + (tt ? f16_bits_to_f32(h[(size_t)m * n + i]) : 0.f);
                 return AHIP_OK;
             }
-            LAUNCH(launch_gemm_mfma(xh.as<f16>(), k, m, W.m, nullptr, dy.as<float>(), nullptr, n, mode, st));
+            LAUNCH(launch_gemm_mfma(xh.as<f16>(), xlo, k, m, W.m, nullptr, dy.as<float>(), nullptr, nullptr, n, mode,
+                                    st));
         } else {
             LAUNCH(launch_gemm_f32(dx.as<float>(), k, m, W.m, up, dy.as<float>(), n, mode, st));
         }
@@ -1658,7 +1724,7 @@ extern "C" int ahip_op_rope(ahip_context* ctx, float* x, int tokens, int heads, 
         const size_t bytes = (size_t)tokens * heads * hd * 4;
         if (int rc = upload(dx, x, bytes, st)) return rc;
         LAUNCH(launch_rope_store(dx.as<float>(), heads * hd, tokens, heads, 0, hd, start, dt.as<float2>(),
-                                 interleaved ? 1 : 0, 1, nullptr, nullptr, nullptr, 1, 0, st));
+                                 interleaved ? 1 : 0, 1, nullptr, nullptr, nullptr, nullptr, 1, 0, st));
         return download(x, dx, bytes, st);
     });
 }
@@ -1692,12 +1758,18 @@ extern "C" int ahip_op_attention(ahip_context* ctx, const float* q, int tokens, 
         if (int rc = upload(dv, vb.data(), vb.size(), st)) return rc;
         const size_t qn = (size_t)tokens * heads * hd;
         if (int rc = dout.alloc(qn * 4)) return rc;
-        if (precision == AHIP_GEMM_FAST && f16kv && tokens >= 16 && (hd == 64 || hd == 128)) {
-            std::vector<uint16_t> qh(qn);
-            for (size_t i = 0; i < qn; i++) qh[i] = f32_to_f16_bits(q[i]);
-            if (int rc = upload(dq, qh.data(), qn * 2, st)) return rc;
-            LAUNCH(launch_flash_attention(dq.as<f16>(), heads * hd, dk.as<f16>(), dv.as<f16>(), capacity, tokens, heads,
-                                          kv_heads, hd, start, dout.as<float>(), nullptr, st));
+        if (precision != AHIP_GEMM_EXACT && f16kv && tokens >= 16 && (hd == 64 || hd == 128)) {
+            // q as one f16 term (FAST_F16) or two (hi, then lo = f16(q - hi))
+            const bool tt = precision == AHIP_GEMM_FAST;
+            std::vector<uint16_t> qh(qn * (tt ? 2 : 1));
+            for (size_t i = 0; i < qn; i++) {
+                qh[i] = f32_to_f16_bits(q[i]);
+                if (tt) qh[qn + i] = f32_to_f16_bits(q[i] - f16_bits_to_f32(qh[i]));
+            }
+            if (int rc = upload(dq, qh.data(), qh.size() * 2, st)) return rc;
+            LAUNCH(launch_flash_attention(dq.as<f16>(), tt ? dq.as<f16>() + qn : nullptr, heads * hd, dk.as<f16>(),
+                                          dv.as<f16>(), capacity, tokens, heads, kv_heads, hd, start, dout.as<float>(),
+                                          nullptr, nullptr, st));
         } else if (tokens == 1 && attention_decode_supported(heads, kv_heads, hd) &&
                    attention_decode_split_len(capacity) <= attention_decode_max_split_len()) {
             if (int rc = upload(dq, q, qn * 4, st)) return rc;
@@ -1835,6 +1907,7 @@ extern "C" int ahip_dev_weight_free(ahip_context* ctx, void* handle) {
 
 template <typename F>
 static int time_launches(ahip_context* ctx, int iters, double* avg, F launch) {
+    drop_stale_error();
     hipStream_t st = ctx->stream;
     hipEvent_t a, b;
     HIP_OR(hipEventCreate(&a), "hipEventCreate");
@@ -1870,12 +1943,16 @@ extern "C" int ahip_dev_gemm(ahip_context* ctx, void* weight, const float* dx, i
     if (!ctx || !weight || !dx || !dy || m <= 0 || iters < 0) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad argument");
     const DevMatrix& w = ((OwnedMatrix*)weight)->m;
     HIP_OR(hipSetDevice(ctx->device), "hipSetDevice");
-    if (precision == AHIP_GEMM_FAST) {
+    if (precision == AHIP_GEMM_FAST || precision == AHIP_GEMM_FAST_F16) {
+        const bool tt = precision == AHIP_GEMM_FAST;
+        const size_t e = (size_t)m * w.cols;
         DevBuf xh;
-        if (int rc = xh.alloc((size_t)m * w.cols * 2)) return rc;
-        LAUNCH(launch_f32_to_f16(dx, xh.as<f16>(), (int64_t)m * w.cols, ctx->stream));
+        if (int rc = xh.alloc(e * 2 * (tt ? 2 : 1))) return rc;
+        f16* xlo = tt ? xh.as<f16>() + e : nullptr;
+        LAUNCH(launch_f32_to_f16(dx, xh.as<f16>(), xlo, (int64_t)e, ctx->stream));
         return time_launches(ctx, iters, avg, [&](hipStream_t st) {
-            return launch_gemm_mfma(xh.as<f16>(), w.cols, m, w, nullptr, dy, nullptr, w.rows, GEMM_STORE, st);
+            return launch_gemm_mfma(xh.as<f16>(), xlo, w.cols, m, w, nullptr, dy, nullptr, nullptr, w.rows, GEMM_STORE,
+                                    st);
         });
     }
     return time_launches(ctx, iters, avg, [&](hipStream_t st) {
@@ -1905,7 +1982,7 @@ extern "C" int ahip_dev_attention(ahip_context* ctx, const void* dq, const void*
                                 hipMemcpyDeviceToDevice, st), "cache copy");
     }
     return time_launches(ctx, iters, avg, [&](hipStream_t s2) {
-        return launch_flash_attention((const f16*)dq, heads * hd, kc.as<f16>(), vc.as<f16>(), tokens, tokens, heads,
-                                      kv_heads, hd, 0, dout, nullptr, s2);
+        return launch_flash_attention((const f16*)dq, nullptr, heads * hd, kc.as<f16>(), vc.as<f16>(), tokens, tokens,
+                                      heads, kv_heads, hd, 0, dout, nullptr, nullptr, s2);
     });
 }

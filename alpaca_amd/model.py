@@ -70,7 +70,7 @@ class LlamaConfig:
 
 
 KV = {"f16": L.KV_F16, "f32": L.KV_F32}
-GEMM = {"exact": L.GEMM_EXACT, "fast": L.GEMM_FAST}
+GEMM = {"exact": L.GEMM_EXACT, "fast": L.GEMM_FAST, "fast-f16": L.GEMM_FAST_F16}
 
 
 class HIPLlamaModel:

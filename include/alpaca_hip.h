@@ -46,9 +46,15 @@ typedef enum { AHIP_F32 = 0, AHIP_F16 = 1, AHIP_Q8_0 = 2, AHIP_Q4_0 = 3 } ahip_d
 /* KVPrecision, Sources/AlpacaMetal/Backend/KernelEncoder.swift:9-17. */
 typedef enum { AHIP_KV_F16 = 0, AHIP_KV_F32 = 1 } ahip_kv_precision;
 
-/* GEMMPrecision, KernelEncoder.swift:41-48: exact = float32 operands;
- * fast = f16 operands on MFMA with float32 accumulation. */
-typedef enum { AHIP_GEMM_EXACT = 0, AHIP_GEMM_FAST = 1 } ahip_gemm_precision;
+/* GEMMPrecision, KernelEncoder.swift:41-48: exact = float32 operands (the
+ * SIMT GEMMs and float32 attention); fast = f16 MFMA with float32
+ * accumulation, the default: weights enter as their exact quants, activations
+ * (and the prefill attention's Q and P) as two f16 terms hi + lo, so prefill
+ * logits stay within 2e-3 + 1e-3 relative of the CPU reference at every
+ * benchmark configuration; fast_f16 = the same MFMA kernels with one f16 term
+ * per activation (the reference's fast-path numerics class: half the MFMA
+ * work, 2^-11 relative input rounding). */
+typedef enum { AHIP_GEMM_EXACT = 0, AHIP_GEMM_FAST = 1, AHIP_GEMM_FAST_F16 = 2 } ahip_gemm_precision;
 
 /* LlamaConfig, Sources/AlpacaCore/Transformer/LlamaConfig.swift:8-20. */
 typedef struct {

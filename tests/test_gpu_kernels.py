@@ -56,20 +56,28 @@ def test_linear_all_formats_and_batch_sizes(hip_ops, k, n, name, dt):  # KernelT
 @pytest.mark.parametrize("k,n", [(64, 10), (576, 193), (1536, 576), (576, 1536)])
 @pytest.mark.parametrize("name,dt", FORMATS)
 def test_fast_gemm_within_analytic_bound(hip_ops, k, n, name, dt):  # KernelTests.swift:179-217
-    """f16 operands: |err| <= 2^-10 * sum_k |x_k w_k| + 1e-5 element-wise."""
+    """One f16 term per activation: |err| <= 2^-10 * sum_k |x_k w_k| + 1e-5
+    element-wise (the reference's fast-path bound); two terms (the default):
+    within the exact GEMM's tolerance."""
     w32 = rand((n, k), k * 31 + n, 0.3)
     w = encode(w32, dt)
     wd = orc.dequantize(dt, w.data, n * k).reshape(n, k).astype(np.float64)
     worst = 0.0
+    worst_tt = 0.0
     for t in [16, 32, 33, 70, 130, 300]:
         x = rand((t, k), 1000 + t)
-        gpu = hip_ops.linear(x, w, "fast").astype(np.float64)
         cpu = orc.linear(x, dt, w.data, n).astype(np.float64)
         bound = np.abs(x.astype(np.float64)) @ np.abs(wd).T / 1024 + 1e-5
-        err = np.abs(gpu - cpu)
+        # one f16 term per activation (the reference's fast path)
+        err = np.abs(hip_ops.linear(x, w, "fast-f16").astype(np.float64) - cpu)
         worst = max(worst, float((err / bound).max()))
-        assert (err <= bound).all(), f"fast GEMM {name} K={k} N={n} T={t}: worst ratio {(err / bound).max()}"
-    print(f"[metrics] fast GEMM {name} K={k} N={n}: worst error / bound = {worst:.3f}")
+        assert (err <= bound).all(), f"fast-f16 GEMM {name} K={k} N={n} T={t}: worst ratio {(err / bound).max()}"
+        # two terms (the default): float32-grade inputs, so within the exact GEMM's 2e-4 + 1e-4 |y|
+        err = np.abs(hip_ops.linear(x, w, "fast").astype(np.float64) - cpu)
+        worst_tt = max(worst_tt, float((err / (2e-4 + 1e-4 * np.abs(cpu))).max()))
+        assert (err <= 2e-4 + 1e-4 * np.abs(cpu)).all(), f"fast GEMM {name} K={k} N={n} T={t}"
+    print(f"[metrics] fast GEMM {name} K={k} N={n}: worst error / bound = {worst:.3f} (one term), "
+          f"{worst_tt:.3f} of 2e-4 + 1e-4 |y| (two terms)")
 
 
 @pytest.mark.parametrize("k,n", [(64, 10), (96, 40), (576, 193), (256, 300)])

@@ -35,13 +35,14 @@ SPECS = [
 ]
 
 
+@pytest.mark.parametrize("prec", ["fast", "fast-f16"])
 @pytest.mark.parametrize("spec", SPECS, ids=lambda s: s.name)
-def test_fused_qkv_rope_is_bit_identical_to_unfused(hip_ctx, spec):
+def test_fused_qkv_rope_is_bit_identical_to_unfused(hip_ctx, spec, prec):
     model = HIPLlamaModel(hip_ctx, spec.config, built(spec))
     prompt = synth.prompt_tokens(spec, 150)
     with env(ALPACA_HIP_FUSE_QKV_ROPE=0):
-        ref = model.make_session(capacity=200, gemm_precision="fast")
-    fused = model.make_session(capacity=200, gemm_precision="fast")
+        ref = model.make_session(capacity=200, gemm_precision=prec)
+    fused = model.make_session(capacity=200, gemm_precision=prec)
     for chunk in (prompt[:70], prompt[70:]):  # the second chunk starts at position 70
         a, b = fused.forward(chunk), ref.forward(chunk)
         assert np.array_equal(a, b), f"prefill logits differ: max |d| {np.abs(a - b).max():.3e}"

@@ -91,3 +91,21 @@ def test_concurrent_sessions_equal_their_solo_runs(hip_ctx, persistent):
         assert np.array_equal(l0, l1), f"session {i}: prefill logits differ"
         assert t0 == t1, f"session {i}: greedy tokens differ"
         assert np.array_equal(d0, d1), f"session {i}: decode logits differ"
+
+
+def test_model_outlives_its_sessions(hip_ctx):
+    """A model destroyed while a session still uses it stays alive until that
+    session is destroyed (MetalLlamaSession keeps its MetalLlamaModel), and no
+    HIP error from the teardown leaks into later calls."""
+    spec = synth.TINY
+    model = HIPLlamaModel(hip_ctx, spec.config, built(spec))
+    prompt = synth.prompt_tokens(spec, 20)
+    s = model.make_session(capacity=64)
+    want = s.forward(prompt)
+    s.reset()
+    model.close()  # the session still holds the model
+    assert np.array_equal(s.forward(prompt), want)
+    s.close()      # the model goes with it
+    other = HIPLlamaModel(hip_ctx, spec.config, built(spec))
+    t = other.make_session(capacity=64)
+    assert np.array_equal(t.forward(prompt), want)

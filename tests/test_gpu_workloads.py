@@ -8,8 +8,8 @@ written by tests/golden/make_synthetic_goldens.py --workloads):
   * C5W: C5 (1.7B-shape Q8_0), 4096-token prompt, 256 greedy steps.
 
 Each runs in the default configuration the bench uses (fast f16-MFMA
-prefill in one 4096-row chunk, f16 KV cache, persistent decode kernel) and is
-held to the BASELINE north star: every one of the 49,152 logits within
+prefill in one 4096-row chunk with two-term activations, f16 KV cache,
+persistent decode kernel) and is held to the BASELINE north star: every one of the 49,152 logits within
 2e-3 absolute + 1e-3 relative of the oracle's (an f16-rounded cache, as the
 GPU keeps) at the prefill and at greedy steps 1-8 and the last, and greedy
 ids identical at every step.  A greedy id may differ only where the oracle's
@@ -47,14 +47,7 @@ def near_tie(margin: float, top: float) -> bool:
     return margin < 2 * (ATOL + RTOL * abs(top))
 
 
-# C4W's fast prefill: one logit at 2.47e-3 from the oracle where the bound is
-# 2.34e-3 (mean 4.4e-4), from the f16 rounding of the GEMM activations.
-FAST_PATH_OVER_BOUND = {"C4W"}
-
-
-@pytest.mark.parametrize("key", [pytest.param(k, marks=pytest.mark.xfail(
-    k in FAST_PATH_OVER_BOUND, reason="fast prefill exceeds 2e-3 + 1e-3 |e| at one logit", strict=True))
-    for k in sorted(SPECS)])
+@pytest.mark.parametrize("key", sorted(SPECS))
 def test_workload_matches_oracle_logits(hip_ctx, key):
     g, meta = load(key)
     spec = SPECS[key]
@@ -123,4 +116,10 @@ def test_workload_exact_prefill_matches_oracle(hip_ctx, key):
     assert_close(logits, e, ATOL, RTOL, f"{key} exact prefill")
     assert int(np.argmax(logits)) == int(g["ids"][0])
     s.close()
+    # the single-term f16 path (the reference's fast-path numerics): reported, not held to the bar
+    f = model.make_session(capacity=n + 16, max_batch=4096, gemm_precision="fast-f16")
+    d = np.abs(f.forward(synth.prompt_tokens(spec, n)).astype(np.float64) - e)
+    print(f"[metrics] {key} fast-f16 prefill: maxAbs {d.max():.3e} worst/bound "
+          f"{(d / (ATOL + RTOL * np.abs(e))).max():.3f}")
+    f.close()
     model.close()
