@@ -744,14 +744,44 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
     const int wm = wave / (BN / WN), wn = wave % (BN / WN);
     const int nk = K / DBK;
 
+    // Per-lane byte offsets of the DMA rows (loop-invariant, 32-bit: the host
+    // checks that every operand spans less than 4 GiB); each stage adds its K
+    // offset to the wave-uniform base pointers instead.
+    uint32_t aoff[G::A_I], boff[NB][G::B_I], soff = 0;
+#pragma unroll
+    for (int i = 0; i < G::A_I; i++) {
+        const int r = (i * 4 + wave) * 8 + (lane >> 3), c = (lane & 7) ^ swz_a(r);
+        aoff[i] = (uint32_t)((min(m0 + r, M - 1) * p.ldx + c * 8) * 2);
+    }
+#pragma unroll
+    for (int mat = 0; mat < NB; mat++)
+#pragma unroll
+        for (int i = 0; i < G::B_I; i++) {
+            if constexpr (FMT == DT_Q8_0) {
+                const int r = (i * 4 + wave) * 16 + (lane >> 2), c = (lane & 3) ^ swz_q8(r);
+                boff[mat][i] = (uint32_t)(min(n0 + r, N - 1) * K + c * 16);
+            } else if constexpr (FMT == DT_Q4_0) {
+                if constexpr (G::Q4_16) {
+                    const int r = (i * 4 + wave) * 32 + (lane >> 1), c = (lane & 1) ^ swz_q4(r);
+                    boff[mat][i] = (uint32_t)((min(n0 + r, N - 1) * nb + c) * 16);
+                } else {
+                    const int r = (i * 4 + wave) * 8 + (lane >> 3), c = ((lane >> 2) & 1) ^ swz_q4(r);
+                    boff[mat][i] = (uint32_t)((min(n0 + r, N - 1) * nb + c) * 16 + (lane & 3) * 4);
+                }
+            } else {
+                const int r = (i * 4 + wave) * 8 + (lane >> 3), c = (lane & 7) ^ swz_a(r);
+                boff[mat][i] = (uint32_t)((min(n0 + r, N - 1) * K + c * 8) * 2);
+            }
+        }
+    if constexpr (FMT != DT_F16) soff = (uint32_t)((n0 + wave * (BN / 4) + lane * 4) * 4);
+
     auto issue = [&](uint32_t sg, int kt) {  // sg: LDS byte address of the stage buffer
         const int k0 = kt * DBK;
 #pragma unroll
         for (int i = 0; i < G::A_I; i++) {
-            const int r0 = (i * 4 + wave) * 8, r = r0 + (lane >> 3), c = (lane & 7) ^ swz_a(r);
-            const int64_t off = (int64_t)min(m0 + r, M - 1) * p.ldx + k0 + c * 8;
-            dma16(p.x + off, sg + r0 * DBK * 2);
-            if constexpr (TT) dma16(p.xlo + off, sg + L::A_LO + r0 * DBK * 2);
+            const int r0 = (i * 4 + wave) * 8;
+            dma16s(p.x + k0, aoff[i], sg + r0 * DBK * 2);
+            if constexpr (TT) dma16s(p.xlo + k0, aoff[i], sg + L::A_LO + r0 * DBK * 2);
         }
 #pragma unroll
         for (int mat = 0; mat < NB; mat++) {
@@ -760,27 +790,18 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
 #pragma unroll
             for (int i = 0; i < G::B_I; i++) {
                 if constexpr (FMT == DT_Q8_0) {
-                    const int r0 = (i * 4 + wave) * 16, r = r0 + (lane >> 2), c = (lane & 3) ^ swz_q8(r);
-                    dma16(w.q + (int64_t)min(n0 + r, N - 1) * K + k0 + c * 16, bq + r0 * 64);
+                    dma16s(w.q + k0, boff[mat][i], bq + (i * 4 + wave) * 16 * 64);
                 } else if constexpr (FMT == DT_Q4_0) {
-                    if constexpr (G::Q4_16) {
-                        const int r0 = (i * 4 + wave) * 32, r = r0 + (lane >> 1), c = (lane & 1) ^ swz_q4(r);
-                        dma16(w.q + ((int64_t)min(n0 + r, N - 1) * nb + 2 * kt + c) * 16, bq + r0 * 32);
-                    } else {
-                        const int r0 = (i * 4 + wave) * 8, r = r0 + (lane >> 3), c = ((lane >> 2) & 1) ^ swz_q4(r);
-                        dma4(w.q + ((int64_t)min(n0 + r, N - 1) * nb + 2 * kt + c) * 16 + (lane & 3) * 4, bq + r0 * 32);
-                    }
+                    if constexpr (G::Q4_16) dma16s(w.q + kt * 32, boff[mat][i], bq + (i * 4 + wave) * 32 * 32);
+                    else dma4s(w.q + kt * 32, boff[mat][i], bq + (i * 4 + wave) * 8 * 32);
                 } else {
-                    const int r0 = (i * 4 + wave) * 8, r = r0 + (lane >> 3), c = (lane & 7) ^ swz_a(r);
-                    dma16(w.q + ((int64_t)min(n0 + r, N - 1) * K + k0 + c * 8) * 2, bq + r0 * 128);
+                    dma16s(w.q + k0 * 2, boff[mat][i], bq + (i * 4 + wave) * 8 * 128);
                 }
             }
             if constexpr (FMT != DT_F16) {
                 // The tile's BN scale pairs are contiguous in s2: each wave moves a
                 // quarter of them, 16 bytes (4 rows) per active lane.
-                if (lane < BN / 16)
-                    dma16(w.s2 + (int64_t)kt * spitch + n0 + wave * (BN / 4) + lane * 4,
-                          sg + L::S_OFF + mat * BN * 4 + wave * BN);
+                if (lane < BN / 16) dma16s(w.s2 + (int64_t)kt * spitch, soff, sg + L::S_OFF + mat * BN * 4 + wave * BN);
             }
         }
     };
@@ -799,29 +820,35 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
     // j+1 are issued before the scaling of column j, so the VALU work of one
     // column runs under the MFMAs of the next instead of waiting on them.
     auto compute_block_quant = [&](const uint8_t* sg, int kk, const f16x8 (&af)[TM], const f16x8 (&al)[TT ? TM : 1]) {
-        f16x8 bf[NB * TN];
+        // The raw quants of every column are read first; each becomes f16 just
+        // before its MFMAs (8 bytes live per column instead of 16).
+        uint2 raw[NB * TN];
         float d[NB * TN];
 #pragma unroll
         for (int c = 0; c < NB * TN; c++) {
             const int mat = c / TN, j = c % TN;
             const int r = wn * WN + 16 * j + (lane & 15);
             const uint8_t* bq = sg + L::B_OFF + mat * BN * L::BROW;
-            uint2 raw;
-            uint32_t o[4];
             if constexpr (FMT == DT_Q8_0) {
                 const int u = 4 * kk + jj;
-                raw = *(const uint2*)(bq + r * 64 + ((u >> 1) ^ swz_q8(r)) * 16 + (u & 1) * 8);
-                int8x4_to_f16(raw.x, o[0], o[1]);
-                int8x4_to_f16(raw.y, o[2], o[3]);
+                raw[c] = *(const uint2*)(bq + r * 64 + ((u >> 1) ^ swz_q8(r)) * 16 + (u & 1) * 8);
             } else {
-                raw = *(const uint2*)(bq + r * 32 + (kk ^ swz_q4(r)) * 16 + (jj & 1) * 8);
-                const int sh = (jj >> 1) * 4;
-                nib4_to_f16((raw.x >> sh) & 0x0F0F0F0Fu, o[0], o[1]);
-                nib4_to_f16((raw.y >> sh) & 0x0F0F0F0Fu, o[2], o[3]);
+                raw[c] = *(const uint2*)(bq + r * 32 + (kk ^ swz_q4(r)) * 16 + (jj & 1) * 8);
             }
-            bf[c] = __builtin_bit_cast(f16x8, make_uint4(o[0], o[1], o[2], o[3]));
             d[c] = (float)*(const f16*)(sg + L::S_OFF + mat * BN * 4 + r * 4 + kk * 2);
         }
+        auto bfrag = [&](int c) {
+            uint32_t o[4];
+            if constexpr (FMT == DT_Q8_0) {
+                int8x4_to_f16(raw[c].x, o[0], o[1]);
+                int8x4_to_f16(raw[c].y, o[2], o[3]);
+            } else {
+                const int sh = (jj >> 1) * 4;
+                nib4_to_f16((raw[c].x >> sh) & 0x0F0F0F0Fu, o[0], o[1]);
+                nib4_to_f16((raw[c].y >> sh) & 0x0F0F0F0Fu, o[2], o[3]);
+            }
+            return __builtin_bit_cast(f16x8, make_uint4(o[0], o[1], o[2], o[3]));
+        };
         f32x4 prev[TM], cur[TM];
         const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
         // the block's product: both activation terms times the exact quants, summed in float32
@@ -830,13 +857,17 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
             if constexpr (TT) t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b, t, 0, 0, 0);
             return t;
         };
+        {
+            const f16x8 b0 = bfrag(0);
 #pragma unroll
-        for (int i = 0; i < TM; i++) prev[i] = block(i, bf[0]);
+            for (int i = 0; i < TM; i++) prev[i] = block(i, b0);
+        }
 #pragma unroll
         for (int c = 1; c <= NB * TN; c++) {
             if (c < NB * TN) {
+                const f16x8 bc = bfrag(c);
 #pragma unroll
-                for (int i = 0; i < TM; i++) cur[i] = block(i, bf[c]);
+                for (int i = 0; i < TM; i++) cur[i] = block(i, bc);
             }
             const int pc = c - 1, mat = pc / TN, j = pc % TN;
 #pragma unroll
@@ -952,15 +983,16 @@ hipError_t run_dgemm(const GemmArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// ALPACA_HIP_GEMM_TILE=256 | 128x128 | 128x64 forces a tile family (tuning and
-// tests; read on every launch); 256 means 256x128 (256x64 per matrix for
-// SwiGLU).
+// ALPACA_HIP_GEMM_TILE=256 | 128x128 | 128x64 | 128x256 forces a tile family
+// (tuning and tests; read on every launch); 256 means 256x128 (256x64 per
+// matrix for SwiGLU), 128x256 means 128x128 per matrix for SwiGLU.
 int forced_tile() {
     const char* e = std::getenv("ALPACA_HIP_GEMM_TILE");
     if (!e) return 0;
     if (!std::strcmp(e, "256")) return 1;
     if (!std::strcmp(e, "128x128")) return 2;
     if (!std::strcmp(e, "128x64")) return 3;
+    if (!std::strcmp(e, "128x256")) return 4;
     return 0;
 }
 
@@ -996,24 +1028,38 @@ int resident_per_cu() {
 // Tile choice, counted in rounds of resident workgroups over the device's CUs.
 template <int FMT, int MODE, int RH, bool TT>
 hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
-    const int M = a.M, N = a.w.rows;
+    const int M = a.M, N = a.w.rows, cus = device_cus();
     auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+    // Wide tiles (one workgroup per CU) pay off in whole rounds or where the
+    // last partial round is a small part of the grid.
+    auto wide_fits = [&](int t) { return t >= cus && (t % cus == 0 || t >= 3 * cus); };
     const int f = forced_tile();
     // The 256-row tiles hold more accumulators than the 256 architectural VGPRs
     // (344-353 with AGPR spills) and are slower wherever measured; they stay
-    // reachable through ALPACA_HIP_GEMM_TILE=256.  128x64 tiles (~169 VGPRs,
-    // two LDS stages) are kept while their grid fits in one round of the
-    // workgroups the device holds at once; past it (a near-empty second round,
-    // e.g. a 1600-column QKV over 4096 rows) 128x128 tiles are faster.
-    // (The 256-row tiles do not fit LDS with two activation terms.)
+    // reachable through ALPACA_HIP_GEMM_TILE=256 (single-term activations only:
+    // with two terms they do not fit LDS).  With two activation terms a
+    // 128x64 tile moves 36 KB per 64-wide K stage for 2 MFLOP and is bound by
+    // the global->LDS rate; 128x256 tiles (128x128 per matrix for SwiGLU,
+    // three stages, 147 KB of LDS) halve the bytes per MFMA and are taken on
+    // grids of whole rounds.  Single-term activations stay on the narrower
+    // tiles, where the wide ones measured slower.  128x64 tiles (two LDS
+    // stages) are kept while their grid fits in one round of the workgroups
+    // the device holds at once; past it (a near-empty second round, e.g. a
+    // 1600-column QKV over 4096 rows) 128x128 tiles are faster.
     if constexpr (MODE == GEMM_SWIGLU) {
         if constexpr (!TT)
             if (f == 1) return run_dgemm<FMT, 256, 64, 128, 32, MODE, RH, TT>(a, st);
+        if constexpr (FMT != DT_F16)  // (f16 weight stages are 4x larger: no third stage fits)
+            if (f == 4 || (f == 0 && TT && wide_fits(tiles(128, 128))))
+                return run_dgemm<FMT, 128, 128, 64, 64, MODE, RH, TT>(a, st);
         return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH, TT>(a, st);
     } else {
         if constexpr (!TT)
             if (f == 1) return run_dgemm<FMT, 256, 128, 128, 64, MODE, RH, TT>(a, st);
-        const int slots = resident_per_cu<FMT, 128, 64, 64, 32, MODE, RH, TT>() * device_cus();
+        if constexpr (FMT != DT_F16)
+            if (f == 4 || (f == 0 && TT && wide_fits(tiles(128, 256))))
+                return run_dgemm<FMT, 128, 256, 64, 128, MODE, RH, TT>(a, st);
+        const int slots = resident_per_cu<FMT, 128, 64, 64, 32, MODE, RH, TT>() * cus;
         if (f == 2 || (f == 0 && tiles(128, 64) > slots)) return run_dgemm<FMT, 128, 128, 64, 64, MODE, RH, TT>(a, st);
         return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH, TT>(a, st);
     }
@@ -1037,6 +1083,18 @@ hipError_t dgemm_mode(const GemmArgs& a, int mode, hipStream_t st) {
 
 }  // namespace
 
+namespace {
+// The DMA kernel addresses activations and weights with 32-bit signed byte
+// offsets from per-stage base pointers.
+bool dma_offsets_fit(int m, int ldx, const DevMatrix& w) {
+    const int64_t lim = INT32_MAX;
+    const int64_t wbytes = w.dtype == DT_Q8_0   ? (int64_t)w.rows * w.cols
+                           : w.dtype == DT_Q4_0 ? (int64_t)w.rows * (w.cols / 32) * 16
+                                                : (int64_t)w.rows * w.cols * 2;
+    return (int64_t)m * ldx * 2 < lim && wbytes < lim;
+}
+}  // namespace
+
 hipError_t launch_gemm_mfma(const f16* x, const f16* xlo, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up,
                             float* y, f16* yh, f16* yhlo, int ldy, int mode, hipStream_t st) {
     if (m <= 0) return hipSuccess;
@@ -1045,7 +1103,7 @@ hipError_t launch_gemm_mfma(const f16* x, const f16* xlo, int ldx, int m, const 
     // for quantised weights, the stage-major scales.
     const bool quant = w.dtype != DT_F16;
     if (w.cols % DBK || ldx % 8 || ((uintptr_t)x & 15) || ((uintptr_t)xlo & 15) ||
-        (quant && (!w.s2 || (w_up && !w_up->s2))))
+        (quant && (!w.s2 || (w_up && !w_up->s2))) || !dma_offsets_fit(m, ldx, w))
         return launch_gemm_mfma_staged(x, xlo, ldx, m, w, w_up, y, yh, yhlo, ldy, mode, st);
     GemmArgs a;
     a.x = x;
@@ -1071,7 +1129,8 @@ hipError_t launch_gemm_qkv_rope(const f16* x, const f16* xlo, int ldx, int m, co
     const bool quant = w.dtype != DT_F16;
     // the pipelined kernel's conditions (as in launch_gemm_mfma); RoPE pairs and
     // 16-column lane groups must not straddle a head; two-term in, two-term q out
-    if (w.cols % DBK || ldx % 8 || ((uintptr_t)x & 15) || ((uintptr_t)xlo & 15) || (quant && !w.s2) || o.hd % 16 ||
+    if (w.cols % DBK || ldx % 8 || ((uintptr_t)x & 15) || ((uintptr_t)xlo & 15) || (quant && !w.s2) ||
+        !dma_offsets_fit(m, ldx, w) || o.hd % 16 ||
         o.hd > 128 || o.heads <= 0 || o.kv_heads <= 0 || w.rows != (o.heads + 2 * o.kv_heads) * o.hd || !o.rope ||
         !o.qh || !o.kc || !o.vc || (xlo && !o.qlo))
         return hipErrorNotSupported;

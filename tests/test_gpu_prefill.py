@@ -77,7 +77,7 @@ def test_fused_qkv_rope_with_large_tiles(hip_ctx):
         x, y = fused.decode(tok), ref.decode(tok)
         assert np.array_equal(x, y), f"decode step {step} differs: max |d| {np.abs(x - y).max():.3e}"
         tok = int(np.argmax(x))
-    for tile in ("128x64", "128x128"):
+    for tile in ("128x64", "128x128", "128x256"):
         fused.reset()
         with env(ALPACA_HIP_GEMM_TILE=tile):
             t = fused.forward(prompt)
