@@ -20,8 +20,11 @@
 // in the cache); Q and P enter either as one f16 term each, or (TT, the
 // default prefill) as two, hi = f16(x) and lo = f16(x - hi), which carry them
 // to ~2^-22 so that scores and P.V keep float32 accuracy at twice the MFMA
-// work (P times 2^14 then, so that lo stays out of the f16 subnormals);
-// accumulation and the softmax statistics are float32.
+// work; P enters as P * 2^14, which keeps small probabilities (and the second
+// term) out of the f16 subnormals.  Accumulation and the softmax statistics
+// are float32.  ALPACA_HIP_FLASH_P_TERMS=1 keeps Q two-term but P single-term
+// (faster; measured past the logit bound at the 1.7B shape's 4096-token
+// prompt).
 //
 // attn_generic_kernel: one wave per (query, head, key split) with an online
 // softmax in float32 over an f16 or f32 cache; splits are merged by
@@ -29,6 +32,8 @@
 // reference's attn_decode_split + attn_decode_merge, attention_decode.metal)
 // and for the exact / f32-KV / odd head-dim cases (attention.metal).
 #include "common.h"
+
+#include <cstdlib>
 
 namespace {
 
@@ -73,12 +78,44 @@ __device__ __forceinline__ f16x4 lds_read_tr(const uint8_t* p) {
     return __builtin_bit_cast(f16x4, v);
 }
 
+// Two floats -> an f16 pair, each rounded to nearest even (v_cvt_pk_f16_f32).
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){a, b}, f16x2v));
+}
+// e - (float)half, with the half read straight from the low (or high) 16 bits
+// of a packed pair by the mixed-precision FMA (exact: the difference of a float
+// and its own f16 rounding is representable).
+__device__ __forceinline__ float minus_f16_lo(uint32_t pk, float e) {
+    float d;
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(pk), "v"(e));
+    return d;
+}
+__device__ __forceinline__ float minus_f16_hi(uint32_t pk, float e) {
+    float d;
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(pk), "v"(e));
+    return d;
+}
+
+// IEEE max of floats that are never signalling NaNs (plain v_max / v_max3).
+__device__ __forceinline__ float vmax(float a, float b) {
+    float d;
+    asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+    float d;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+
 // NSET wave-sets per workgroup.  With NSET = 2 (head dim 64) a second set of
 // four waves takes the second half of the key blocks of the same 64 queries,
 // halving the sequential walk of the longest (causal) query blocks; the halves
 // merge at the end.  It costs LDS (one workgroup per CU), so the launcher uses
 // it only when one-set workgroups would not fill the chip.
-template <int HD, int NSET, bool OUT16, bool TT>
+template <int HD, int NSET, bool OUT16, bool TT, bool PT>
 __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
     static_assert(NSET == 1 || (NSET == 2 && HD == 64), "two wave-sets fit LDS at head dim 64 only");
     constexpr int KS = HD / 32, DT = HD / 16;
@@ -113,9 +150,11 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
     uint8_t* const st1 = set ? sB1 : sA1;
     uint8_t* const st2 = set ? sB2 : sA2;
 
-    // P enters the MFMA scaled by 2^14 in the two-term form (lo stays out of the
-    // f16 subnormals); the output's normalisation undoes it.
-    constexpr float kPScale = TT ? 16384.f : 1.f;
+    // P enters the MFMA scaled by 2^14 (P <= 1 becomes <= 2^14): over long key
+    // ranges most probabilities lie below f16's smallest normal (2^-14) and
+    // would otherwise lose relative precision, as would the second term of the
+    // two-term form; the output's normalisation undoes the scale.
+    constexpr float kLog2PScale = 14.f;
     f16x8 qf[KS], ql[TT ? KS : 1];
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
@@ -152,7 +191,6 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
     f32x4 oacc[DT];
 #pragma unroll
     for (int d = 0; d < DT; d++) oacc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
-    auto fmax2 = [](float x, float y) { return fmaxf(x, y); };
     auto add2 = [](float x, float y) { return x + y; };
 
     auto compute = [&](const uint8_t* sg, int kb) {
@@ -182,10 +220,13 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
         }
         // Running max in log2 units (m, mn): the scale is positive, so the max
         // of the raw scores scales to the max of the scaled ones.
-        float mx = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < 4; t++) mx = fmaxf(mx, fmaxf(fmaxf(sacc[t][0], sacc[t][1]), fmaxf(sacc[t][2], sacc[t][3])));
-        mx = xor32_combine(xor16_combine(mx, fmax2), fmax2);  // the 4 lanes of this query
+        // (v_max3 without the compiler's signalling-NaN quieting of every
+        // operand: MFMA results and -inf are never signalling NaNs)
+        const float m0 = vmax3(sacc[0][0], sacc[0][1], sacc[0][2]), m1 = vmax3(sacc[0][3], sacc[1][0], sacc[1][1]);
+        const float m2 = vmax3(sacc[1][2], sacc[1][3], sacc[2][0]), m3 = vmax3(sacc[2][1], sacc[2][2], sacc[2][3]);
+        const float m4 = vmax3(sacc[3][0], sacc[3][1], sacc[3][2]);
+        float mx = vmax(vmax3(m0, m1, sacc[3][3]), vmax3(m2, m3, m4));
+        mx = xor32_combine(xor16_combine(mx, vmax), vmax);  // the 4 lanes of this query
         const float mn = fmaxf(m, mx * a.scale_log2);
         // -inf while every key seen so far is masked (possible in the second
         // set); referencing 0 then keeps alpha and P at exactly 0.
@@ -193,33 +234,43 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
         // v_exp_f32 without the library's denormal-result path: values below
         // 2^-126 become 0, as they do anyway once P is rounded to f16.
         const float alpha = __builtin_amdgcn_exp2f(m - mref);
-        // The row sum takes the float32 probabilities; P enters the MFMA as f16
-        // (hi, and lo with two terms).
+        // P * 2^14 straight from the exponent (the scale is exact); the row sum
+        // takes the same float32 values, so lsum carries the scale too and the
+        // final normalisation cancels it.  P enters the MFMA as f16 (hi, and lo
+        // with two terms).
+        const float eref = kLog2PScale - mref;
         float ps = 0.f;
-        f16 ph[4][4], pl[TT ? 4 : 1][4];
+        // f16 pairs (keys r = 0,1 and 2,3 of tile t): hi = RNE(P), lo = RNE(P - hi)
+        uint32_t ph[4][2], pl[PT ? 4 : 1][2];
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float e = __builtin_amdgcn_exp2f(fmaf(sacc[t][r], a.scale_log2, -mref));
-                const float es = e * kPScale;
-                ph[t][r] = (f16)es;
-                if constexpr (TT) pl[t][r] = (f16)(es - (float)ph[t][r]);
-                ps += e;
+            for (int pr = 0; pr < 2; pr++) {
+                const float e0 = __builtin_amdgcn_exp2f(fmaf(sacc[t][2 * pr], a.scale_log2, eref));
+                const float e1 = __builtin_amdgcn_exp2f(fmaf(sacc[t][2 * pr + 1], a.scale_log2, eref));
+                const uint32_t h = pack_f16x2(e0, e1);
+                ph[t][pr] = h;
+                if constexpr (PT) pl[t][pr] = pack_f16x2(minus_f16_lo(h, e0), minus_f16_hi(h, e1));
+                ps += e0;
+                ps += e1;
             }
         lsum = lsum * alpha + ps;
+        // alpha is exactly 1 in every lane whose running max did not move (the
+        // usual case past the first blocks): the wave then skips the rescale.
+        if (__builtin_amdgcn_ballot_w64(m != mn)) {
 #pragma unroll
-        for (int d = 0; d < DT; d++) oacc[d] *= alpha;
+            for (int d = 0; d < DT; d++) oacc[d] *= alpha;
+        }
         // O^T += V^T P^T.  Key order inside a 32-key step, identical on both
         // operands: slot e < 4 is key 32s + 4g + e, slot e >= 4 is 32s + 16 + 4g + e - 4.
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            const f16x8 pf = {ph[2 * s][0], ph[2 * s][1], ph[2 * s][2], ph[2 * s][3],
-                              ph[2 * s + 1][0], ph[2 * s + 1][1], ph[2 * s + 1][2], ph[2 * s + 1][3]};
+            const f16x8 pf = __builtin_bit_cast(f16x8, make_uint4(ph[2 * s][0], ph[2 * s][1], ph[2 * s + 1][0],
+                                                                  ph[2 * s + 1][1]));
             f16x8 plf;
-            if constexpr (TT)
-                plf = f16x8{pl[2 * s][0], pl[2 * s][1], pl[2 * s][2], pl[2 * s][3],
-                            pl[2 * s + 1][0], pl[2 * s + 1][1], pl[2 * s + 1][2], pl[2 * s + 1][3]};
+            if constexpr (PT)
+                plf = __builtin_bit_cast(f16x8, make_uint4(pl[2 * s][0], pl[2 * s][1], pl[2 * s + 1][0],
+                                                           pl[2 * s + 1][1]));
             const int ra = 32 * s + 4 * g + (c16 >> 2), rb = ra + 16;
 #pragma unroll
             for (int d = 0; d < DT; d++) {
@@ -228,7 +279,7 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
                 const f16x4 hi = lds_read_tr(Vt + rb * ROWB + ((cb ^ kv_swz(rb)) * 16) + hb);
                 const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 oacc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, oacc[d], 0, 0, 0);
-                if constexpr (TT) oacc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, plf, oacc[d], 0, 0, 0);
+                if constexpr (PT) oacc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, plf, oacc[d], 0, 0, 0);
             }
         }
         m = mn;
@@ -297,7 +348,7 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
             for (int r = 0; r < 4; r++) oacc[d][r] = oacc[d][r] * a0 + xo[(d * 4 + r) * 64 + lane] * a1;
     }
     if (qi >= a.T) return;
-    const float inv = (1.0f / lsum) * (1.0f / kPScale);
+    const float inv = 1.0f / lsum;  // lsum and O both carry the 2^14
     // oacc[d][r] = O(query qi, dim 16d + 4g + r)
 #pragma unroll
     for (int d = 0; d < DT; d++) {
@@ -547,22 +598,22 @@ hipError_t decode_dispatch(int G, dim3 grid, hipStream_t st, const float* q, con
 
 }  // namespace
 
-template <bool TT>
+template <bool TT, bool PT>
 hipError_t flash_dispatch(const FlashArgs& a, dim3 grid, int hd, bool out16, hipStream_t st) {
     // One-set workgroups (48 KB of LDS at head dim 64) run three per CU: below
     // three per CU the causal critical path dominates and two sets win.
     const bool two_sets = (int64_t)grid.x * grid.y < 3 * 256;
     if (hd == 64) {
         if (two_sets) {
-            if (out16) flash_attn_kernel<64, 2, true, TT><<<grid, 512, 0, st>>>(a);
-            else flash_attn_kernel<64, 2, false, TT><<<grid, 512, 0, st>>>(a);
+            if (out16) flash_attn_kernel<64, 2, true, TT, PT><<<grid, 512, 0, st>>>(a);
+            else flash_attn_kernel<64, 2, false, TT, PT><<<grid, 512, 0, st>>>(a);
         } else {
-            if (out16) flash_attn_kernel<64, 1, true, TT><<<grid, 256, 0, st>>>(a);
-            else flash_attn_kernel<64, 1, false, TT><<<grid, 256, 0, st>>>(a);
+            if (out16) flash_attn_kernel<64, 1, true, TT, PT><<<grid, 256, 0, st>>>(a);
+            else flash_attn_kernel<64, 1, false, TT, PT><<<grid, 256, 0, st>>>(a);
         }
     } else if (hd == 128) {
-        if (out16) flash_attn_kernel<128, 1, true, TT><<<grid, 256, 0, st>>>(a);
-        else flash_attn_kernel<128, 1, false, TT><<<grid, 256, 0, st>>>(a);
+        if (out16) flash_attn_kernel<128, 1, true, TT, PT><<<grid, 256, 0, st>>>(a);
+        else flash_attn_kernel<128, 1, false, TT, PT><<<grid, 256, 0, st>>>(a);
     } else {
         return hipErrorInvalidValue;
     }
@@ -590,7 +641,10 @@ hipError_t launch_flash_attention(const f16* q, const f16* qlo, int ldq, const f
     a.out16 = out_f16;
     a.out16lo = out_f16_lo;
     dim3 grid(heads, (tokens + BQ - 1) / BQ);
-    return qlo ? flash_dispatch<true>(a, grid, hd, out_f16, st) : flash_dispatch<false>(a, grid, hd, out_f16, st);
+    if (!qlo) return flash_dispatch<false, false>(a, grid, hd, out_f16, st);
+    const char* pe = std::getenv("ALPACA_HIP_FLASH_P_TERMS");
+    if (pe && pe[0] == '1') return flash_dispatch<true, false>(a, grid, hd, out_f16, st);
+    return flash_dispatch<true, true>(a, grid, hd, out_f16, st);
 }
 
 // Splits for the generic kernel: decode spreads the context over >= 64-key
