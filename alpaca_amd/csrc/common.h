@@ -336,13 +336,10 @@ struct DecodeParams {
 // Phase-end stamps per launch: [0] start, 6 per layer (qkv, attention, merge,
 // wo, gate/up, down), then logits and the arg-max (workgroup 0 only).
 __host__ __device__ inline int decode_trace_points(int layers) { return 3 + 6 * layers; }
-// After those points, kDecodeAttnSubPoints stamps inside the phases of the
-// last layer (the last value written wins): [0, 8) the attention item (entry,
-// loads issued, q ready, current k/v ready, scores, softmax, P.V, published);
-// then four per phase (entry, inputs arrived, inputs staged / normalised, rows
-// done) for QKV [8, 12), merge [12, 16), Wo [16, 20), gate/up [20, 24) and
-// down [24, 28).
-constexpr int kDecodeAttnSubPoints = 28;
+// After those points, kDecodeAttnSubPoints stamps inside the attention phase
+// of the last layer (the last value written wins): entry, loads issued, q
+// ready, current k/v ready, scores, softmax, P.V, published.
+constexpr int kDecodeAttnSubPoints = 8;
 // Support, shared-memory size and launch of the persistent decode kernel.
 bool decode_kernel_supported(int fmt, int hd, int heads, int kv_heads);
 int decode_attention_max_splits(int capacity, int kv_heads, int target_items);

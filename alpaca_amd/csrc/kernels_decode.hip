@@ -136,13 +136,6 @@ __device__ __forceinline__ Shared lds_of() {
     return l;
 }
 
-// Profiling: thread 0 stamps sub-point k of the current phase (the points
-// after the phase-end stamps; each layer overwrites the previous layer's).
-__device__ __forceinline__ void substamp(int k) {
-    const DecodeParams& p = P();
-    if (p.trace && threadIdx.x == 0)
-        *gptr(p.trace + (int64_t)(decode_trace_points(p.n_layers) + k) * gridDim.x + blockIdx.x) = wall_clock64();
-}
 
 // ------------------------------------------------------------------ exchange words
 __device__ __forceinline__ u64 ld_word(const u64* p) {
@@ -161,7 +154,16 @@ struct Ctl {
     unsigned* abort_word;
     int* status;
     long long timeout;
+    unsigned long long* sub;  // profiling: the sub-point stamps, or null
 };
+
+// Profiling: thread 0 stamps sub-point k of the attention phase (the points
+// after the phase-end stamps; each layer overwrites the previous layer's).
+// The pointer travels in Ctl (registers), so an untraced launch pays one
+// scalar test per point.
+__device__ __forceinline__ void substamp(const Ctl& c, int k) {
+    if (c.sub && threadIdx.x == 0) *gptr(c.sub + (int64_t)k * gridDim.x + blockIdx.x) = wall_clock64();
+}
 
 __device__ __noinline__ void raise_abort(Ctl c) {
     __hip_atomic_store(gptr(c.abort_word), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -433,7 +435,6 @@ struct PhaseQKV {
         const Shared sh = lds_of();
         const DevMatrix W = L.qkv;
         const int hd = p.hd, QW = p.heads * hd, KW = p.kv_heads * hd, half = hd / 2, cap = p.capacity;
-        substamp(8);
         int r0, r1;
         my_rows(p.rows_qkv, W.rows, r0, r1);
         Rows<FMT, LPR, false> rw;
@@ -452,9 +453,7 @@ struct PhaseQKV {
             for (int k = threadIdx.x; k < H; k += kT) sh.xres[k] = matrix_elem(E, token, k);
             __syncthreads();
         }
-        substamp(9);
         rmsnorm_lds(sh.xres, gain, H, p.eps, sh.xn, sh.red);
-        substamp(10);
         // RoPE on the pair, f16 rounding of k/v as the cache stores them, cache
         // append at row pos (KVCache.write, KVCache.swift:44-63), publication.
         f16* kc = (f16*)L.kc;
@@ -483,7 +482,6 @@ struct PhaseQKV {
             put_word(o + r, v0, tag);
             put_word(o + r + 1, v1, tag);
         });
-        substamp(11);
         return true;
     }
 };
@@ -564,11 +562,7 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
     const float sl2 = 1.4426950408889634f / sqrtf((float)HD);
     auto fmax2 = [](float x, float y) { return fmaxf(x, y); };
     auto add2 = [](float x, float y) { return x + y; };
-    unsigned long long* sub_trace =
-        p.trace ? p.trace + (int64_t)decode_trace_points(p.n_layers) * gridDim.x : nullptr;
-    auto sub = [&](int k) {
-        if (sub_trace && tid == 0) *gptr(sub_trace + (int64_t)k * gridDim.x + blockIdx.x) = wall_clock64();
-    };
+    auto sub = [&](int k) { substamp(c, k); };
     // An item's cached K rows (cache rows past nc are loaded from row 0 of the
     // split, valid memory, and never used).  A workgroup with several items loads
     // the next item's K rows and V rows once the current P.V is done, so those
@@ -807,10 +801,8 @@ __device__ __forceinline__ bool merge_phase(const u64* part, u64* ctx, int pos, 
     const int SL = split_len_for(len, p.kv_heads, p.target_items);
     const int S = (len + SL - 1) / SL;
     float* wsplit = scr + S * (HD + 2);
-    substamp(12);
     for (int h = blockIdx.x; h < heads; h += gridDim.x) {
         if (!wait_words(part + (int64_t)h * max_splits * (HD + 2), S * (HD + 2), scr, c)) return false;
-        substamp(13);
         float m = -INFINITY;
         for (int s = threadIdx.x; s < S; s += kT) m = fmaxf(m, scr[s * (HD + 2)]);
         m = wave_max(m);
@@ -836,7 +828,6 @@ __device__ __forceinline__ bool merge_phase(const u64* part, u64* ctx, int pos, 
         o = lane_sum<QPD>(o);
         if (q == 0) put_word(ctx + h * HD + d, o * inv, c.tag);
         __syncthreads();
-        substamp(15);
     }
     return true;
 }
@@ -853,8 +844,6 @@ struct PhaseResidual {
         const DecodeParams& p = P();
         const Shared sh = lds_of();
         const DevMatrix W = which ? LY().down : LY().wo;
-        const int sp = which ? 24 : 16;
-        substamp(sp);
         int r0, r1;
         my_rows(which ? p.rows_down : p.rows_wo, W.rows, r0, r1);
         Rows<FMT, LPR, false> rw;
@@ -865,14 +854,11 @@ struct PhaseResidual {
         // still reading.  Attention and merge items end with a barrier, but a
         // workgroup that has none goes straight from QKV to here.
         __syncthreads();
-        substamp(sp + 1);
         if (!wait_words(in, W.cols, sh.xn, c)) return false;
-        substamp(sp + 2);
         const unsigned tag = c.tag;
         const float* xres = sh.xres;
         u64* o = out;
         rw.run(W, W, r0, r1, sh.xn, [&](int r, float v, float) { put_word(o + r, xres[r] + v, tag); });
-        substamp(sp + 3);
         return true;
     }
 };
@@ -890,7 +876,6 @@ struct PhaseGateUp {
         const DecLayer& L = LY();
         const Shared sh = lds_of();
         const DevMatrix Wg = L.gate, Wu = L.up;
-        substamp(20);
         int r0, r1;
         my_rows(p.rows_ffn, Wg.rows, r0, r1);
         Rows<FMT, LPR, true> rw;
@@ -898,12 +883,10 @@ struct PhaseGateUp {
         NormGain gain;
         gain.load(L.ffn_norm, p.hidden);
         if (!wait_rmsnorm(in, p.hidden, sh.xres, gain, p.eps, sh.xn, sh.red, c)) return false;
-        substamp(22);
         const unsigned tag = c.tag;
         u64* o = out;
         rw.run(Wg, Wu, r0, r1, sh.xn,
                [&](int r, float g, float u) { put_word(o + r, (g / (1.0f + expf(-g))) * u, tag); });
-        substamp(23);
         return true;
     }
 };
@@ -1004,6 +987,7 @@ __global__ __launch_bounds__(kT) void decode_step_kernel(DecodeParams kp) {
     c.abort_word = kp.abort_word;
     c.status = kp.status;
     c.timeout = kp.timeout_ticks;
+    c.sub = kp.trace ? kp.trace + (int64_t)decode_trace_points(kp.n_layers) * gridDim.x : nullptr;
     const int pos = *(volatile int*)kp.pos;
     const int token = *(volatile int*)kp.chain;
     const int n_layers = kp.n_layers, layer_words = kp.layer_words;
