@@ -7,13 +7,35 @@ same method names (snake_case), argument meaning and error behaviour.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
+import weakref
 from dataclasses import dataclass, field
 
 import numpy as np
 
 from . import _lib as L
 from .tensor import QTensor
+
+# Handles still open when the interpreter exits are closed by an atexit hook
+# (sessions, then models, then contexts), which runs at the start of
+# interpreter finalization, while the library and the HIP runtime are intact.
+# Left to finalizers at module teardown they may not be released at all, and
+# the HIP runtime then frees the session's streams, events and mapped host
+# words in its own exit handlers, after an attached profiler (rocprofv3) has
+# finalized the API tables it intercepts.
+_LIVE: "weakref.WeakSet" = weakref.WeakSet()
+
+
+def close_all() -> None:
+    """Closes every session, model and context still open, in that order."""
+    for kind in ("session", "model", "context"):
+        for obj in list(_LIVE):
+            if getattr(obj, "_kind", None) == kind:
+                obj.close()
+
+
+atexit.register(close_all)
 
 
 class HIPContext:
@@ -24,6 +46,8 @@ class HIPContext:
         L.check(L.lib().ahip_context_create(device, C.byref(h)))
         self.handle = h
         self.device = device
+        self._kind = "context"
+        _LIVE.add(self)
 
     @staticmethod
     def is_available() -> bool:
@@ -95,6 +119,8 @@ class HIPLlamaModel:
         L.check(L.lib().ahip_model_create(context.handle, C.byref(cfg), arr, len(descs),
                                           1 if prefill_weight_cache else 0, C.byref(h)))
         self.handle = h
+        self._kind = "model"
+        _LIVE.add(self)
 
     @property
     def weight_bytes(self) -> int:
@@ -147,6 +173,8 @@ class HIPLlamaSession:
         L.check(L.lib().ahip_session_create(model.handle, capacity, max_batch, KV[kv_precision],
                                             GEMM[gemm_precision], C.byref(h)))
         self.handle = h
+        self._kind = "session"
+        _LIVE.add(self)
         self.gpu_seconds = 0.0  # accumulated, as MetalSessionAdapter.gpuSeconds
 
     # -- InferenceSession ---------------------------------------------------

@@ -30,10 +30,19 @@ embeddings), random-init synthetic weights, all resident in HBM.
     at context 2048) and C5 (1.7B-shape Q8_0, decode at 4096, 4096-token
     prefill) with their fractions of the HBM and MFMA rooflines; reported
     beside the C1 value, not instead of it.
-  * cpu_baseline: the C oracle (restatement of AlpacaCore's CPU path) on the
-    host cores: decode steps at context 2048 (the oracle's cache is filled
-    with synthetic rows, since prefilling 2048 positions on the CPU would take
-    minutes).
+  * cpu_baseline: the C oracle (restatement of AlpacaCore's CPU path, threaded
+    over 16-row chunks of each linear as CPUOps does with concurrentPerform) on
+    every host core this process may run on (capped by OMP_NUM_THREADS when
+    set: the GPU box's CPU share): `value` is decode tok/s at context 2048 (the
+    oracle's cache is filled with synthetic rows, since prefilling 2048
+    positions on the CPU would take minutes), beside the reference's own
+    CPU-runnable case (a 128-token prompt, then 16
+    greedy tokens) as prefill and decode tok/s; nproc and the CPU model are
+    recorded.
+  * roofline.traffic: HBM bytes per decode launch from the committed counter
+    summary (profiles/c1_decode_hbm_counters.md), used only when the summary
+    was measured on the decode kernel's current sources (it records a hash of
+    them; see --counter-summary), else null with the reason.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -145,30 +154,120 @@ def stage_table(profile: dict, units: dict, scale: float, unit: str, per: int = 
     return out
 
 
+DECODE_SOURCES = ("alpaca_amd/csrc/kernels_decode.hip", "alpaca_amd/csrc/gemv_chunks.h", "alpaca_amd/csrc/common.h",
+                  "alpaca_amd/csrc/runtime.cpp")
+
+
+def source_hash(root: str) -> str:
+    """sha256 (first 16 hex digits) of the sources that decide the decode
+    kernel's memory traffic: its kernel file, the shared headers and the host
+    side that sets its launch (items, workgroups, exchange layout)."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in DECODE_SOURCES:
+        with open(os.path.join(root, rel), "rb") as f:
+            h.update(rel.encode() + b"\0" + f.read())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic(root: str):
-    """HBM bytes per decode launch from the committed rocprofv3 counter summary
-    (FETCH_SIZE and WRITE_SIZE runs, scaled by a copy of known size), or None."""
+    """(HBM bytes per decode launch, source note) from the committed rocprofv3
+    counter summary, or (None, reason) when it is missing or was measured on
+    other decode sources than this tree's."""
     import re
-    path = os.path.join(root, "profiles", "c1_decode_hbm_counters.md")
+    rel = "profiles/c1_decode_hbm_counters.md"
     try:
-        with open(path) as f:
-            m = re.search(r"Traffic per launch[^:]*:\s*([0-9.]+)\s*MB", f.read())
+        with open(os.path.join(root, rel)) as f:
+            text = f.read()
     except OSError:
-        return None
-    return None if not m else float(m.group(1)) * 1e6
+        return None, f"{rel} missing"
+    m = re.search(r"Traffic per launch[^:]*:\s*([0-9.]+)\s*MB", text)
+    h = re.search(r"Decode source hash:\s*([0-9a-f]+)", text)
+    cur = source_hash(root)
+    if not m or not h:
+        return None, f"{rel} has no traffic figure or source hash"
+    if h.group(1) != cur:
+        return None, f"stale: {rel} was measured on decode sources {h.group(1)}, this tree has {cur}"
+    return float(m.group(1)) * 1e6, f"{rel} (rocprofv3 FETCH_SIZE and WRITE_SIZE runs, scaled by a copy; sources {cur})"
+
+
+def counter_summary(dirs: dict, kernel: str) -> int:
+    """Markdown summary of rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of
+    `kernel` and of the calibration copy, with the source hash bench.py checks."""
+    import glob
+    import sqlite3
+
+    def values(d: str, name: str, counter: str):
+        out = []
+        for db in glob.glob(os.path.join(d, "**", "*results.db"), recursive=True):
+            con = sqlite3.connect(db)
+            rows = con.execute("select kernel_name, counter_name, value from counters_collection").fetchall()
+            out += [v for k, c, v in rows if name in k and c == counter]
+        return out
+
+    cf, cw = values(dirs["copy_fetch"], "copyBuffer", "FETCH_SIZE"), values(dirs["copy_write"], "copyBuffer", "WRITE_SIZE")
+    kf, kw = values(dirs["fetch"], kernel, "FETCH_SIZE"), values(dirs["write"], kernel, "WRITE_SIZE")
+    if not (cf and cw and kf and kw):
+        print("missing counter rows", file=sys.stderr)
+        return 1
+    copy_kib = 256 * 1024
+    sf, sw = copy_kib / max(cf), copy_kib / max(cw)
+    mf, mw = sum(kf) / len(kf), sum(kw) / len(kw)
+    traffic = (mf * sf + mw * sw) * 1024 / 1e6
+    root = os.path.dirname(os.path.abspath(__file__))
+    print(f"Calibration: a 256 MiB device-to-device copy reads FETCH_SIZE = {max(cf):,.0f} KiB and "
+          f"WRITE_SIZE = {max(cw):,.0f} KiB: FETCH_SIZE is scaled by {sf:.2f}, WRITE_SIZE by {sw:.2f}.\n")
+    print(f"| counter | dispatches of {kernel} | mean KiB / dispatch | min | max | scaled MB / dispatch |")
+    print("|---|---:|---:|---:|---:|---:|")
+    for name, v, sc in (("FETCH_SIZE", kf, sf), ("WRITE_SIZE", kw, sw)):
+        print(f"| {name} | {len(v)} | {sum(v) / len(v):.1f} | {min(v):.1f} | {max(v):.1f} | "
+              f"{sum(v) / len(v) * sc * 1024 / 1e6:.1f} |")
+    print(f"\nTraffic per launch: {traffic:.1f} MB\n\nDecode source hash: {source_hash(root)}")
+    return 0
+
+
+def cpu_info() -> dict:
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    cap = os.environ.get("OMP_NUM_THREADS")
+    threads = min(avail, int(cap)) if cap and cap.isdigit() and int(cap) > 0 else avail
+    return {"nproc": os.cpu_count(), "affinity_cores": avail, "threads": threads, "cpu_model": model}
 
 
 def cpu_baseline(weights, spec, budget_s: float = 12.0) -> dict:
     import numpy as np
 
+    from alpaca_amd import synth
     import oracle.oracle as orc
     c = spec.config
     cfg = dict(vocab=c.vocab_size, hidden=c.hidden_size, layers=c.layer_count, heads=c.head_count,
                kv_heads=c.kv_head_count, head_dim=c.head_dim, ffn=c.feed_forward_size, context=c.context_length,
                eps=c.rms_norm_eps, theta=c.rope_theta, interleaved=c.rope_interleaved)
     om = orc.OracleModel(cfg, {n: (t.dtype, t.data) for n, t in weights.items()})
-    threads = min(16, os.cpu_count() or 1)
-    orc.set_threads(threads)
+    info = cpu_info()
+    orc.set_threads(info["threads"])
+    # the reference's CPU-runnable case: 128-token prompt, then 16 greedy tokens
+    kv0 = orc.OracleKV(cfg, 256)
+    prompt = synth.prompt_tokens(spec, 128)
+    t0 = time.perf_counter()
+    tok = int(np.argmax(orc.forward(om, kv0, prompt)))
+    pre_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    for _ in range(16):
+        tok = int(np.argmax(orc.forward(om, kv0, [tok])))
+    dec128_s = time.perf_counter() - t0
+    # the headline point: decode at context 2048
     kv = orc.OracleKV(cfg, DECODE_CTX + 64)
     kv.fill(DECODE_CTX - 1, seed=7)
     tok = 1
@@ -180,9 +279,11 @@ def cpu_baseline(weights, spec, budget_s: float = 12.0) -> dict:
         el = time.perf_counter() - t0
         if (el > budget_s and steps >= 2) or steps >= 64:
             break
-    return {"value": round(steps / el, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+    return {"value": round(steps / el, 3), "unit": "tok/s", "cores": info["threads"], "kind": "port",
             "sample": f"C1 decode, {steps} greedy steps starting at ctx {DECODE_CTX} (oracle KV cache filled with "
-                      f"synthetic rows), oracle threaded over 16-row chunks of each linear as AlpacaCore"}
+                      f"synthetic rows), oracle threaded over 16-row chunks of each linear as AlpacaCore",
+            "prefill_128_tok_s": round(128 / pre_s, 2), "decode_after_128_tok_s": round(16 / dec128_s, 3),
+            "nproc": info["nproc"], "affinity_cores": info["affinity_cores"], "cpu_model": info["cpu_model"]}
 
 
 def main() -> int:
@@ -202,7 +303,13 @@ def main() -> int:
                     help="only the timed decode steps (for counter passes of the decode kernel)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only a device-to-device copy of 256 MiB, the reference the HBM byte counters are scaled by")
+    ap.add_argument("--counter-summary", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
+                    help="print the markdown summary of rocprofv3 --pmc output directories (no GPU use)")
+    ap.add_argument("--counter-kernel", default="decode_step_kernel")
     args = ap.parse_args()
+    if args.counter_summary:
+        fd, wd, cfd, cwd = args.counter_summary
+        return counter_summary({"fetch": fd, "write": wd, "copy_fetch": cfd, "copy_write": cwd}, args.counter_kernel)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures the single-GPU hot path only: this build runs on one GPU "
@@ -263,11 +370,12 @@ def main() -> int:
     mean_ctx = decode_ctx + (args.steps - 1) / 2 + 1
     tok_bytes = decode_token_bytes(c, mean_ctx, block)
     achieved = tok_bytes / avg_launch / 1e9
+    traffic, traffic_note = (measured_traffic(os.path.dirname(os.path.abspath(__file__))) if args.config == "C1"
+                             else (None, "counters are summarised for C1 only"))
     roof = {"bound": "hbm", "kernel": "decode_step_kernel (persistent, one cooperative launch per token)",
             "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 5),
-            "traffic": measured_traffic(os.path.dirname(os.path.abspath(__file__))) if args.config == "C1" else None,
-            "traffic_source": "profiles/c1_decode_hbm_counters.md (rocprofv3 FETCH_SIZE x2.00 + WRITE_SIZE x1.00)",
+            "traffic": traffic, "traffic_source": traffic_note,
             "bytes_per_launch": int(tok_bytes), "avg_launch_us": round(avg_launch * 1e6, 3),
             "timing": "HIP events on the session stream around the timed steps, divided by the steps"}
     log(f"decode: {decode_tok_s:.1f} tok/s ({el / args.steps * 1e3:.3f} ms/token wall, "
@@ -365,7 +473,9 @@ def main() -> int:
     if not args.no_cpu_baseline:
         log("CPU oracle baseline ...")
         cpu = cpu_baseline(weights, spec)
-        log(f"CPU oracle: {cpu['value']} tok/s on {cpu['cores']} threads")
+        log(f"CPU oracle: {cpu['value']} tok/s decode at ctx {DECODE_CTX}, 128-token prefill "
+            f"{cpu['prefill_128_tok_s']} tok/s, decode after it {cpu['decode_after_128_tok_s']} tok/s, on "
+            f"{cpu['cores']} threads ({cpu['cpu_model']}, nproc {cpu['nproc']})")
 
     line = {
         "metric": METRIC, "value": round(decode_tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
