@@ -554,14 +554,20 @@ template <int FMT, int BM, int BN, int WM, int WN, int MODE, bool TT>
 struct DGemm {
     static constexpr int NB = MODE == GEMM_SWIGLU ? 2 : 1;
     static constexpr int TM = WM / 16, TN = WN / 16;
-    static_assert((BM / WM) * (BN / WN) == 4, "four waves");
-    // DMA instructions per wave per stage (A rows: 8 of 128 B per instruction, 4 waves; twice with two terms)
-    static constexpr int A_I = BM / 32;
-    static constexpr bool Q4_16 = (BN / 32) % 4 == 0;
-    static constexpr int B_I = FMT == DT_Q8_0 ? BN / 64 : FMT == DT_Q4_0 ? (Q4_16 ? BN / 128 : BN / 32) : BN / 32;
-    static constexpr int S_I = FMT == DT_F16 ? 0 : 1;  // a quarter of the tile's scale pairs per wave
+    // waves per workgroup: four (one per SIMD) or eight (two per SIMD, so that
+    // one wave's VALU work can issue while the other's MFMAs run)
+    static constexpr int NW = (BM / WM) * (BN / WN);
+    static_assert(NW == 4 || NW == 8, "four or eight waves");
+    // DMA instructions per wave per stage (A rows: 8 of 128 B per instruction; twice with two terms)
+    static constexpr int A_I = BM / (8 * NW);
+    static constexpr bool Q4_16 = (BN / 8) % (4 * NW) == 0;
+    static constexpr int B_I = FMT == DT_Q8_0   ? BN / (16 * NW)
+                               : FMT == DT_Q4_0 ? (Q4_16 ? BN / (32 * NW) : BN / (8 * NW))
+                                                : BN / (8 * NW);
+    static constexpr int S_I = FMT == DT_F16 ? 0 : 1;  // 1/NW of the tile's scale pairs per wave
     static constexpr int PER = A_I * (TT ? 2 : 1) + NB * (B_I + S_I);
-    static_assert(BM % 32 == 0 && BN % 64 == 0, "tile shape");
+    static_assert(A_I >= 1 && B_I >= 1 && BM % (8 * NW) == 0 && BN % (16 * NW) == 0 && BN / (4 * NW) <= 64,
+                  "tile shape");
 };
 
 // Epilogues that read memory (GEMM_ACC reads the residual rows, GEMM_QKV_ROPE
@@ -642,13 +648,14 @@ __device__ __forceinline__ void qkv_rope_epilogue(const GemmArgs& p, const f32x4
         const int total = min(BM, M - m0) * half / 2;  // float4 = two (cos, sin) pairs
         const float4* src = (const float4*)(o.rope + (int64_t)(o.pos + m0) * half);
         float4* dst = (float4*)smem;
-        for (int base = 0; base < total; base += 8 * 256) {
+        const int nt = blockDim.x;
+        for (int base = 0; base < total; base += 8 * nt) {
             float4 v[8];  // loads clamped to the last element (valid memory), stores guarded
 #pragma unroll
-            for (int u = 0; u < 8; u++) v[u] = src[min(base + (int)threadIdx.x + 256 * u, total - 1)];
+            for (int u = 0; u < 8; u++) v[u] = src[min(base + (int)threadIdx.x + nt * u, total - 1)];
 #pragma unroll
             for (int u = 0; u < 8; u++) {
-                const int k = base + threadIdx.x + 256 * u;
+                const int k = base + threadIdx.x + nt * u;
                 if (k < total) dst[k] = v[u];
             }
         }
@@ -716,10 +723,10 @@ __device__ __forceinline__ void qkv_rope_epilogue(const GemmArgs& p, const f32x4
 // RH: for GEMM_QKV_ROPE, the largest head dim the RoPE staging holds (64 or
 // 128); 0 for the other modes.
 template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH, bool TT>
-__global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
+__global__ __launch_bounds__(64 * (BM / WM) * (BN / WN)) void dgemm_kernel(GemmArgs p) {
     using G = DGemm<FMT, BM, BN, WM, WN, MODE, TT>;
     using L = DStage<FMT, BM, BN, G::NB, TT>;
-    constexpr int NB = G::NB, TM = G::TM, TN = G::TN, PER = G::PER;
+    constexpr int NB = G::NB, TM = G::TM, TN = G::TN, PER = G::PER, NW = G::NW;
     // The stage buffers, in one array that the GEMM_QKV_ROPE epilogue reuses
     // for the tile's RoPE rows (BM positions x RH/2 pairs of 8 bytes: 32 KB at
     // head dim 64, so a 128x64 QKV tile keeps the two-stage footprint).
@@ -750,7 +757,7 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
     uint32_t aoff[G::A_I], boff[NB][G::B_I], soff = 0;
 #pragma unroll
     for (int i = 0; i < G::A_I; i++) {
-        const int r = (i * 4 + wave) * 8 + (lane >> 3), c = (lane & 7) ^ swz_a(r);
+        const int r = (i * NW + wave) * 8 + (lane >> 3), c = (lane & 7) ^ swz_a(r);
         aoff[i] = (uint32_t)((min(m0 + r, M - 1) * p.ldx + c * 8) * 2);
     }
 #pragma unroll
@@ -758,28 +765,28 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
 #pragma unroll
         for (int i = 0; i < G::B_I; i++) {
             if constexpr (FMT == DT_Q8_0) {
-                const int r = (i * 4 + wave) * 16 + (lane >> 2), c = (lane & 3) ^ swz_q8(r);
+                const int r = (i * NW + wave) * 16 + (lane >> 2), c = (lane & 3) ^ swz_q8(r);
                 boff[mat][i] = (uint32_t)(min(n0 + r, N - 1) * K + c * 16);
             } else if constexpr (FMT == DT_Q4_0) {
                 if constexpr (G::Q4_16) {
-                    const int r = (i * 4 + wave) * 32 + (lane >> 1), c = (lane & 1) ^ swz_q4(r);
+                    const int r = (i * NW + wave) * 32 + (lane >> 1), c = (lane & 1) ^ swz_q4(r);
                     boff[mat][i] = (uint32_t)((min(n0 + r, N - 1) * nb + c) * 16);
                 } else {
-                    const int r = (i * 4 + wave) * 8 + (lane >> 3), c = ((lane >> 2) & 1) ^ swz_q4(r);
+                    const int r = (i * NW + wave) * 8 + (lane >> 3), c = ((lane >> 2) & 1) ^ swz_q4(r);
                     boff[mat][i] = (uint32_t)((min(n0 + r, N - 1) * nb + c) * 16 + (lane & 3) * 4);
                 }
             } else {
-                const int r = (i * 4 + wave) * 8 + (lane >> 3), c = (lane & 7) ^ swz_a(r);
+                const int r = (i * NW + wave) * 8 + (lane >> 3), c = (lane & 7) ^ swz_a(r);
                 boff[mat][i] = (uint32_t)((min(n0 + r, N - 1) * K + c * 8) * 2);
             }
         }
-    if constexpr (FMT != DT_F16) soff = (uint32_t)((n0 + wave * (BN / 4) + lane * 4) * 4);
+    if constexpr (FMT != DT_F16) soff = (uint32_t)((n0 + wave * (BN / NW) + lane * 4) * 4);
 
     auto issue = [&](uint32_t sg, int kt) {  // sg: LDS byte address of the stage buffer
         const int k0 = kt * DBK;
 #pragma unroll
         for (int i = 0; i < G::A_I; i++) {
-            const int r0 = (i * 4 + wave) * 8;
+            const int r0 = (i * NW + wave) * 8;
             dma16s(p.x + k0, aoff[i], sg + r0 * DBK * 2);
             if constexpr (TT) dma16s(p.xlo + k0, aoff[i], sg + L::A_LO + r0 * DBK * 2);
         }
@@ -790,18 +797,19 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
 #pragma unroll
             for (int i = 0; i < G::B_I; i++) {
                 if constexpr (FMT == DT_Q8_0) {
-                    dma16s(w.q + k0, boff[mat][i], bq + (i * 4 + wave) * 16 * 64);
+                    dma16s(w.q + k0, boff[mat][i], bq + (i * NW + wave) * 16 * 64);
                 } else if constexpr (FMT == DT_Q4_0) {
-                    if constexpr (G::Q4_16) dma16s(w.q + kt * 32, boff[mat][i], bq + (i * 4 + wave) * 32 * 32);
-                    else dma4s(w.q + kt * 32, boff[mat][i], bq + (i * 4 + wave) * 8 * 32);
+                    if constexpr (G::Q4_16) dma16s(w.q + kt * 32, boff[mat][i], bq + (i * NW + wave) * 32 * 32);
+                    else dma4s(w.q + kt * 32, boff[mat][i], bq + (i * NW + wave) * 8 * 32);
                 } else {
-                    dma16s(w.q + k0 * 2, boff[mat][i], bq + (i * 4 + wave) * 8 * 128);
+                    dma16s(w.q + k0 * 2, boff[mat][i], bq + (i * NW + wave) * 8 * 128);
                 }
             }
             if constexpr (FMT != DT_F16) {
-                // The tile's BN scale pairs are contiguous in s2: each wave moves a
-                // quarter of them, 16 bytes (4 rows) per active lane.
-                if (lane < BN / 16) dma16s(w.s2 + (int64_t)kt * spitch, soff, sg + L::S_OFF + mat * BN * 4 + wave * BN);
+                // The tile's BN scale pairs are contiguous in s2: each wave moves
+                // 1/NW of them, 16 bytes (4 rows) per active lane.
+                if (lane < BN / (4 * NW))
+                    dma16s(w.s2 + (int64_t)kt * spitch, soff, sg + L::S_OFF + mat * BN * 4 + wave * (BN / NW) * 4);
             }
         }
     };
@@ -979,7 +987,7 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs p) {
 template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH, bool TT>
 hipError_t run_dgemm(const GemmArgs& a, hipStream_t st) {
     const int tiles = ((a.M + BM - 1) / BM) * ((a.w.rows + BN - 1) / BN);
-    dgemm_kernel<FMT, BM, BN, WM, WN, MODE, RH, TT><<<tiles, 256, 0, st>>>(a);
+    dgemm_kernel<FMT, BM, BN, WM, WN, MODE, RH, TT><<<tiles, 64 * (BM / WM) * (BN / WN), 0, st>>>(a);
     return hipGetLastError();
 }
 
@@ -1015,7 +1023,8 @@ template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH, bool TT>
 int resident_per_cu() {
     static const int v = [] {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, dgemm_kernel<FMT, BM, BN, WM, WN, MODE, RH, TT>, 256, 0) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, dgemm_kernel<FMT, BM, BN, WM, WN, MODE, RH, TT>,
+                                                         64 * (BM / WM) * (BN / WN), 0) !=
                 hipSuccess || n < 1) {
             hipGetLastError();
             return 1;
@@ -1040,25 +1049,29 @@ hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
     // with two terms they do not fit LDS).  With two activation terms a
     // 128x64 tile moves 36 KB per 64-wide K stage for 2 MFLOP and is bound by
     // the global->LDS rate; 128x256 tiles (128x128 per matrix for SwiGLU,
-    // three stages, 147 KB of LDS) halve the bytes per MFMA and are taken on
-    // grids of whole rounds.  Single-term activations stay on the narrower
-    // tiles, where the wide ones measured slower.  128x64 tiles (two LDS
-    // stages) are kept while their grid fits in one round of the workgroups
-    // the device holds at once; past it (a near-empty second round, e.g. a
-    // 1600-column QKV over 4096 rows) 128x128 tiles are faster.
+    // three stages, 147 KB of LDS, one workgroup per CU) halve the bytes per
+    // MFMA and are taken on grids of whole rounds.  They run eight waves of
+    // 64x64 (64x32 per matrix), two per SIMD, so that one wave's VALU work
+    // (block scaling, quant conversion) issues while the other's MFMAs run:
+    // at the 1.7B shape 4-7% faster than four waves of 64x128.  Single-term
+    // activations stay on the narrower tiles, where the wide ones measured
+    // slower.  128x64 tiles (two LDS stages) are kept while their grid fits in
+    // one round of the workgroups the device holds at once; past it (a
+    // near-empty second round, e.g. a 1600-column QKV over 4096 rows) 128x128
+    // tiles are faster.
     if constexpr (MODE == GEMM_SWIGLU) {
         if constexpr (!TT)
             if (f == 1) return run_dgemm<FMT, 256, 64, 128, 32, MODE, RH, TT>(a, st);
         if constexpr (FMT != DT_F16)  // (f16 weight stages are 4x larger: no third stage fits)
             if (f == 4 || (f == 0 && TT && wide_fits(tiles(128, 128))))
-                return run_dgemm<FMT, 128, 128, 64, 64, MODE, RH, TT>(a, st);
+                return run_dgemm<FMT, 128, 128, 64, 32, MODE, RH, TT>(a, st);
         return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH, TT>(a, st);
     } else {
         if constexpr (!TT)
             if (f == 1) return run_dgemm<FMT, 256, 128, 128, 64, MODE, RH, TT>(a, st);
         if constexpr (FMT != DT_F16)
             if (f == 4 || (f == 0 && TT && wide_fits(tiles(128, 256))))
-                return run_dgemm<FMT, 128, 256, 64, 128, MODE, RH, TT>(a, st);
+                return run_dgemm<FMT, 128, 256, 64, 64, MODE, RH, TT>(a, st);
         const int slots = resident_per_cu<FMT, 128, 64, 64, 32, MODE, RH, TT>() * cus;
         if (f == 2 || (f == 0 && tiles(128, 64) > slots)) return run_dgemm<FMT, 128, 128, 64, 64, MODE, RH, TT>(a, st);
         return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH, TT>(a, st);

@@ -928,7 +928,20 @@ static int pdec_launch(ahip_session* s, bool logits, bool emitted) {
         HIP_OR(hipEventRecord(s->pdec_peer, order.last_stream), "hipEventRecord on the previous session's stream");
         HIP_OR(hipStreamWaitEvent(s->stream, s->pdec_peer, 0), "order after another session");
     }
-    LAUNCH(launch_decode_step(s->pdec_fmt, p, s->pdec_grid, s->pdec_lds, s->pdec_coop, s->stream));
+    hipError_t le = launch_decode_step(s->pdec_fmt, p, s->pdec_grid, s->pdec_lds, s->pdec_coop, s->stream);
+    if (le != hipSuccess && s->pdec_coop) {
+        // The runtime refuses cooperative launches in a process while another
+        // process on the device holds its cooperative-launch resource
+        // (hipErrorIllegalState).  The session then launches the same kernel
+        // the ordinary way for the rest of its life: its workgroups (one per
+        // CU) are all resident on a device that is otherwise idle, and every
+        // wait inside the kernel is bounded, so a launch that cannot get the
+        // whole chip aborts with AHIP_ERR_COMMAND_FAILED instead of hanging.
+        hipGetLastError();
+        s->pdec_coop = 0;
+        le = launch_decode_step(s->pdec_fmt, p, s->pdec_grid, s->pdec_lds, 0, s->stream);
+    }
+    LAUNCH(le);
     order.last = s;
     order.last_stream = s->stream;
     s->pdec_launches++;
