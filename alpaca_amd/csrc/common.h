@@ -332,6 +332,10 @@ struct DecodeParams {
     int off_part = 0, off_ctx = 0, off_xa = 0, off_ffn = 0, off_xf = 0, layer_words = 0, off_cand = 0;
     // rows per workgroup of each projection (even)
     int rows_qkv = 0, rows_wo = 0, rows_ffn = 0, rows_down = 0, rows_out = 0;
+    // leading rows of a workgroup's output-matrix share that the logits phase
+    // stages in LDS by DMA before its wait (the rest stream through registers)
+    int out_lds_rows = 0;
+    int out_lds_off = 0;  // their byte offset in dynamic LDS (past every phase's use)
 };
 // Phase-end stamps per launch: [0] start, 6 per layer (qkv, attention, merge,
 // wo, gate/up, down), then logits and the arg-max (workgroup 0 only).
@@ -344,6 +348,13 @@ constexpr int kDecodeAttnSubPoints = 8;
 bool decode_kernel_supported(int fmt, int hd, int heads, int kv_heads);
 int decode_attention_max_splits(int capacity, int kv_heads, int target_items);
 size_t decode_lds_bytes(const DecodeParams& p, int grid);
+// Static LDS of the kernel variant (launch parameters and layer table).
+size_t decode_static_lds(int fmt, int hd, int heads, int kv_heads);
+// Byte offset of the staged output rows in dynamic LDS (past every phase's
+// use), and the most rows of a share of `rows_out` that fit below `lds_limit`
+// bytes from there (p.out_lds_off set).
+size_t decode_logits_stage_offset(const DecodeParams& p, int grid);
+int decode_logits_stage_rows(const DecodeParams& p, size_t lds_limit);
 hipError_t decode_kernel_occupancy(int fmt, int hd, int heads, int kv_heads, size_t lds, int* blocks_per_cu);
 // cooperative = 0 launches the same grid as an ordinary kernel (for profilers
 // that cannot follow cooperative launches); residency is then not guaranteed

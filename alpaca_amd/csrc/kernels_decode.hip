@@ -98,6 +98,24 @@ __device__ inline void item_split(int it, int S, int kv_heads, int& j, int& s) {
 // Group-size bucket: the kernel variant sized for G query heads per KV head.
 __host__ __device__ inline int group_bucket(int g) { return g <= 1 ? 1 : g <= 2 ? 2 : g <= 4 ? 4 : g <= 8 ? 8 : 16; }
 
+// Output rows the logits phase stages in LDS: the rows' quants (or f16 values)
+// exactly as they lie in HBM, padded to whole 1 KB DMA instructions, then, for
+// quantised formats, their f16 scales padded to whole 256-byte instructions.
+// They sit past every other phase's LDS (byte offset out_lds_off), so the copy
+// can be issued layers before the logits phase reads it.
+__host__ __device__ inline int staged_row_bytes(int fmt, int K) {
+    return fmt == DT_Q8_0 ? K : fmt == DT_Q4_0 ? K / 2 : 2 * K;
+}
+__host__ __device__ inline int staged_q_bytes(int fmt, int K, int n) {
+    return (n * staged_row_bytes(fmt, K) + 1023) / 1024 * 1024;
+}
+__host__ __device__ inline int staged_s_bytes(int fmt, int K, int n) {
+    return fmt == DT_F16 ? 0 : (n * (K / 32) * 2 + 255) / 256 * 256;
+}
+// Layers over whose QKV phases the copy is spread (a slice per layer, issued
+// before the phase's wait, where it overlaps the hand-off).
+constexpr int kStageLayers = 8;
+
 }  // namespace
 
 #ifdef DECODE_FMT
@@ -891,8 +909,81 @@ struct PhaseGateUp {
     }
 };
 
+// Slice `part` of `parts` of the copy of rows [r0, r0 + n) of W (quants, then
+// scales) into LDS at sq / ss, by DMA (global_load_lds: no registers).  A row
+// share is one contiguous byte range of each stream, so instruction i of the
+// copy moves bytes [1024 i, 1024 i + 1024) of the quants (256-byte pieces of
+// the scales); lanes past the end re-read the range's last bytes (in bounds)
+// into the padding.  A slice is a contiguous run of instructions, dealt to the
+// waves in turn; they stay this wave's outstanding loads until its next wait.
+template <int FMT>
+__device__ __forceinline__ void stage_rows(const DevMatrix& W, int r0, int n, uint8_t* sq, uint8_t* ss, int part,
+                                           int parts) {
+    const int K = W.cols, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: the LDS address goes to m0
+    const int qbytes = n * staged_row_bytes(FMT, K), nq = (qbytes + 1023) / 1024;
+    const uint8_t* qsrc = W.q + (int64_t)r0 * staged_row_bytes(FMT, K);
+    const uint32_t lq = __builtin_amdgcn_readfirstlane(lds_addr(sq));
+    for (int i = nq * part / parts + wave; i < nq * (part + 1) / parts; i += kWaves) {
+        const int off = min(i * 1024 + 16 * lane, qbytes - 16);
+        dma16(qsrc + off, lq + i * 1024);
+    }
+    if constexpr (FMT != DT_F16) {
+        const int sbytes = n * (K / 32) * 2, ns = (sbytes + 255) / 256;
+        const uint8_t* ssrc = (const uint8_t*)W.s + (int64_t)r0 * (K / 32) * 2;
+        const uint32_t ls = __builtin_amdgcn_readfirstlane(lds_addr(ss));
+        for (int i = ns * part / parts + wave; i < ns * (part + 1) / parts; i += kWaves) {
+            const int off = min(i * 256 + 4 * lane, sbytes - 4);
+            dma4(ssrc + off, ls + i * 256);
+        }
+    }
+}
+// The staged region of this workgroup's output rows and its row range.
+struct Staged {
+    uint8_t *sq, *ss;
+    int r0, n;
+};
+__device__ __forceinline__ Staged staged_of(const DecodeParams& p) {
+    Staged g;
+    g.sq = (uint8_t*)dyn_lds + p.out_lds_off;
+    g.ss = g.sq + staged_q_bytes(p.out.dtype, p.out.cols, p.out_lds_rows);
+    g.r0 = min(p.out.rows, (int)blockIdx.x * p.rows_out);
+    g.n = max(0, min(p.out.rows, g.r0 + p.out_lds_rows) - g.r0);
+    return g;
+}
+
+// Rows [0, n) staged by stage_rows against xs (LDS), with the lanes-per-row
+// mapping, chunk order and lane reduction of Rows::run (so each row's sum is
+// the one the register path forms, bit for bit); epi(rbase + row, sum) runs on
+// the row's first lane, rows ascending within a lane.
+template <int FMT, int LPR, typename Epi>
+__device__ __forceinline__ void run_staged(const uint8_t* sq, const uint8_t* ss, int K, int rbase, int n,
+                                           const float* xs, Epi& epi) {
+    constexpr int RPB = kWaves * (64 / LPR);
+    const int lane = threadIdx.x & 63, li = lane % LPR;
+    const int local = (threadIdx.x >> 6) * (64 / LPR) + lane / LPR;
+    const int nch = gemv::chunks_of<FMT>(K), rb = staged_row_bytes(FMT, K), nb = K >> 5;
+    const f16* sc = (const f16*)ss;
+    for (int base = 0; base < n; base += RPB) {
+        const int r = base + local;
+        float v = 0.f;
+        if (r < n) {
+            for (int c = li; c < nch; c += LPR) {
+                const int4 q = *(const int4*)(sq + r * rb + 16 * c);
+                const float d = FMT == DT_Q8_0 ? (float)sc[r * nb + (c >> 1)] : FMT == DT_Q4_0 ? (float)sc[r * nb + c] : 1.f;
+                v += gemv::chunk_dot<FMT>(q, d, c, xs);
+            }
+        }
+        v = lane_sum<LPR>(v);
+        if (r < n && li == 0) epi(rbase + r, v, 0.f);
+    }
+}
+
 // P7: final RMSNorm, output rows (logits) and this workgroup's arg-max, which
-// it publishes as two words (value, index bits).
+// it publishes as two words (value, index bits).  The first out_lds_rows rows of
+// the workgroup's share were staged in LDS by DMA during the last layers (a
+// slice before each of their QKV waits); the rest stream through registers as
+// in the other phases.
 template <int FMT>
 struct PhaseLogits {
     const u64* in;  // last layer's xf words
@@ -905,8 +996,10 @@ struct PhaseLogits {
         const DevMatrix W = p.out;
         int r0, r1;
         my_rows(p.rows_out, W.rows, r0, r1);
+        const Staged g = staged_of(p);
+        const int rs = r0 + g.n;  // rows [r0, rs) staged in LDS
         Rows<FMT, LPR, false> rw;
-        rw.prefetch(W, W, r0, r1);
+        rw.prefetch(W, W, rs, r1);
         NormGain gain;
         gain.load(p.out_norm, p.hidden);
         if (!wait_words(in, p.hidden, sh.xres, c)) return false;
@@ -914,13 +1007,18 @@ struct PhaseLogits {
         float best = -INFINITY;
         int bi = INT_MAX;
         float* logits = p.logits;
-        rw.run(W, W, r0, r1, sh.xn, [&](int r, float v, float) {
+        auto epi = [&](int r, float v, float) {
             if (logits) *gptr(logits + r) = v;
             if (v > best) {  // rows ascend within a lane, so ties keep the lower index; NaN never wins
                 best = v;
                 bi = r;
             }
-        });
+        };
+        if (rs > r0) {
+            wait_stage_barrier<0>();  // every wave's DMA has landed
+            run_staged<FMT, LPR>(g.sq, g.ss, W.cols, r0, g.n, sh.xn, epi);
+        }
+        rw.run(W, W, rs, r1, sh.xn, epi);
         wave_argmax(best, bi);
         __syncthreads();
         if ((threadIdx.x & 63) == 0) {
@@ -1011,6 +1109,20 @@ __global__ __launch_bounds__(kT) void decode_step_kernel(DecodeParams kp) {
             return;
         }
         copy_to_lds(lds_layer, kp.layers + l, (int)sizeof(DecLayer));
+        if (kp.out_lds_rows > 0) {
+            // slice of the staged output rows (the logits phase reads them after a wait)
+            const int parts = min(kStageLayers, n_layers), part = l - (n_layers - parts);
+            if (part >= 0) {
+                const Staged g = staged_of(P());
+                if (g.n > 0) {
+                    switch (kp.out.dtype) {
+                    case DT_Q8_0: stage_rows<DT_Q8_0>(kp.out, g.r0, g.n, g.sq, g.ss, part, parts); break;
+                    case DT_Q4_0: stage_rows<DT_Q4_0>(kp.out, g.r0, g.n, g.sq, g.ss, part, parts); break;
+                    default: stage_rows<DT_F16>(kp.out, g.r0, g.n, g.sq, g.ss, part, parts); break;
+                    }
+                }
+            }
+        }
         u64* X = kp.xbuf + (int64_t)l * layer_words;
         if (!qkv_phase<FMT>(xprev, X, pos, token, c)) return;
         stamp();
@@ -1139,7 +1251,36 @@ size_t decode_lds_bytes(const DecodeParams& p, int grid) {
     need((size_t)p.max_splits * (HD + 2) + p.max_splits);                         // merge
     need(16);                                                                     // logits arg-max
     need((size_t)2 * grid);                                                       // candidates
-    return ((size_t)kRedFloats + p.hidden + p.stage + scr) * sizeof(float);
+    const size_t phases = ((size_t)kRedFloats + p.hidden + p.stage + scr) * sizeof(float);
+    if (p.out_lds_rows <= 0) return phases;
+    return (size_t)p.out_lds_off + staged_q_bytes(p.out.dtype, p.out.cols, p.out_lds_rows) +
+           staged_s_bytes(p.out.dtype, p.out.cols, p.out_lds_rows);
+}
+
+size_t decode_logits_stage_offset(const DecodeParams& p, int grid) {
+    DecodeParams q = p;
+    q.out_lds_rows = 0;
+    return (decode_lds_bytes(q, grid) + 15) & ~size_t(15);
+}
+
+int decode_logits_stage_rows(const DecodeParams& p, size_t lds_limit) {
+    const int fmt = p.out.dtype, K = p.out.cols;
+    const size_t base = (size_t)p.out_lds_off;
+    int n = 0;
+    while (n < p.rows_out &&
+           base + staged_q_bytes(fmt, K, n + 1) + staged_s_bytes(fmt, K, n + 1) <= lds_limit)
+        n++;
+    return n;
+}
+
+size_t decode_static_lds(int fmt, int hd, int heads, int kv_heads) {
+    const void* f = kernel_for(fmt, hd, heads, kv_heads);
+    hipFuncAttributes a;
+    if (!f || hipFuncGetAttributes(&a, f) != hipSuccess) {
+        hipGetLastError();
+        return 0;
+    }
+    return a.sharedSizeBytes;
 }
 
 hipError_t decode_kernel_occupancy(int fmt, int hd, int heads, int kv_heads, size_t lds, int* blocks_per_cu) {

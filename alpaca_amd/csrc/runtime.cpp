@@ -854,7 +854,23 @@ static int setup_persistent_decode(ahip_session* s) {
     p.rows_ffn = even_share(F);
     p.rows_down = even_share(H);
     p.rows_out = even_share(V);
+    // The logits phase stages the leading rows of each workgroup's output share
+    // in whatever LDS the device leaves beyond the kernel's static arrays
+    // (ALPACA_HIP_DECODE_LOGIT_STAGE_ROWS caps the count; 0 streams every row
+    // through registers).
+    {
+        const size_t stat = decode_static_lds(fmt, hd, c.head_count, c.kv_head_count);
+        const size_t limit = (size_t)max_lds > stat ? (size_t)max_lds - stat : 0;
+        p.out_lds_off = (int)decode_logits_stage_offset(p, grid);
+        p.out_lds_rows = std::max(0, std::min(env_int("ALPACA_HIP_DECODE_LOGIT_STAGE_ROWS", 1 << 30),
+                                              decode_logits_stage_rows(p, limit)));
+    }
     lds = decode_lds_bytes(p, grid);
+    if (decode_kernel_occupancy(fmt, hd, c.head_count, c.kv_head_count, lds, &per_cu) != hipSuccess ||
+        per_cu * cus < grid) {
+        hipGetLastError();
+        return AHIP_OK;
+    }
 
     std::vector<DecLayer> table(c.layer_count);
     for (int l = 0; l < c.layer_count; l++) {

@@ -238,3 +238,46 @@ def test_persistent_decode_multi_item_attention(hip_ctx, spec):
                 assert s.length == p
             s.close()
     print(f"[metrics] {spec.name} multi-item attention: worst persistent vs multi-kernel peak-rel {worst:.2e}")
+
+
+# Output rows per workgroup: a tiny layer shape with a 12,000-entry vocabulary
+# (48 rows per workgroup at 256 workgroups), and C1's 49,152-entry vocabulary
+# over two C1 layers (192 rows per workgroup, more than LDS can stage).
+BIG_VOCAB = [shaped("tiny-v12k", vocab_size=12000),
+             synth.with_dtype(shaped("tiny-v12k-q4", vocab_size=12000), Q4_0),
+             synth.with_dtype(shaped("tiny-v12k-f16", vocab_size=12000), F16),
+             replace(synth.C1, config=replace(synth.C1.config, layer_count=2, context_length=512), name="c1-2l")]
+
+
+@pytest.mark.parametrize("spec", BIG_VOCAB, ids=lambda s: s.name)
+def test_persistent_decode_staged_logit_rows(hip_ctx, spec):
+    """The logits phase stages the leading rows of each workgroup's output
+    share in LDS by DMA (ALPACA_HIP_DECODE_LOGIT_STAGE_ROWS, read at session
+    creation, caps how many) and streams the rest through registers.  Both
+    paths form a row's sum with the same lane mapping, chunk order and lane
+    reduction, so the logits and greedy ids must be bit-identical whatever the
+    split: none staged, one, an odd count, and the default (as many as fit)."""
+    c = spec.config
+    model = HIPLlamaModel(hip_ctx, c, built(spec))
+    prompt = synth.prompt_tokens(spec, 29)
+    runs = {}
+    for cap in ("0", "1", "7", None):
+        with env(ALPACA_HIP_DECODE_LOGIT_STAGE_ROWS=cap):
+            s = model.make_session(capacity=96)
+        tok = int(np.argmax(s.forward(prompt)))
+        out = []
+        for _ in range(3):
+            g = s.decode(tok)
+            out.append(g)
+            tok = int(np.argmax(g))
+        chain = []
+        s.decode_greedy(tok, 6, lambda t: chain.append(t) or True)
+        runs[cap] = (out, chain)
+        s.close()
+    ref_out, ref_chain = runs["0"]
+    for cap, (out, chain) in runs.items():
+        for step, (a, b) in enumerate(zip(out, ref_out)):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), \
+                f"{spec.name} stage rows {cap}: step {step} logits differ (max |d| {np.abs(a - b).max():.3e})"
+        assert chain == ref_chain, f"{spec.name} stage rows {cap}: greedy {chain} != {ref_chain}"
+    model.close()
