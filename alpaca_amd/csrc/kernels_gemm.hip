@@ -1108,6 +1108,14 @@ bool dma_offsets_fit(int m, int ldx, const DevMatrix& w) {
 }
 }  // namespace
 
+// Whether an M x N two-term prefill GEMM runs the wide tiles (128x256, one
+// workgroup per CU: grids of whole rounds, as pick_dgemm decides).
+bool gemm_takes_wide_tiles(int m, int n) {
+    const int cus = device_cus();
+    const int t = ((m + 127) / 128) * ((n + 255) / 256);
+    return t >= cus && (t % cus == 0 || t >= 3 * cus);
+}
+
 hipError_t launch_gemm_mfma(const f16* x, const f16* xlo, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up,
                             float* y, f16* yh, f16* yhlo, int ldy, int mode, hipStream_t st) {
     if (m <= 0) return hipSuccess;

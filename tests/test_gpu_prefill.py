@@ -84,6 +84,43 @@ def test_fused_qkv_rope_with_large_tiles(hip_ctx):
         assert np.array_equal(t, a), f"tile {tile}: prefill logits differ: max |d| {np.abs(t - a).max():.3e}"
 
 
+# ------------------------------------------------------------------ two-stream prefill
+
+C1_2L = replace(synth.C1, config=replace(synth.C1.config, layer_count=2, context_length=4352), name="c1-shape-2l")
+
+
+@pytest.mark.parametrize("prec", ["fast", "fast-f16"])
+@pytest.mark.parametrize("spec", [C1_2L, C4_LONG, synth.with_dtype(replace(C1_2L, name="c1-shape-2l-f16"), F16)],
+                         ids=lambda s: s.name)
+def test_two_stream_prefill_is_bit_identical(hip_ctx, spec, prec):
+    """A long fast prefill whose GEMMs run narrow tiles runs as two halves on two
+    streams (the second half's attention of each layer waits for the first
+    half's K/V rows).  Every row goes through the same kernels as in one
+    stream, so the logits and the decode steps that read the cache must be
+    bit-identical to ALPACA_HIP_PREFILL_STREAMS=1 (read per call): one
+    3100-token chunk (uneven halves), then a 4300-token prompt over chunks of
+    3200 (a split chunk, then a short one at position 3200)."""
+    model = HIPLlamaModel(hip_ctx, spec.config, built(spec))
+    prompt = synth.prompt_tokens(spec, 4300)
+    for n in (3100, 4300):
+        out = {}
+        for streams in ("1", "2"):
+            s = model.make_session(capacity=4352, max_batch=3200, gemm_precision=prec)
+            with env(ALPACA_HIP_PREFILL_STREAMS=streams):
+                g = s.forward(prompt[:n])
+            tok = int(np.argmax(g))
+            steps = [g]
+            for _ in range(2):
+                steps.append(s.decode(tok))
+                tok = int(np.argmax(steps[-1]))
+            out[streams] = steps
+            s.close()
+        for k, (a, b) in enumerate(zip(out["1"], out["2"])):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), \
+                f"{spec.name} {prec} n={n} step {k}: two streams differ (max |d| {np.abs(a - b).max():.3e})"
+    model.close()
+
+
 # ------------------------------------------------------------------ prefill weight cache
 
 LAYER_MATS = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
