@@ -648,11 +648,14 @@ struct ahip_session {
     bool logits_ready = false;  // `logits` holds the last forward's logits (for ahip_session_sample)
     DevBuf sample_idx, sample_p, sample_out;  // sampler scratch, allocated on first use
     hipStream_t stream = nullptr;
-    // Second stream of a split prefill (two halves of a long chunk on two
-    // streams) and its events: [0] S1 -> S2 start, [1] a layer's QKV of the
-    // first half, [2] S2 -> S1 end.  Created on first use.
-    hipStream_t stream2 = nullptr;
-    hipEvent_t split_ev[3] = {nullptr, nullptr, nullptr};
+    // Extra streams of a split prefill (parts of a long chunk on their own
+    // streams; part 0 runs on `stream`) and their events: start[k] orders part
+    // k after the session stream's earlier work, qkv[k] marks part k's K/V rows
+    // of the current layer in the cache, done[k] joins part k back.  Created on
+    // first use.
+    static constexpr int kMaxParts = 2;  // three and four parts measured slower (C1 4096: 466k / 494k tok/s)
+    hipStream_t part_stream[kMaxParts] = {};
+    hipEvent_t part_start = nullptr, part_qkv[kMaxParts] = {}, part_done[kMaxParts] = {};
     std::vector<std::unique_ptr<DevBuf>> kc, vc;
     DevBuf x, xn, xh, qkv, qh, ctx, ctxh, ffn, ffnh, partials, logits, tokens, chain, dpos;
     float* logits_host = nullptr;
@@ -698,10 +701,14 @@ struct ahip_session {
         if (tokens_host) hipHostFree(tokens_host);
         if (pdec_status) hipHostFree(pdec_status);
         if (pdec_peer) hipEventDestroy(pdec_peer);
-        if (stream2) hipStreamSynchronize(stream2);
-        for (auto e : split_ev)
-            if (e) hipEventDestroy(e);
-        if (stream2) hipStreamDestroy(stream2);
+        for (int k = 1; k < kMaxParts; k++)
+            if (part_stream[k]) hipStreamSynchronize(part_stream[k]);
+        if (part_start) hipEventDestroy(part_start);
+        for (int k = 0; k < kMaxParts; k++) {
+            if (part_qkv[k]) hipEventDestroy(part_qkv[k]);
+            if (part_done[k]) hipEventDestroy(part_done[k]);
+            if (k && part_stream[k]) hipStreamDestroy(part_stream[k]);
+        }
         if (stream) hipStreamDestroy(stream);
     }
 
@@ -1190,10 +1197,10 @@ static int encode_decode_layer(ahip_session* s, int li, int pos, const int* pos_
 // MetalLlamaModel.swift:307-384).  Tokens are read from device memory.
 // One layer of the fast (MFMA) prefill for the n tokens at activation rows
 // [row0, row0 + n) and positions [pos, pos + n), on stream st.  after_qkv (if
-// set) is recorded once this half's K/V rows are in the cache; before_attn (if
-// set) is waited for before the attention reads the cache.
+// set) is recorded once these rows' K/V are in the cache; the attention first
+// waits for the n_before events of before_attn (earlier rows' K/V).
 static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, bool flash, hipStream_t st,
-                             hipEvent_t after_qkv, hipEvent_t before_attn) {
+                             hipEvent_t after_qkv, const hipEvent_t* before_attn = nullptr, int n_before = 0) {
     ahip_model* m = s->m;
     const ahip_llama_config& c = m->c;
     const int H = c.hidden_size, QW = c.head_count * c.head_dim, KW = c.kv_head_count * c.head_dim,
@@ -1243,7 +1250,7 @@ static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, 
                                  flash ? qh : nullptr, flash ? qhlo : nullptr, kc, vc, s->kv_f16, s->capacity, st));
     }
     if (after_qkv) HIP_OR(hipEventRecord(after_qkv, st), "hipEventRecord");
-    if (before_attn) HIP_OR(hipStreamWaitEvent(st, before_attn, 0), "hipStreamWaitEvent");
+    for (int k = 0; k < n_before; k++) HIP_OR(hipStreamWaitEvent(st, before_attn[k], 0), "hipStreamWaitEvent");
     s->stage("attention");
     if (flash) {
         LAUNCH(launch_flash_attention(qh, qhlo, QW, (const f16*)kc, (const f16*)vc, s->capacity, n, c.head_count,
@@ -1276,35 +1283,51 @@ static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, 
 // 775k -> 821k tok/s (at C4's 2048 tokens it measured -2% to +1%, so shorter
 // prefills keep one stream).  Where the wide tiles fill the device in
 // whole rounds (the 1.7B shape) halving the rows costs more than the overlap
-// gains (132k -> 122k), so those prefills keep one stream.  Each row's results
-// are the same either way (bit for bit in every measured config).
+// gains (132k -> 122k), so those prefills keep one stream.  Each row goes
+// through the same kernels; only the flash kernel may pick its other key-range
+// split for the smaller grid of a half (a different float32 summation order:
+// C4 at 4096 tokens, logits within 3.5e-5).  C4 at 4096 tokens: 406k -> 441k.
 // ALPACA_HIP_PREFILL_STREAMS=1 (read per call) keeps one stream.
 constexpr int kSplitPrefillMin = 3072;
 
-static int encode_split_prefill(ahip_session* s, const int32_t* dtok, int n, int pos, bool logits, bool flash) {
+static int encode_split_prefill(ahip_session* s, const int32_t* dtok, int n, int pos, bool logits, bool flash,
+                                int parts) {
     ahip_model* m = s->m;
     const ahip_llama_config& c = m->c;
     const int H = c.hidden_size;
-    if (!s->stream2) {
-        HIP_OR(hipStreamCreateWithFlags(&s->stream2, hipStreamNonBlocking), "hipStreamCreate");
-        for (auto& e : s->split_ev) HIP_OR(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
+    parts = std::max(2, std::min(parts, ahip_session::kMaxParts));
+    if (!s->part_start) HIP_OR(hipEventCreateWithFlags(&s->part_start, hipEventDisableTiming), "hipEventCreate");
+    s->part_stream[0] = s->stream;
+    for (int k = 0; k < parts; k++) {
+        if (!s->part_stream[k])
+            HIP_OR(hipStreamCreateWithFlags(&s->part_stream[k], hipStreamNonBlocking), "hipStreamCreate");
+        if (!s->part_qkv[k]) HIP_OR(hipEventCreateWithFlags(&s->part_qkv[k], hipEventDisableTiming), "hipEventCreate");
+        if (!s->part_done[k]) HIP_OR(hipEventCreateWithFlags(&s->part_done[k], hipEventDisableTiming), "hipEventCreate");
     }
-    hipStream_t s1 = s->stream, s2 = s->stream2;
-    const int na = (n / 2 + 63) / 64 * 64, nb = n - na;  // query blocks of 64 stay whole in the first half
-    HIP_OR(hipEventRecord(s->split_ev[0], s1), "hipEventRecord");
-    HIP_OR(hipStreamWaitEvent(s2, s->split_ev[0], 0), "hipStreamWaitEvent");
+    // part k: rows [r[k], r[k+1]); every boundary but the last a multiple of 64
+    int r[ahip_session::kMaxParts + 1];
+    for (int k = 0; k < parts; k++) r[k] = (int)((int64_t)n * k / parts / 64 * 64);
+    r[parts] = n;
+    HIP_OR(hipEventRecord(s->part_start, s->stream), "hipEventRecord");
     float* x = s->x.as<float>();
-    LAUNCH(launch_embed(dtok, na, m->embed.m, x, s1));
-    LAUNCH(launch_embed(dtok + na, nb, m->embed.m, x + (int64_t)na * H, s2));
-    for (int li = 0; li < c.layer_count; li++) {
-        if (int rc = encode_mfma_layer(s, li, 0, na, pos, flash, s1, s->split_ev[1], nullptr)) return rc;
-        if (int rc = encode_mfma_layer(s, li, na, nb, pos + na, flash, s2, nullptr, s->split_ev[1])) return rc;
+    for (int k = 0; k < parts; k++) {
+        hipStream_t st = s->part_stream[k];
+        if (k) HIP_OR(hipStreamWaitEvent(st, s->part_start, 0), "hipStreamWaitEvent");
+        LAUNCH(launch_embed(dtok + r[k], r[k + 1] - r[k], m->embed.m, x + (int64_t)r[k] * H, st));
     }
+    for (int li = 0; li < c.layer_count; li++)
+        for (int k = 0; k < parts; k++)
+            if (int rc = encode_mfma_layer(s, li, r[k], r[k + 1] - r[k], pos + r[k], flash, s->part_stream[k],
+                                           k + 1 < parts ? s->part_qkv[k] : nullptr, s->part_qkv, k))
+                return rc;
+    hipStream_t last = s->part_stream[parts - 1];
     if (logits)
         LAUNCH(launch_gemv(m->out_matrix(), nullptr, x + (int64_t)(n - 1) * H, m->output_norm.as<float>(),
-                           c.rms_norm_eps, s->logits.as<float>(), GEMV_STORE, s2));
-    HIP_OR(hipEventRecord(s->split_ev[2], s2), "hipEventRecord");
-    HIP_OR(hipStreamWaitEvent(s1, s->split_ev[2], 0), "hipStreamWaitEvent");
+                           c.rms_norm_eps, s->logits.as<float>(), GEMV_STORE, last));
+    for (int k = 1; k < parts; k++) {
+        HIP_OR(hipEventRecord(s->part_done[k], s->part_stream[k]), "hipEventRecord");
+        HIP_OR(hipStreamWaitEvent(s->stream, s->part_done[k], 0), "hipStreamWaitEvent");
+    }
     return AHIP_OK;
 }
 
@@ -1322,7 +1345,7 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
     const bool flash = s->fast && n >= 16 && !s->prefill_generic_attention && s->kv_f16 && (hd == 64 || hd == 128);
     if (mfma && n >= kSplitPrefillMin && !s->profiling && env_int("ALPACA_HIP_PREFILL_STREAMS", 2) >= 2 &&
         !gemm_takes_wide_tiles(n, QW + 2 * KW))
-        return encode_split_prefill(s, dtok, n, pos, logits, flash);
+        return encode_split_prefill(s, dtok, n, pos, logits, flash, env_int("ALPACA_HIP_PREFILL_STREAMS", 2));
     s->stage("embed");
     LAUNCH(launch_embed(dtok, n, m->embed.m, x, st));
     // Second-term planes of the f16 activation buffers (two-term prefill), after the first planes.

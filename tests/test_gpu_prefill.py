@@ -92,12 +92,14 @@ C1_2L = replace(synth.C1, config=replace(synth.C1.config, layer_count=2, context
 @pytest.mark.parametrize("prec", ["fast", "fast-f16"])
 @pytest.mark.parametrize("spec", [C1_2L, C4_LONG, synth.with_dtype(replace(C1_2L, name="c1-shape-2l-f16"), F16)],
                          ids=lambda s: s.name)
-def test_two_stream_prefill_is_bit_identical(hip_ctx, spec, prec):
+def test_two_stream_prefill_matches_one_stream(hip_ctx, spec, prec):
     """A long fast prefill whose GEMMs run narrow tiles runs as two halves on two
     streams (the second half's attention of each layer waits for the first
     half's K/V rows).  Every row goes through the same kernels as in one
-    stream, so the logits and the decode steps that read the cache must be
-    bit-identical to ALPACA_HIP_PREFILL_STREAMS=1 (read per call): one
+    stream (the flash kernel may choose its other key-range split for a
+    half's smaller grid, a different float32 summation order), so the logits
+    and the decode steps that read the cache must agree with
+    ALPACA_HIP_PREFILL_STREAMS=1 (read per call) to 1e-5 of the logit peak: one
     3100-token chunk (uneven halves), then a 4300-token prompt over chunks of
     3200 (a split chunk, then a short one at position 3200)."""
     model = HIPLlamaModel(hip_ctx, spec.config, built(spec))
@@ -116,8 +118,10 @@ def test_two_stream_prefill_is_bit_identical(hip_ctx, spec, prec):
             out[streams] = steps
             s.close()
         for k, (a, b) in enumerate(zip(out["1"], out["2"])):
-            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), \
-                f"{spec.name} {prec} n={n} step {k}: two streams differ (max |d| {np.abs(a - b).max():.3e})"
+            d = float(np.abs(a - b).max())
+            print(f"[metrics] {spec.name} {prec} n={n} step {k}: two streams vs one max |d| {d:.2e}")
+            assert d <= 1e-5 * float(np.abs(a).max()), f"{spec.name} {prec} n={n} step {k}: max |d| {d:.3e}"
+            assert int(np.argmax(a)) == int(np.argmax(b))
     model.close()
 
 
