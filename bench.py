@@ -21,7 +21,11 @@ embeddings), random-init synthetic weights, all resident in HBM.
   * prefill_tok_s: 4096-token prompt / median wall time of forward.
   * roofline_prefill: the dominant prefill GEMM (MFMA, f16 operands, f32
     accumulate): algorithmic FLOPs per launch / mean launch time from the
-    session's per-stage HIP events; peak 2.5 PFLOP/s dense fp16.
+    session's per-stage HIP events; peak 2.5 PFLOP/s dense fp16.  issued_frac
+    doubles it: the default prefill enters activations as two f16 terms, so
+    the MFMA units execute twice the algorithmic multiply-adds.
+  * prefill_mfma_frac: the whole 4096-token prefill (projections + causal
+    attention, algorithmic FLOPs) over its wall time, against the same peak.
   * prefill_weight_cache: the same prefill on a model created with the
     prefill weight cache (MetalLlamaModel.buildPrefillCache, f16 copies of the
     layer projections, as `--prefill-cache` in the reference CLI): tok/s and
@@ -43,6 +47,10 @@ embeddings), random-init synthetic weights, all resident in HBM.
     summary (profiles/c1_decode_hbm_counters.md), used only when the summary
     was measured on the decode kernel's current sources (it records a hash of
     them; see --counter-summary), else null with the reason.
+
+--decode-only and --prefill-only (with --config C1/C4/C5) run only the timed
+decode steps or only --prefill-runs 4096-token prefills, for rocprofv3 counter
+passes and kernel traces.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -301,6 +309,9 @@ def main() -> int:
                     help="model config of a --decode-only run (default C1, the headline)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the timed decode steps (for counter passes of the decode kernel)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only --prefill-runs unprofiled 4096-token prefills of --config (for counter passes and "
+                         "traces of the prefill kernels)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only a device-to-device copy of 256 MiB, the reference the HBM byte counters are scaled by")
     ap.add_argument("--counter-summary", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
@@ -337,8 +348,8 @@ def main() -> int:
     spec = {"C1": synth.C1, "C4": synth.C4, "C5": synth.C5}[args.config]
     decode_ctx = {"C1": DECODE_CTX, "C4": 2048, "C5": 4096}[args.config]
     block = 18 if args.config == "C4" else 34
-    if args.config != "C1" and not args.decode_only:
-        log("--config other than C1 is for --decode-only runs")
+    if args.config != "C1" and not (args.decode_only or args.prefill_only):
+        log("--config other than C1 is for --decode-only and --prefill-only runs")
         return 2
     c = spec.config
     t0 = time.perf_counter()
@@ -348,6 +359,20 @@ def main() -> int:
     model = HIPLlamaModel(ctx, c, weights)
     log(f"model resident: {model.weight_bytes / 1e6:.1f} MB")
     prompt = synth.prompt_tokens(spec, PREFILL_TOKENS)
+    if args.prefill_only:
+        p = model.make_session(capacity=PREFILL_TOKENS, max_batch=PREFILL_TOKENS)
+        walls = []
+        for _ in range(max(1, args.prefill_runs)):
+            t0 = time.perf_counter()
+            p.forward(prompt)
+            walls.append(time.perf_counter() - t0)
+            p.reset()
+        print(json.dumps({"config": args.config, "prefill_tokens": PREFILL_TOKENS,
+                          "prefill_tok_s": round(PREFILL_TOKENS / float(np.median(walls)), 1)}), flush=True)
+        p.close()
+        model.close()
+        ctx.close()
+        return 0
 
     # ---------------------------------------------------------------- decode
     cap = decode_ctx + args.steps + 16
@@ -428,6 +453,12 @@ def main() -> int:
         gemm_s = sum(profp[k].seconds for k in profp if k in fl and k != "attention")
         gemm_f = sum(fl[k] * profp[k].dispatches for k in profp if k in fl and k != "attention")
         roof_p["all_prefill_gemms_frac"] = round(gemm_f / gemm_s / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
+        # The default prefill enters the activations as two f16 terms (hi + lo), so each
+        # algorithmic multiply-add is issued twice on the MFMA units (QK^T and PV likewise).
+        roof_p["issued_frac"] = round(2 * roof_p["frac"], 4)
+        roof_p["all_prefill_gemms_issued_frac"] = round(2 * roof_p["all_prefill_gemms_frac"], 4)
+        roof_p["note"] = ("frac counts 2*M*N*K algorithmic FLOPs per GEMM; issued_frac counts the MFMA work the "
+                          "two-term activations actually issue (twice that), both against 2.5 PFLOP/s dense f16")
         log(f"prefill dominant GEMM: {domp} {ach:.1f} TFLOP/s")
 
     # ---------------------------------------------------------------- prefill with the weight cache
@@ -486,9 +517,13 @@ def main() -> int:
                                "4096-token prefill (prefill_tok_s)",
                    "layers": c.layer_count, "hidden": c.hidden_size, "heads": f"{c.head_count}/{c.kv_head_count}",
                    "head_dim": c.head_dim, "ffn": c.feed_forward_size, "vocab": c.vocab_size,
-                   "kv_cache": "f16", "prefill_precision": "fast (f16 MFMA, f32 accumulate)",
+                   "kv_cache": "f16",
+                   "prefill_precision": "fast: f16 MFMA, activations as two f16 terms (hi + lo), exact integer "
+                                        "quants, per-block f32 scaling, f32 accumulate",
                    "greedy_depth": args.depth},
         "prefill_tok_s": round(prefill_tok_s, 1),
+        "prefill_mfma_frac": round(c.layer_count * sum(prefill_stage_flops(c, PREFILL_TOKENS).values()) *
+                                   prefill_tok_s / PREFILL_TOKENS / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
         "prefill_weight_cache": wcache,
         "other_configs": others,
         "decode_ms_per_token": round(el / args.steps * 1e3, 4),
