@@ -649,10 +649,11 @@ struct ahip_session {
     DevBuf sample_idx, sample_p, sample_out;  // sampler scratch, allocated on first use
     hipStream_t stream = nullptr;
     // Extra streams of a split prefill (parts of a long chunk on their own
-    // streams; part 0 runs on `stream`) and their events: start[k] orders part
-    // k after the session stream's earlier work, qkv[k] marks part k's K/V rows
-    // of the current layer in the cache, done[k] joins part k back.  Created on
-    // first use.
+    // streams; part 0 runs on `stream`) and their events: part_start orders the
+    // parts after the session stream's earlier work, part_qkv[k] marks part k's
+    // K/V rows of the current layer in the cache, part_done[k] joins part k
+    // back.  Created with the session stream (fast sessions whose max_batch
+    // allows a split).
     static constexpr int kMaxParts = 2;  // three and four parts measured slower (C1 4096: 466k / 494k tok/s)
     hipStream_t part_stream[kMaxParts] = {};
     hipEvent_t part_start = nullptr, part_qkv[kMaxParts] = {}, part_done[kMaxParts] = {};
@@ -763,6 +764,10 @@ struct ahip_session {
     }
 };
 
+
+// Shortest prefill chunk that may run as two halves on two streams
+// (encode_split_prefill).
+constexpr int kSplitPrefillMin = 3072;
 
 // Persistent decode launches of all sessions on one device run one at a time.
 // Each launch needs every one of its workgroups resident at once (one per CU,
@@ -1066,6 +1071,25 @@ extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, i
         s->prefill_f32_gemm = g && !std::strcmp(g, "f32");
     }
     HIP_OR(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate");
+    // The second stream of a split prefill must not share a hardware queue
+    // with the session stream (the halves would then run one after the other,
+    // with an inter-stream barrier per layer: measured 30% slower than one
+    // stream).  The runtime deals its few hardware queues (GPU_MAX_HW_QUEUES)
+    // out to ordinary streams as it sees fit, while a stream created with a
+    // CU mask gets a queue of its own; the mask enables every CU.
+    if (s->fast && max_batch >= kSplitPrefillMin) {
+        int cus = 0;
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->device);
+        std::vector<uint32_t> all((size_t)std::max(1, (cus + 31) / 32), 0xFFFFFFFFu);
+        for (int k = 1; k < ahip_session::kMaxParts; k++)
+            HIP_OR(hipExtStreamCreateWithCUMask(&s->part_stream[k], (uint32_t)all.size(), all.data()),
+                   "hipExtStreamCreateWithCUMask");
+        HIP_OR(hipEventCreateWithFlags(&s->part_start, hipEventDisableTiming), "hipEventCreate");
+        for (int k = 0; k < ahip_session::kMaxParts; k++) {
+            HIP_OR(hipEventCreateWithFlags(&s->part_qkv[k], hipEventDisableTiming), "hipEventCreate");
+            HIP_OR(hipEventCreateWithFlags(&s->part_done[k], hipEventDisableTiming), "hipEventCreate");
+        }
+    }
     const SessionSizes z = session_sizes(c, capacity, max_batch, s->kv_f16);
     for (int l = 0; l < c.layer_count; l++) {
         s->kc.emplace_back(new DevBuf());
@@ -1288,7 +1312,6 @@ static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, 
 // split for the smaller grid of a half (a different float32 summation order:
 // C4 at 4096 tokens, logits within 3.5e-5).  C4 at 4096 tokens: 406k -> 441k.
 // ALPACA_HIP_PREFILL_STREAMS=1 (read per call) keeps one stream.
-constexpr int kSplitPrefillMin = 3072;
 
 static int encode_split_prefill(ahip_session* s, const int32_t* dtok, int n, int pos, bool logits, bool flash,
                                 int parts) {
@@ -1296,14 +1319,7 @@ static int encode_split_prefill(ahip_session* s, const int32_t* dtok, int n, int
     const ahip_llama_config& c = m->c;
     const int H = c.hidden_size;
     parts = std::max(2, std::min(parts, ahip_session::kMaxParts));
-    if (!s->part_start) HIP_OR(hipEventCreateWithFlags(&s->part_start, hipEventDisableTiming), "hipEventCreate");
-    s->part_stream[0] = s->stream;
-    for (int k = 0; k < parts; k++) {
-        if (!s->part_stream[k])
-            HIP_OR(hipStreamCreateWithFlags(&s->part_stream[k], hipStreamNonBlocking), "hipStreamCreate");
-        if (!s->part_qkv[k]) HIP_OR(hipEventCreateWithFlags(&s->part_qkv[k], hipEventDisableTiming), "hipEventCreate");
-        if (!s->part_done[k]) HIP_OR(hipEventCreateWithFlags(&s->part_done[k], hipEventDisableTiming), "hipEventCreate");
-    }
+    s->part_stream[0] = s->stream;  // the other parts' streams and the events exist since session creation
     // part k: rows [r[k], r[k+1]); every boundary but the last a multiple of 64
     int r[ahip_session::kMaxParts + 1];
     for (int k = 0; k < parts; k++) r[k] = (int)((int64_t)n * k / parts / 64 * 64);
@@ -1343,8 +1359,8 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
     const float2* rope = m->rope.as<float2>();
     const bool mfma = s->fast && n >= 16 && !s->prefill_f32_gemm;
     const bool flash = s->fast && n >= 16 && !s->prefill_generic_attention && s->kv_f16 && (hd == 64 || hd == 128);
-    if (mfma && n >= kSplitPrefillMin && !s->profiling && env_int("ALPACA_HIP_PREFILL_STREAMS", 2) >= 2 &&
-        !gemm_takes_wide_tiles(n, QW + 2 * KW))
+    if (mfma && n >= kSplitPrefillMin && s->part_stream[1] && !s->profiling &&
+        env_int("ALPACA_HIP_PREFILL_STREAMS", 2) >= 2 && !gemm_takes_wide_tiles(n, QW + 2 * KW))
         return encode_split_prefill(s, dtok, n, pos, logits, flash, env_int("ALPACA_HIP_PREFILL_STREAMS", 2));
     s->stage("embed");
     LAUNCH(launch_embed(dtok, n, m->embed.m, x, st));

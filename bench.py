@@ -166,32 +166,38 @@ DECODE_SOURCES = ("alpaca_amd/csrc/kernels_decode.hip", "alpaca_amd/csrc/gemv_ch
                   "alpaca_amd/csrc/runtime.cpp")
 
 
-def source_hash(root: str) -> str:
-    """sha256 (first 16 hex digits) of the sources that decide the decode
-    kernel's memory traffic: its kernel file, the shared headers and the host
-    side that sets its launch (items, workgroups, exchange layout)."""
+# The sources that decide the prefill GEMMs' memory traffic: the kernels (tile
+# choice included) and the shared header.
+GEMM_SOURCES = ("alpaca_amd/csrc/kernels_gemm.hip", "alpaca_amd/csrc/common.h")
+
+
+def source_hash(root: str, sources=DECODE_SOURCES) -> str:
+    """sha256 (first 16 hex digits) of the sources that decide a kernel's
+    memory traffic (for the decode kernel: its kernel file, the shared headers
+    and the host side that sets its launch: items, workgroups, exchange
+    layout)."""
     import hashlib
     h = hashlib.sha256()
-    for rel in DECODE_SOURCES:
+    for rel in sources:
         with open(os.path.join(root, rel), "rb") as f:
             h.update(rel.encode() + b"\0" + f.read())
     return h.hexdigest()[:16]
 
 
-def measured_traffic(root: str):
-    """(HBM bytes per decode launch, source note) from the committed rocprofv3
-    counter summary, or (None, reason) when it is missing or was measured on
-    other decode sources than this tree's."""
+def measured_traffic(root: str, rel: str = "profiles/c1_decode_hbm_counters.md", sources=DECODE_SOURCES,
+                     label: str = "Decode"):
+    """(HBM bytes per launch, source note) from a committed rocprofv3 counter
+    summary, or (None, reason) when it is missing or was measured on other
+    sources than this tree's."""
     import re
-    rel = "profiles/c1_decode_hbm_counters.md"
     try:
         with open(os.path.join(root, rel)) as f:
             text = f.read()
     except OSError:
         return None, f"{rel} missing"
     m = re.search(r"Traffic per launch[^:]*:\s*([0-9.]+)\s*MB", text)
-    h = re.search(r"Decode source hash:\s*([0-9a-f]+)", text)
-    cur = source_hash(root)
+    h = re.search(label + r" source hash:\s*([0-9a-f]+)", text)
+    cur = source_hash(root, sources)
     if not m or not h:
         return None, f"{rel} has no traffic figure or source hash"
     if h.group(1) != cur:
@@ -199,7 +205,7 @@ def measured_traffic(root: str):
     return float(m.group(1)) * 1e6, f"{rel} (rocprofv3 FETCH_SIZE and WRITE_SIZE runs, scaled by a copy; sources {cur})"
 
 
-def counter_summary(dirs: dict, kernel: str) -> int:
+def counter_summary(dirs: dict, kernel: str, gemm: bool = False) -> int:
     """Markdown summary of rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of
     `kernel` and of the calibration copy, with the source hash bench.py checks."""
     import glob
@@ -230,7 +236,8 @@ def counter_summary(dirs: dict, kernel: str) -> int:
     for name, v, sc in (("FETCH_SIZE", kf, sf), ("WRITE_SIZE", kw, sw)):
         print(f"| {name} | {len(v)} | {sum(v) / len(v):.1f} | {min(v):.1f} | {max(v):.1f} | "
               f"{sum(v) / len(v) * sc * 1024 / 1e6:.1f} |")
-    print(f"\nTraffic per launch: {traffic:.1f} MB\n\nDecode source hash: {source_hash(root)}")
+    label, src = ("GEMM", GEMM_SOURCES) if gemm else ("Decode", DECODE_SOURCES)
+    print(f"\nTraffic per launch: {traffic:.1f} MB\n\n{label} source hash: {source_hash(root, src)}")
     return 0
 
 
@@ -317,10 +324,13 @@ def main() -> int:
     ap.add_argument("--counter-summary", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
                     help="print the markdown summary of rocprofv3 --pmc output directories (no GPU use)")
     ap.add_argument("--counter-kernel", default="decode_step_kernel")
+    ap.add_argument("--counter-gemm", action="store_true",
+                    help="the summarised kernel is a prefill GEMM: record the GEMM sources' hash")
     args = ap.parse_args()
     if args.counter_summary:
         fd, wd, cfd, cwd = args.counter_summary
-        return counter_summary({"fetch": fd, "write": wd, "copy_fetch": cfd, "copy_write": cwd}, args.counter_kernel)
+        return counter_summary({"fetch": fd, "write": wd, "copy_fetch": cfd, "copy_write": cwd}, args.counter_kernel,
+                               args.counter_gemm)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures the single-GPU hot path only: this build runs on one GPU "
@@ -447,8 +457,14 @@ def main() -> int:
         domp = max((k for k in profp if k in fl and k != "attention"), key=lambda k: profp[k].seconds)
         avgp = profp[domp].seconds / profp[domp].dispatches
         ach = fl[domp] / avgp / 1e12
+        ptraffic, ptraffic_note = (None, "counters are summarised for the gate+up+silu GEMM only")
+        if domp == "ffn gate+up+silu":
+            ptraffic, ptraffic_note = measured_traffic(os.path.dirname(os.path.abspath(__file__)),
+                                                       "profiles/c1_prefill_gemm_hbm_counters.md", GEMM_SOURCES,
+                                                       "GEMM")
         roof_p = {"bound": "mfma", "kernel": domp, "achieved": round(ach, 2), "peak": MFMA_F16_PEAK_TFLOPS,
-                  "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+                  "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFLOPS, 4), "traffic": ptraffic,
+                  "traffic_source": ptraffic_note,
                   "flops_per_launch": int(fl[domp]), "avg_launch_us": round(avgp * 1e6, 3)}
         gemm_s = sum(profp[k].seconds for k in profp if k in fl and k != "attention")
         gemm_f = sum(fl[k] * profp[k].dispatches for k in profp if k in fl and k != "attention")
