@@ -648,12 +648,11 @@ struct ahip_session {
     bool logits_ready = false;  // `logits` holds the last forward's logits (for ahip_session_sample)
     DevBuf sample_idx, sample_p, sample_out;  // sampler scratch, allocated on first use
     hipStream_t stream = nullptr;
-    // Extra streams of a split prefill (parts of a long chunk on their own
-    // streams; part 0 runs on `stream`) and their events: part_start orders the
-    // parts after the session stream's earlier work, part_qkv[k] marks part k's
-    // K/V rows of the current layer in the cache, part_done[k] joins part k
-    // back.  Created with the session stream (fast sessions whose max_batch
-    // allows a split).
+    // Streams of a split prefill (part 0 on `stream`, the other part on the
+    // device's split stream, shared by all sessions) and this session's events:
+    // part_start orders the parts after the session stream's earlier work,
+    // part_qkv[k] marks part k's K/V rows of the current layer in the cache,
+    // part_done[k] joins part k back.  Set up on the first split.
     static constexpr int kMaxParts = 2;  // three and four parts measured slower (C1 4096: 466k / 494k tok/s)
     hipStream_t part_stream[kMaxParts] = {};
     hipEvent_t part_start = nullptr, part_qkv[kMaxParts] = {}, part_done[kMaxParts] = {};
@@ -702,13 +701,12 @@ struct ahip_session {
         if (tokens_host) hipHostFree(tokens_host);
         if (pdec_status) hipHostFree(pdec_status);
         if (pdec_peer) hipEventDestroy(pdec_peer);
-        for (int k = 1; k < kMaxParts; k++)
-            if (part_stream[k]) hipStreamSynchronize(part_stream[k]);
+        // (a split's work on the shared split stream ends in part_done, which the
+        // session stream waits for, so syncing the session stream covers it)
         if (part_start) hipEventDestroy(part_start);
         for (int k = 0; k < kMaxParts; k++) {
             if (part_qkv[k]) hipEventDestroy(part_qkv[k]);
             if (part_done[k]) hipEventDestroy(part_done[k]);
-            if (k && part_stream[k]) hipStreamDestroy(part_stream[k]);
         }
         if (stream) hipStreamDestroy(stream);
     }
@@ -768,6 +766,39 @@ struct ahip_session {
 // Shortest prefill chunk that may run as two halves on two streams
 // (encode_split_prefill).
 constexpr int kSplitPrefillMin = 3072;
+
+// The second-half stream of split prefills, one per device, shared by every
+// session and kept for the life of the process.  It must not share a hardware
+// queue with the sessions' streams (the halves would then run one after the
+// other, with an inter-stream barrier per layer: measured 30% slower than one
+// stream).  The runtime deals its few hardware queues (GPU_MAX_HW_QUEUES) out
+// to ordinary streams as it sees fit, while a stream created with a CU mask
+// gets a queue of its own; the mask enables every CU.  One per device rather
+// than one per session, because every extra active queue is another one for
+// the hardware scheduler to time-slice: with a masked stream per session the
+// bench's fourth session prefilled at 442k instead of 790k tok/s.
+namespace {
+struct SplitStream {
+    std::mutex lock;
+    hipStream_t st = nullptr;
+};
+SplitStream g_split_stream[64];
+}  // namespace
+
+static hipStream_t split_stream(int device) {
+    SplitStream& g = g_split_stream[device & 63];
+    std::lock_guard<std::mutex> l(g.lock);
+    if (!g.st) {
+        int cus = 0;
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+        std::vector<uint32_t> all((size_t)std::max(1, (cus + 31) / 32), 0xFFFFFFFFu);
+        if (hipExtStreamCreateWithCUMask(&g.st, (uint32_t)all.size(), all.data()) != hipSuccess) {
+            hipGetLastError();
+            g.st = nullptr;
+        }
+    }
+    return g.st;
+}
 
 // Persistent decode launches of all sessions on one device run one at a time.
 // Each launch needs every one of its workgroups resident at once (one per CU,
@@ -1071,25 +1102,6 @@ extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, i
         s->prefill_f32_gemm = g && !std::strcmp(g, "f32");
     }
     HIP_OR(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate");
-    // The second stream of a split prefill must not share a hardware queue
-    // with the session stream (the halves would then run one after the other,
-    // with an inter-stream barrier per layer: measured 30% slower than one
-    // stream).  The runtime deals its few hardware queues (GPU_MAX_HW_QUEUES)
-    // out to ordinary streams as it sees fit, while a stream created with a
-    // CU mask gets a queue of its own; the mask enables every CU.
-    if (s->fast && max_batch >= kSplitPrefillMin) {
-        int cus = 0;
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->device);
-        std::vector<uint32_t> all((size_t)std::max(1, (cus + 31) / 32), 0xFFFFFFFFu);
-        for (int k = 1; k < ahip_session::kMaxParts; k++)
-            HIP_OR(hipExtStreamCreateWithCUMask(&s->part_stream[k], (uint32_t)all.size(), all.data()),
-                   "hipExtStreamCreateWithCUMask");
-        HIP_OR(hipEventCreateWithFlags(&s->part_start, hipEventDisableTiming), "hipEventCreate");
-        for (int k = 0; k < ahip_session::kMaxParts; k++) {
-            HIP_OR(hipEventCreateWithFlags(&s->part_qkv[k], hipEventDisableTiming), "hipEventCreate");
-            HIP_OR(hipEventCreateWithFlags(&s->part_done[k], hipEventDisableTiming), "hipEventCreate");
-        }
-    }
     const SessionSizes z = session_sizes(c, capacity, max_batch, s->kv_f16);
     for (int l = 0; l < c.layer_count; l++) {
         s->kc.emplace_back(new DevBuf());
@@ -1319,7 +1331,14 @@ static int encode_split_prefill(ahip_session* s, const int32_t* dtok, int n, int
     const ahip_llama_config& c = m->c;
     const int H = c.hidden_size;
     parts = std::max(2, std::min(parts, ahip_session::kMaxParts));
-    s->part_stream[0] = s->stream;  // the other parts' streams and the events exist since session creation
+    s->part_stream[0] = s->stream;
+    if (!s->part_start) {
+        HIP_OR(hipEventCreateWithFlags(&s->part_start, hipEventDisableTiming), "hipEventCreate");
+        for (int k = 0; k < ahip_session::kMaxParts; k++) {
+            HIP_OR(hipEventCreateWithFlags(&s->part_qkv[k], hipEventDisableTiming), "hipEventCreate");
+            HIP_OR(hipEventCreateWithFlags(&s->part_done[k], hipEventDisableTiming), "hipEventCreate");
+        }
+    }
     // part k: rows [r[k], r[k+1]); every boundary but the last a multiple of 64
     int r[ahip_session::kMaxParts + 1];
     for (int k = 0; k < parts; k++) r[k] = (int)((int64_t)n * k / parts / 64 * 64);
@@ -1359,9 +1378,12 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
     const float2* rope = m->rope.as<float2>();
     const bool mfma = s->fast && n >= 16 && !s->prefill_f32_gemm;
     const bool flash = s->fast && n >= 16 && !s->prefill_generic_attention && s->kv_f16 && (hd == 64 || hd == 128);
-    if (mfma && n >= kSplitPrefillMin && s->part_stream[1] && !s->profiling &&
-        env_int("ALPACA_HIP_PREFILL_STREAMS", 2) >= 2 && !gemm_takes_wide_tiles(n, QW + 2 * KW))
-        return encode_split_prefill(s, dtok, n, pos, logits, flash, env_int("ALPACA_HIP_PREFILL_STREAMS", 2));
+    if (mfma && n >= kSplitPrefillMin && !s->profiling && env_int("ALPACA_HIP_PREFILL_STREAMS", 2) >= 2 &&
+        !gemm_takes_wide_tiles(n, QW + 2 * KW)) {
+        s->part_stream[1] = split_stream(m->device);
+        if (s->part_stream[1])
+            return encode_split_prefill(s, dtok, n, pos, logits, flash, env_int("ALPACA_HIP_PREFILL_STREAMS", 2));
+    }
     s->stage("embed");
     LAUNCH(launch_embed(dtok, n, m->embed.m, x, st));
     // Second-term planes of the f16 activation buffers (two-term prefill), after the first planes.
