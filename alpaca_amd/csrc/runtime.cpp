@@ -636,6 +636,8 @@ struct StageMark {
     int dispatches;
 };
 
+static void split_stream_release(int device);  // below, with the split prefill
+
 struct ahip_session {
     ahip_model* m = nullptr;
     int capacity = 0, max_batch = 0, kv_f16 = 1, fast = 1;
@@ -703,6 +705,7 @@ struct ahip_session {
         if (pdec_peer) hipEventDestroy(pdec_peer);
         // (a split's work on the shared split stream ends in part_done, which the
         // session stream waits for, so syncing the session stream covers it)
+        if (part_stream[1]) split_stream_release(m->device);
         if (part_start) hipEventDestroy(part_start);
         for (int k = 0; k < kMaxParts; k++) {
             if (part_qkv[k]) hipEventDestroy(part_qkv[k]);
@@ -767,8 +770,11 @@ struct ahip_session {
 // (encode_split_prefill).
 constexpr int kSplitPrefillMin = 3072;
 
-// The second-half stream of split prefills, one per device, shared by every
-// session and kept for the life of the process.  It must not share a hardware
+// The second-half stream of split prefills, one per device, shared by the
+// sessions that split a prefill: created on the first such split, destroyed
+// when the last of those sessions is (nothing HIP owns is left to the runtime's
+// exit-time teardown, under which a leftover stream crashed the profiled
+// process in exit handlers).  It must not share a hardware
 // queue with the sessions' streams (the halves would then run one after the
 // other, with an inter-stream barrier per layer: measured 30% slower than one
 // stream).  The runtime deals its few hardware queues (GPU_MAX_HW_QUEUES) out
@@ -781,11 +787,13 @@ namespace {
 struct SplitStream {
     std::mutex lock;
     hipStream_t st = nullptr;
+    int users = 0;  // sessions holding it
 };
 SplitStream g_split_stream[64];
 }  // namespace
 
-static hipStream_t split_stream(int device) {
+// A reference to the device's split stream (created if none exists), or null.
+static hipStream_t split_stream_acquire(int device) {
     SplitStream& g = g_split_stream[device & 63];
     std::lock_guard<std::mutex> l(g.lock);
     if (!g.st) {
@@ -797,7 +805,19 @@ static hipStream_t split_stream(int device) {
             g.st = nullptr;
         }
     }
+    if (g.st) g.users++;
     return g.st;
+}
+
+// Drops a session's reference; the last one synchronises and destroys the stream.
+static void split_stream_release(int device) {
+    SplitStream& g = g_split_stream[device & 63];
+    std::lock_guard<std::mutex> l(g.lock);
+    if (g.users > 0 && --g.users == 0 && g.st) {
+        hipStreamSynchronize(g.st);
+        hipStreamDestroy(g.st);
+        g.st = nullptr;
+    }
 }
 
 // Persistent decode launches of all sessions on one device run one at a time.
@@ -1380,7 +1400,7 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
     const bool flash = s->fast && n >= 16 && !s->prefill_generic_attention && s->kv_f16 && (hd == 64 || hd == 128);
     if (mfma && n >= kSplitPrefillMin && !s->profiling && env_int("ALPACA_HIP_PREFILL_STREAMS", 2) >= 2 &&
         !gemm_takes_wide_tiles(n, QW + 2 * KW)) {
-        s->part_stream[1] = split_stream(m->device);
+        if (!s->part_stream[1]) s->part_stream[1] = split_stream_acquire(m->device);
         if (s->part_stream[1])
             return encode_split_prefill(s, dtok, n, pos, logits, flash, env_int("ALPACA_HIP_PREFILL_STREAMS", 2));
     }
