@@ -201,7 +201,7 @@ def measured_traffic(root: str, rel: str = "profiles/c1_decode_hbm_counters.md",
     if not m or not h:
         return None, f"{rel} has no traffic figure or source hash"
     if h.group(1) != cur:
-        return None, f"stale: {rel} was measured on decode sources {h.group(1)}, this tree has {cur}"
+        return None, f"stale: {rel} was measured on {label.lower()} sources {h.group(1)}, this tree has {cur}"
     return float(m.group(1)) * 1e6, f"{rel} (rocprofv3 FETCH_SIZE and WRITE_SIZE runs, scaled by a copy; sources {cur})"
 
 
@@ -460,7 +460,7 @@ def main() -> int:
         ptraffic, ptraffic_note = (None, "counters are summarised for the gate+up+silu GEMM only")
         if domp == "ffn gate+up+silu":
             ptraffic, ptraffic_note = measured_traffic(os.path.dirname(os.path.abspath(__file__)),
-                                                       "profiles/c1_prefill_gemm_hbm_counters.md", GEMM_SOURCES,
+                                                       "profiles/c1_prefill_hbm_counters.md", GEMM_SOURCES,
                                                        "GEMM")
         roof_p = {"bound": "mfma", "kernel": domp, "achieved": round(ach, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                   "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFLOPS, 4), "traffic": ptraffic,
