@@ -9,7 +9,7 @@
 // flash_attn_kernel (prefill, f16 cache, hd 64/128): replaces the reference's
 // tensor-op and simdgroup prefill attention (tensor_attention.metal,
 // attention_prefill.metal).  A workgroup takes 64 queries of one head (16 per
-// wave; at head dim 64 two sets of four waves split the key range) and walks
+// wave; at head dim 64 two or four sets of four waves split the key range) and walks
 // 64-key blocks that move global -> LDS by DMA, three blocks in flight, K and V
 // both row-major; V^T fragments come from LDS transpose reads.
 // Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_f16,
@@ -34,6 +34,7 @@
 #include "common.h"
 
 #include <cstdlib>
+#include <type_traits>
 
 namespace {
 
@@ -110,14 +111,15 @@ __device__ __forceinline__ float vmax3(float a, float b, float c) {
     return d;
 }
 
-// NSET wave-sets per workgroup.  With NSET = 2 (head dim 64) a second set of
-// four waves takes the second half of the key blocks of the same 64 queries,
-// halving the sequential walk of the longest (causal) query blocks; the halves
-// merge at the end.  It costs LDS (one workgroup per CU), so the launcher uses
-// it only when one-set workgroups would not fill the chip.
+// NSET wave-sets per workgroup.  With NSET = 2 or 4 (head dim 64) the sets of
+// four waves take consecutive ranges of the key blocks of the same 64 queries,
+// dividing the sequential walk of the longest (causal) query blocks by NSET;
+// the ranges merge at the end.  It costs LDS (32 KB per set: two workgroups
+// per CU with two sets, one with four), so the launcher uses it only when
+// one-set workgroups would not fill the chip.
 template <int HD, int NSET, bool OUT16, bool TT, bool PT>
 __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
-    static_assert(NSET == 1 || (NSET == 2 && HD == 64), "two wave-sets fit LDS at head dim 64 only");
+    static_assert(NSET == 1 || ((NSET == 2 || NSET == 4) && HD == 64), "several wave-sets fit LDS at head dim 64 only");
     constexpr int KS = HD / 32, DT = HD / 16;
     constexpr int ROWB = HD * 2;          // bytes per key row
     constexpr int CH = HD / 8;            // 16-byte chunks per row
@@ -125,13 +127,11 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
     constexpr int TILE = BKV * ROWB;      // bytes of one K (or V) block
     constexpr int PERW = TILE / 1024 / 4; // DMA instructions per wave per block and matrix
     constexpr int PER = 2 * PERW;
-    // Three stage buffers per set, each K block then V block, both row-major and swizzled.
-    // With two sets the pipeline is two stages deep (64 KB of LDS, two
-    // workgroups per CU); with one set, three (48 KB, three per CU).
+    // Stage buffers per set, each K block then V block, both row-major and
+    // swizzled.  With several sets the pipeline is two stages deep (32 KB per
+    // set); with one set, three (48 KB, three workgroups per CU).
     constexpr int NSTAGE = NSET > 1 ? 2 : 3;
-    __shared__ __attribute__((aligned(16))) uint8_t sA0[2 * TILE], sA1[2 * TILE], sA2[NSTAGE > 2 ? 2 * TILE : 16];
-    __shared__ __attribute__((aligned(16))) uint8_t sB0[NSET > 1 ? 2 * TILE : 16], sB1[NSET > 1 ? 2 * TILE : 16],
-        sB2[NSET > 1 && NSTAGE > 2 ? 2 * TILE : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t stage_lds[NSET * NSTAGE * 2 * TILE];
 
     const int h = blockIdx.x;
     const int qb = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks first
@@ -146,9 +146,7 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
     // Positions of this wave's first and last query (clamped like qc).
     const int wpos_lo = a.start + min(qb * BQ + wl * 16, a.T - 1);
     const int wpos_hi = a.start + min(qb * BQ + wl * 16 + 15, a.T - 1);
-    uint8_t* const st0 = set ? sB0 : sA0;
-    uint8_t* const st1 = set ? sB1 : sA1;
-    uint8_t* const st2 = set ? sB2 : sA2;
+    uint8_t* const st0 = stage_lds + (set * NSTAGE) * 2 * TILE;  // this set's K buffers, then its V buffers
 
     // P enters the MFMA scaled by 2^14 (P <= 1 becomes <= 2^14): over long key
     // ranges most probabilities lie below f16's smallest normal (2^-14) and
@@ -172,33 +170,49 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
     const f16* kbase = a.kc + (int64_t)kvh * a.cap * HD;
     const f16* vbase = a.vc + (int64_t)kvh * a.cap * HD;
 
-    // K and V rows of this set's i-th key block into the stage buffer at LDS
-    // address sg.  Past the set's last block (or for a set with none) the load
-    // repeats a valid block that is never read, so every step waits on the same
-    // count; rows past kend repeat row kend-1 (in bounds; masked or unused).
-    auto issue = [&](uint32_t sg, int i) {
-        const int key0 = min(first + min(i, max(count, 1) - 1), nkb - 1) * BKV;
+    // K (or V) rows of this set's j-th key block into a stage buffer at LDS
+    // address dst.  Past the set's last block (or for a set with none) the load
+    // repeats a valid block that is never used, so every step waits on the
+    // same count; rows past kend repeat row kend-1 (in bounds; masked or unused).
+    // The block's first row is a wave-uniform base (SGPRs); each lane's byte
+    // offset within the block (its row and swizzled chunk) is fixed, so only a
+    // block that reaches past kend needs per-lane clamping.
+    uint32_t lane_off[PERW];
 #pragma unroll
-        for (int j = 0; j < PERW; j++) {
-            const int r0 = (j * 4 + wl) * RPI, r = r0 + lane / CH, c = (lane % CH) ^ kv_swz(r);
-            const int64_t off = (int64_t)min(key0 + r, kend - 1) * HD + c * 8;
-            dma16(kbase + off, sg + r0 * ROWB);
-            dma16(vbase + off, sg + TILE + r0 * ROWB);
+    for (int jj = 0; jj < PERW; jj++) {
+        const int r = (jj * 4 + wl) * RPI + lane / CH;
+        lane_off[jj] = r * ROWB + ((lane % CH) ^ kv_swz(r)) * 16;
+    }
+    auto issue = [&](const f16* base, uint32_t dst, int j) {
+        const int key0 = min(first + min(j, max(count, 1) - 1), nkb - 1) * BKV;
+        const f16* src = base + (int64_t)key0 * HD;
+        const int lim = kend - 1 - key0;  // last row of the block that exists
+        if (lim >= BKV - 1) {
+#pragma unroll
+            for (int jj = 0; jj < PERW; jj++) dma16s(src, lane_off[jj], dst + (jj * 4 + wl) * RPI * ROWB);
+        } else {
+#pragma unroll
+            for (int jj = 0; jj < PERW; jj++) {
+                const int r0 = (jj * 4 + wl) * RPI, r = r0 + lane / CH, c = (lane % CH) ^ kv_swz(r);
+                dma16s(src, min(r, lim) * ROWB + c * 16, dst + r0 * ROWB);
+            }
         }
     };
+    // Block j of the set is this wave's when it exists and some key of it lies
+    // at or before the wave's last query (a prefix of the set's blocks).
+    auto mine = [&](int j) { return j < count && (first + j) * BKV <= wpos_hi; };
 
-    float m = -INFINITY, lsum = 0.f;
-    f32x4 oacc[DT];
+    float m = -INFINITY;
+    // O^T accumulators, and lacc: the row sums of P (every element of lacc is
+    // the sum for the lane's query), from an MFMA with an all-ones A operand
+    // on the same f16 terms of P that O^T takes.
+    f32x4 oacc[DT], lacc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int d = 0; d < DT; d++) oacc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
-    auto add2 = [](float x, float y) { return x + y; };
+    const f16x8 ones = {(f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f};
 
-    auto compute = [&](const uint8_t* sg, int kb) {
-        const int key0 = kb * BKV;
-        const uint8_t* Kt = sg;
-        const uint8_t* Vt = sg + TILE;
-        // S^T tiles: sacc[t][r] = score(key0 + 16t + 4g + r, query qi)
-        f32x4 sacc[4];
+    // S^T tiles of one key block: sacc[t][r] = score(key0 + 16t + 4g + r, query qi)
+    auto qk = [&](const uint8_t* Kt, f32x4* sacc) {
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             sacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -210,7 +224,10 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
                 if constexpr (TT) sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[ks], sacc[t], 0, 0, 0);
             }
         }
-        // Masking only where some key of the block lies past some query of the wave.
+    };
+    // Masking only where some key of the block lies past some query of the wave.
+    auto mask = [&](f32x4* sacc, int kb) {
+        const int key0 = kb * BKV;
         if (key0 + BKV - 1 > wpos_lo) {
 #pragma unroll
             for (int t = 0; t < 4; t++)
@@ -218,6 +235,9 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
                 for (int r = 0; r < 4; r++)
                     if (key0 + 16 * t + 4 * g + r > pos_q) sacc[t][r] = -INFINITY;
         }
+    };
+    // Online softmax of one block's (masked) scores, then O^T += V^T P^T.
+    auto softmax_pv = [&](const f32x4* sacc, const uint8_t* Vt) {
         // Running max in log2 units (m, mn): the scale is positive, so the max
         // of the raw scores scales to the max of the scaled ones.
         // (v_max3 without the compiler's signalling-NaN quieting of every
@@ -228,18 +248,17 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
         float mx = vmax(vmax3(m0, m1, sacc[3][3]), vmax3(m2, m3, m4));
         mx = xor32_combine(xor16_combine(mx, vmax), vmax);  // the 4 lanes of this query
         const float mn = fmaxf(m, mx * a.scale_log2);
-        // -inf while every key seen so far is masked (possible in the second
+        // -inf while every key seen so far is masked (possible past the first
         // set); referencing 0 then keeps alpha and P at exactly 0.
         const float mref = mn == -INFINITY ? 0.f : mn;
         // v_exp_f32 without the library's denormal-result path: values below
         // 2^-126 become 0, as they do anyway once P is rounded to f16.
         const float alpha = __builtin_amdgcn_exp2f(m - mref);
-        // P * 2^14 straight from the exponent (the scale is exact); the row sum
-        // takes the same float32 values, so lsum carries the scale too and the
-        // final normalisation cancels it.  P enters the MFMA as f16 (hi, and lo
-        // with two terms).
+        // P * 2^14 straight from the exponent (the scale is exact); the row sums
+        // take the same terms, so they carry the scale too and the final
+        // normalisation cancels it.  P enters the MFMA as f16 (hi, and lo with
+        // two terms).
         const float eref = kLog2PScale - mref;
-        float ps = 0.f;
         // f16 pairs (keys r = 0,1 and 2,3 of tile t): hi = RNE(P), lo = RNE(P - hi)
         uint32_t ph[4][2], pl[PT ? 4 : 1][2];
 #pragma unroll
@@ -251,15 +270,13 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
                 const uint32_t h = pack_f16x2(e0, e1);
                 ph[t][pr] = h;
                 if constexpr (PT) pl[t][pr] = pack_f16x2(minus_f16_lo(h, e0), minus_f16_hi(h, e1));
-                ps += e0;
-                ps += e1;
             }
-        lsum = lsum * alpha + ps;
         // alpha is exactly 1 in every lane whose running max did not move (the
         // usual case past the first blocks): the wave then skips the rescale.
         if (__builtin_amdgcn_ballot_w64(m != mn)) {
 #pragma unroll
             for (int d = 0; d < DT; d++) oacc[d] *= alpha;
+            lacc *= alpha;
         }
         // O^T += V^T P^T.  Key order inside a 32-key step, identical on both
         // operands: slot e < 4 is key 32s + 4g + e, slot e >= 4 is 32s + 16 + 4g + e - 4.
@@ -271,6 +288,8 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
             if constexpr (PT)
                 plf = __builtin_bit_cast(f16x8, make_uint4(pl[2 * s][0], pl[2 * s][1], pl[2 * s + 1][0],
                                                            pl[2 * s + 1][1]));
+            lacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf, lacc, 0, 0, 0);
+            if constexpr (PT) lacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, plf, lacc, 0, 0, 0);
             const int ra = 32 * s + 4 * g + (c16 >> 2), rb = ra + 16;
 #pragma unroll
             for (int d = 0; d < DT; d++) {
@@ -285,50 +304,67 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
         m = mn;
     };
 
-    // Three-stage pipeline as in the prefill GEMM: wait for the step's block
-    // (the next stays in flight), barrier, refill the buffer of the previous
-    // step two blocks ahead, multiply.  A wave skips blocks whose keys all lie
-    // past its queries.
-    auto step = [&](const uint8_t* cur, uint8_t* refill, int i) {
-        wait_stage_barrier<PER>();
-        issue(lds_addr(refill), i + 2);
-        const int kb = first + i;
-        if (i < count && kb * BKV <= wpos_hi) compute(cur, kb);
-    };
-    if constexpr (NSTAGE == 3) {
-        issue(lds_addr(st0), 0);
-        issue(lds_addr(st1), 1);
-        for (int i = 0; i < steps; i += 3) {
-            step(st0, st2, i);
-            if (i + 1 < steps) step(st1, st0, i + 1);
-            if (i + 2 < steps) step(st2, st1, i + 2);
+    // Pipeline, K one block ahead of V: step i multiplies the scores of block
+    // i+1 (K) while it runs the softmax and P.V of block i, so a wave's MFMAs
+    // and its softmax VALU work are independent within a step.  NSTAGE buffers
+    // each for K and V; before step i the loads of K(i+1) and V(i) have been
+    // issued NSTAGE-2 steps earlier.  Step i: wait for them, barrier (every
+    // wave is done with K(i) and V(i-1)), refill those two buffers with
+    // K(i+NSTAGE) and V(i+NSTAGE-1), compute.
+    uint8_t* const kbuf = st0;
+    uint8_t* const vbuf = st0 + NSTAGE * TILE;
+    issue(kbase, lds_addr(kbuf), 0);
+#pragma unroll
+    for (int j = 0; j + 1 < NSTAGE; j++) {
+        issue(kbase, lds_addr(kbuf + (j + 1) * TILE), j + 1);
+        issue(vbase, lds_addr(vbuf + j * TILE), j);
+    }
+    wait_stage_barrier<(NSTAGE - 1) * PER>();  // K(0)
+    // Scores of the current and the next block alternate between sa and sb
+    // (the loop is unrolled over both parities, so no copies).
+    f32x4 sa[4], sb[4];
+    qk(kbuf, sa);
+    if (mine(0)) mask(sa, first);
+    auto step = [&](auto uc, int i, f32x4* scur, f32x4* snext) {
+        constexpr int R = decltype(uc)::value % NSTAGE;  // i % NSTAGE
+        wait_stage_barrier<(NSTAGE - 2) * PER>();
+        issue(kbase, lds_addr(kbuf + R * TILE), i + NSTAGE);
+        issue(vbase, lds_addr(vbuf + ((R + NSTAGE - 1) % NSTAGE) * TILE), i + NSTAGE - 1);
+        if (mine(i)) {
+            qk(kbuf + ((R + 1) % NSTAGE) * TILE, snext);
+            softmax_pv(scur, vbuf + R * TILE);
+            if (mine(i + 1)) mask(snext, first + i + 1);
         }
-    } else {
-        // wait for the step's block (nothing else in flight), barrier (every
-        // wave is done with the other buffer), refill it with the next block,
-        // multiply
-        auto step2 = [&](const uint8_t* cur, uint8_t* refill, int i) {
-            wait_stage_barrier<0>();
-            issue(lds_addr(refill), i + 1);
-            const int kb = first + i;
-            if (i < count && kb * BKV <= wpos_hi) compute(cur, kb);
-        };
-        issue(lds_addr(st0), 0);
-        for (int i = 0; i < steps; i += 2) {
-            step2(st0, st1, i);
-            if (i + 1 < steps) step2(st1, st0, i + 1);
+    };
+    using std::integral_constant;
+    for (int i = 0; i < steps; i += 2 * NSTAGE) {
+        step(integral_constant<int, 0>(), i, sa, sb);
+        if (i + 1 >= steps) break;
+        step(integral_constant<int, 1>(), i + 1, sb, sa);
+        if (i + 2 >= steps) break;
+        step(integral_constant<int, 2>(), i + 2, sa, sb);
+        if (i + 3 >= steps) break;
+        step(integral_constant<int, 3>(), i + 3, sb, sa);
+        if constexpr (NSTAGE > 2) {
+            if (i + 4 >= steps) break;
+            step(integral_constant<int, 4>(), i + 4, sa, sb);
+            if (i + 5 >= steps) break;
+            step(integral_constant<int, 5>(), i + 5, sb, sa);
         }
     }
     wait_stage_barrier<0>();  // no DMA may still be writing LDS past this point
 
-    lsum = xor32_combine(xor16_combine(lsum, add2), add2);
+    float lsum = lacc[0];
     if constexpr (NSET > 1) {
-        // The second set hands (m, lsum, O) to the first through LDS (its own
-        // stage buffers, idle now); the first merges and writes the output.
+        // Every other set hands (m, lsum, O) to the first through LDS (its own
+        // stage buffers, idle now: its DMA has landed); the first merges the
+        // sets in order and writes the output.
         static_assert(4 * DT * 4 * 64 * 4 <= 2 * TILE && 4 * 2 * 64 * 4 <= 2 * TILE, "merge scratch");
-        float* xo = (float*)sB0 + wl * DT * 4 * 64;  // O: 4 KB per wave
-        float* xml = (float*)sB1 + wl * 2 * 64;      // m, lsum
-        if (set == 1) {
+        auto xo_of = [&](int s) { return (float*)(stage_lds + (s * NSTAGE) * 2 * TILE) + wl * DT * 4 * 64; };
+        auto xml_of = [&](int s) { return (float*)(stage_lds + (s * NSTAGE + 1) * 2 * TILE) + wl * 2 * 64; };
+        if (set) {
+            float* xo = xo_of(set);  // O: 4 KB per wave
+            float* xml = xml_of(set);  // m, lsum
 #pragma unroll
             for (int d = 0; d < DT; d++)
 #pragma unroll
@@ -337,15 +373,29 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
             xml[64 + lane] = lsum;
         }
         __syncthreads();
-        if (set == 1) return;
-        const float m1 = xml[lane], l1 = xml[64 + lane];
-        const float mt = fmaxf(m, m1);  // finite: the first set saw key 0
-        const float a0 = __builtin_amdgcn_exp2f(m - mt), a1 = __builtin_amdgcn_exp2f(m1 - mt);
-        lsum = lsum * a0 + l1 * a1;
+        if (set) return;
+        float ms[NSET];
+        ms[0] = m;
+        float mt = m;  // finite: the first set saw key 0
 #pragma unroll
-        for (int d = 0; d < DT; d++)
+        for (int s = 1; s < NSET; s++) {
+            ms[s] = xml_of(s)[lane];
+            mt = fmaxf(mt, ms[s]);
+        }
+        const float a0 = __builtin_amdgcn_exp2f(m - mt);
+        lsum *= a0;
 #pragma unroll
-            for (int r = 0; r < 4; r++) oacc[d][r] = oacc[d][r] * a0 + xo[(d * 4 + r) * 64 + lane] * a1;
+        for (int d = 0; d < DT; d++) oacc[d] *= a0;
+#pragma unroll
+        for (int s = 1; s < NSET; s++) {
+            const float as = __builtin_amdgcn_exp2f(ms[s] - mt);
+            const float* xo = xo_of(s);
+            lsum = fmaf(xml_of(s)[64 + lane], as, lsum);
+#pragma unroll
+            for (int d = 0; d < DT; d++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) oacc[d][r] = fmaf(xo[(d * 4 + r) * 64 + lane], as, oacc[d][r]);
+        }
     }
     if (qi >= a.T) return;
     const float inv = 1.0f / lsum;  // lsum and O both carry the 2^14
@@ -598,18 +648,31 @@ hipError_t decode_dispatch(int G, dim3 grid, hipStream_t st, const float* q, con
 
 }  // namespace
 
+// Wave-sets per workgroup at head dim 64 (ALPACA_HIP_FLASH_SETS = 1 or 2,
+// read per launch, forces a count).  One-set workgroups (48 KB of LDS) run
+// three per CU: below three per CU the causal critical path dominates and
+// two sets win.  Four sets (one 1024-thread workgroup per CU) were slower at
+// every measured shape: the kernel is bound by the SIMDs' issue, not by the
+// longest query block's walk.
+static int flash_sets(dim3 grid) {
+    const char* e = std::getenv("ALPACA_HIP_FLASH_SETS");
+    const int forced = e ? std::atoi(e) : 0;
+    if (forced == 1 || forced == 2) return forced;
+    return (int64_t)grid.x * grid.y < 3 * 256 ? 2 : 1;
+}
+
+template <int NSET, bool TT, bool PT>
+void flash_launch64(const FlashArgs& a, dim3 grid, bool out16, hipStream_t st) {
+    if (out16) flash_attn_kernel<64, NSET, true, TT, PT><<<grid, 256 * NSET, 0, st>>>(a);
+    else flash_attn_kernel<64, NSET, false, TT, PT><<<grid, 256 * NSET, 0, st>>>(a);
+}
+
 template <bool TT, bool PT>
 hipError_t flash_dispatch(const FlashArgs& a, dim3 grid, int hd, bool out16, hipStream_t st) {
-    // One-set workgroups (48 KB of LDS at head dim 64) run three per CU: below
-    // three per CU the causal critical path dominates and two sets win.
-    const bool two_sets = (int64_t)grid.x * grid.y < 3 * 256;
     if (hd == 64) {
-        if (two_sets) {
-            if (out16) flash_attn_kernel<64, 2, true, TT, PT><<<grid, 512, 0, st>>>(a);
-            else flash_attn_kernel<64, 2, false, TT, PT><<<grid, 512, 0, st>>>(a);
-        } else {
-            if (out16) flash_attn_kernel<64, 1, true, TT, PT><<<grid, 256, 0, st>>>(a);
-            else flash_attn_kernel<64, 1, false, TT, PT><<<grid, 256, 0, st>>>(a);
+        switch (flash_sets(grid)) {
+        case 2: flash_launch64<2, TT, PT>(a, grid, out16, st); break;
+        default: flash_launch64<1, TT, PT>(a, grid, out16, st); break;
         }
     } else if (hd == 128) {
         if (out16) flash_attn_kernel<128, 1, true, TT, PT><<<grid, 256, 0, st>>>(a);

@@ -231,6 +231,36 @@ def test_flash_attention(hip_ops, t, start, heads, kv, hd):  # KernelTests.swift
         assert m["max_abs"] < 1.5e-3
 
 
+SET_CASES = [(8, 0, 9, 3), (17, 3, 6, 3), (100, 0, 9, 3), (64, 200, 9, 3), (300, 40, 15, 5), (1024, 0, 9, 3),
+             (64, 2000, 9, 3), (1536, 0, 32, 8)]
+
+
+@pytest.mark.parametrize("t,start,heads,kv", SET_CASES)
+def test_flash_attention_wave_sets(hip_ops, t, start, heads, kv):
+    """Head dim 64 with one and two wave-sets per workgroup
+    (ALPACA_HIP_FLASH_SETS, read per launch): two sets split each query
+    block's key blocks into consecutive ranges and merge them at the end, so
+    both counts are held to the CPU at 1.5e-3 and to each other at 2e-6 (the
+    merge changes the float32 summation order only).  Covers a set with no
+    key block (8 and 17 tokens: one block), ragged ranges (start 2000: 33
+    blocks) and grids past one round."""
+    hd = 64
+    cap = start + t
+    q, k, v = rand((t, heads, hd), t * 17 + start), rand((cap, kv, hd), t * 17 + start + 1), \
+        rand((cap, kv, hd), t * 17 + start + 2)
+    cpu = orc.attention(q, _f16(k), _f16(v), start)
+    out = {}
+    for sets in ("1", "2"):
+        with env(ALPACA_HIP_FLASH_SETS=sets):
+            out[sets] = hip_ops.attention(q, k, v, start, "f16", "fast")
+        m = metrics(out[sets], cpu)
+        print(f"[metrics] attention sets={sets} T={t} start={start} H={heads}/{kv}: {m}")
+        assert np.isfinite(out[sets]).all()
+        assert m["max_abs"] < 1.5e-3
+    for sets in ("2",):
+        assert np.abs(out[sets] - out["1"]).max() <= 2e-6, f"sets={sets}"
+
+
 @pytest.mark.parametrize("name,dt", FORMATS)
 def test_embedding_all_formats(hip_ops, name, dt):  # KernelTests.swift:90-99
     table = rand((50, 96), 21)
