@@ -237,7 +237,25 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
         }
     };
     // Online softmax of one block's (masked) scores, then O^T += V^T P^T.
+    // V^T fragment (dims 16d.., keys of 32-key step s) from row-major V in LDS.
+    auto v_frag = [&](const uint8_t* Vt, int s, int d) {
+        const int ra = 32 * s + 4 * g + (c16 >> 2), rb = ra + 16;
+        const int cb = 2 * d + ((c16 & 3) >> 1), hb = (c16 & 1) * 8;
+        const f16x4 lo = lds_read_tr(Vt + ra * ROWB + ((cb ^ kv_swz(ra)) * 16) + hb);
+        const f16x4 hi = lds_read_tr(Vt + rb * ROWB + ((cb ^ kv_swz(rb)) * 16) + hb);
+        return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+    // With one set (three waves per SIMD, registers to spare) the block's V^T
+    // fragments are read before the softmax, so their LDS latency overlaps it.
+    constexpr bool kEarlyV = NSET == 1 && HD == 64;
     auto softmax_pv = [&](const f32x4* sacc, const uint8_t* Vt) {
+        f16x8 vpre[kEarlyV ? 2 : 1][kEarlyV ? DT : 1];
+        if constexpr (kEarlyV) {
+#pragma unroll
+            for (int s = 0; s < 2; s++)
+#pragma unroll
+                for (int d = 0; d < DT; d++) vpre[s][d] = v_frag(Vt, s, d);
+        }
         // Running max in log2 units (m, mn): the scale is positive, so the max
         // of the raw scores scales to the max of the scaled ones.
         // (v_max3 without the compiler's signalling-NaN quieting of every
@@ -290,13 +308,11 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
                                                            pl[2 * s + 1][1]));
             lacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf, lacc, 0, 0, 0);
             if constexpr (PT) lacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, plf, lacc, 0, 0, 0);
-            const int ra = 32 * s + 4 * g + (c16 >> 2), rb = ra + 16;
 #pragma unroll
             for (int d = 0; d < DT; d++) {
-                const int cb = 2 * d + ((c16 & 3) >> 1), hb = (c16 & 1) * 8;
-                const f16x4 lo = lds_read_tr(Vt + ra * ROWB + ((cb ^ kv_swz(ra)) * 16) + hb);
-                const f16x4 hi = lds_read_tr(Vt + rb * ROWB + ((cb ^ kv_swz(rb)) * 16) + hb);
-                const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                f16x8 vf;
+                if constexpr (kEarlyV) vf = vpre[s][d];
+                else vf = v_frag(Vt, s, d);
                 oacc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, oacc[d], 0, 0, 0);
                 if constexpr (PT) oacc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, plf, oacc[d], 0, 0, 0);
             }
