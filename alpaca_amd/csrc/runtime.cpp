@@ -767,7 +767,7 @@ struct ahip_session {
 
 
 // Shortest prefill chunk that may run as two halves on two streams
-// (encode_split_prefill).
+// (encode_split_prefill); ALPACA_HIP_SPLIT_MIN (read per call) overrides it.
 constexpr int kSplitPrefillMin = 3072;
 
 // The second-half stream of split prefills, one per device, shared by the
@@ -1398,7 +1398,7 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
     const float2* rope = m->rope.as<float2>();
     const bool mfma = s->fast && n >= 16 && !s->prefill_f32_gemm;
     const bool flash = s->fast && n >= 16 && !s->prefill_generic_attention && s->kv_f16 && (hd == 64 || hd == 128);
-    if (mfma && n >= kSplitPrefillMin && !s->profiling && env_int("ALPACA_HIP_PREFILL_STREAMS", 2) >= 2 &&
+    if (mfma && n >= env_int("ALPACA_HIP_SPLIT_MIN", kSplitPrefillMin) && !s->profiling && env_int("ALPACA_HIP_PREFILL_STREAMS", 2) >= 2 &&
         !gemm_takes_wide_tiles(n, QW + 2 * KW)) {
         if (!s->part_stream[1]) s->part_stream[1] = split_stream_acquire(m->device);
         if (s->part_stream[1])
