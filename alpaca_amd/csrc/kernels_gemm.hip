@@ -1055,10 +1055,10 @@ hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
     // (block scaling, quant conversion) issues while the other's MFMAs run:
     // at the 1.7B shape 4-7% faster than four waves of 64x128.  Single-term
     // activations stay on the narrower tiles, where the wide ones measured
-    // slower.  128x64 tiles (two LDS stages) are kept while their grid fits in
-    // one round of the workgroups the device holds at once; past it (a
-    // near-empty second round, e.g. a 1600-column QKV over 4096 rows) 128x128
-    // tiles are faster.
+    // slower: 128x64 tiles (two LDS stages) while their grid fits in one round
+    // of the workgroups the device holds at once, else 128x128.  With two
+    // terms the other modes choose between 128x64 and 128x256 by the cost
+    // below.
     if constexpr (MODE == GEMM_SWIGLU) {
         if constexpr (!TT)
             if (f == 1) return run_dgemm<FMT, 256, 64, 128, 32, MODE, RH, TT>(a, st);
@@ -1069,10 +1069,24 @@ hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
     } else {
         if constexpr (!TT)
             if (f == 1) return run_dgemm<FMT, 256, 128, 128, 64, MODE, RH, TT>(a, st);
-        if constexpr (FMT != DT_F16)
-            if (f == 4 || (f == 0 && TT && wide_fits(tiles(128, 256))))
-                return run_dgemm<FMT, 128, 256, 64, 64, MODE, RH, TT>(a, st);
         const int slots = resident_per_cu<FMT, 128, 64, 64, 32, MODE, RH, TT>() * cus;
+        if constexpr (FMT != DT_F16) {
+            if (f == 4) return run_dgemm<FMT, 128, 256, 64, 64, MODE, RH, TT>(a, st);
+            if (f == 0 && TT) {
+                // Two terms: 128x64 tiles (two per CU) or 128x256 (one per CU),
+                // by a cost in rounds of resident workgroups.  A 128x64 round
+                // costs 1; a last round of at most one tile per CU 0.6 (a tile
+                // alone on its CU runs faster); a 128x256 round W = 1.32 at
+                // K <= 960 and 1.87 at K = 2048, as measured over prompts of
+                // 1,024-4,096 rows at the 135M, 360M and 1.7B shapes (128x128
+                // tiles, one per CU, were never the fastest there).
+                const int t64 = tiles(128, 64), rem = t64 % slots;
+                const double c64 = t64 / slots + (rem ? (rem <= cus ? 0.6 : 1.0) : 0.0);
+                const double cw = ((tiles(128, 256) + cus - 1) / cus) * (a.w.cols >= 1536 ? 1.87 : 1.32);
+                if (cw < c64) return run_dgemm<FMT, 128, 256, 64, 64, MODE, RH, TT>(a, st);
+                return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH, TT>(a, st);
+            }
+        }
         if (f == 2 || (f == 0 && tiles(128, 64) > slots)) return run_dgemm<FMT, 128, 128, 64, 64, MODE, RH, TT>(a, st);
         return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH, TT>(a, st);
     }
@@ -1108,8 +1122,10 @@ bool dma_offsets_fit(int m, int ldx, const DevMatrix& w) {
 }
 }  // namespace
 
-// Whether an M x N two-term prefill GEMM runs the wide tiles (128x256, one
-// workgroup per CU: grids of whole rounds, as pick_dgemm decides).
+// Whether an M x N two-term prefill GEMM has whole rounds of wide tiles
+// (128x256, one workgroup per CU: a multiple of the CUs, or at least three
+// rounds).  Splitting the rows of such a GEMM in two would cost the wide
+// tiles their full rounds, so those prefills stay on one stream.
 bool gemm_takes_wide_tiles(int m, int n) {
     const int cus = device_cus();
     const int t = ((m + 127) / 128) * ((n + 255) / 256);
