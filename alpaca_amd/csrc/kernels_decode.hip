@@ -547,7 +547,8 @@ __device__ __forceinline__ f16x4 vt_read_tr(const uint8_t* p) {
 // enters as hi + lo of P * 2^14 (scaled so that lo stays out of the f16
 // subnormals); V^T fragments come from LDS transpose reads of the V rows, which
 // move global -> LDS by DMA (no registers; a workgroup with several items
-// requests the next item's V and K rows as soon as the current P.V is done).  Writes,
+// requests the next item's K rows once the current scores are reduced and its V
+// rows once the current P.V is done).  Writes,
 // per query head g of the group, the words
 // [max (base-2 units), sum, unnormalised output[HD]] of the split
 // (attention_decode.metal:27-116 computes the same triple).
@@ -583,8 +584,9 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
     auto sub = [&](int k) { substamp(c, k); };
     // An item's cached K rows (cache rows past nc are loaded from row 0 of the
     // split, valid memory, and never used).  A workgroup with several items loads
-    // the next item's K rows and V rows once the current P.V is done, so those
-    // loads overlap the publication of the current item.
+    // the next item's K rows (every chunk) as soon as the current scores are
+    // reduced, and its V rows once the current P.V is done, so those loads
+    // overlap the current item's softmax, P.V and publication.
     int4 kr[NCH][2][KC];
     auto rows_of = [&](int t, int64_t& base, int& ncached, int& nrows) {
         int jt, st;
@@ -594,13 +596,13 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
         nrows = q1 - q0;
         base = ((int64_t)jt * cap + q0) * HD;
     };
-    auto load_k = [&](int t) {
+    auto load_k = [&](int t, bool all) {
         int64_t base;
         int ncached, nrows;
         rows_of(t, base, ncached, nrows);
 #pragma unroll
         for (int ci = 0; ci < NCH; ci++) {
-            if (32 * (wave + kWaves * ci) >= nrows) continue;  // uniform across the wave
+            if (!all && 32 * (wave + kWaves * ci) >= nrows) continue;  // uniform across the wave
 #pragma unroll
             for (int u = 0; u < 2; u++) {
                 const int r = 32 * (wave + kWaves * ci) + 16 * u + c16;
@@ -629,7 +631,7 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
         }
     };
     if (blockIdx.x < items) {
-        load_k(blockIdx.x);
+        load_k(blockIdx.x, false);
         dma_v(blockIdx.x);
     }
     for (int it = blockIdx.x; it < items; it += gridDim.x) {
@@ -734,6 +736,8 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
             }
         }
         __syncthreads();
+        // kr is free: the next item's K rows load during this item's softmax and P.V
+        if (next < items) load_k(next, true);
         sub(4);
         const int gq = c16 < G ? c16 : 0;
         const float mg = fmaxf(fmaxf(red[gq * 8 + 0], red[gq * 8 + 1]), fmaxf(red[gq * 8 + 2], red[gq * 8 + 3]));
@@ -781,10 +785,7 @@ __device__ __forceinline__ bool attention_phase(const u64* qkv, u64* part, int p
                 *(f32x4*)&ws[(wave * GM + c16) * HD + 16 * dt + 4 * q4] = oacc[dt];
         }
         __syncthreads();
-        if (next < items) {  // every wave is done with vt and kr: the next item's rows
-            dma_v(next);
-            load_k(next);
-        }
+        if (next < items) dma_v(next);  // every wave is done with vt: the next item's V rows
         sub(6);
         for (int i = tid; i < G * (HD + 2); i += kT) {
             const int g = i / (HD + 2), e = i - g * (HD + 2);
