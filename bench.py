@@ -130,10 +130,11 @@ def other_config(ctx, spec, ctx_len: int, prefill_tokens: int, steps: int = 64) 
     tok_bytes = decode_token_bytes(c, ctx_len + (steps - 1) / 2 + 1, 18 if spec.dtype == Q4_0 else 34)
     s.close()
     p = model.make_session(capacity=prefill_tokens, max_batch=4096)
-    p.forward(prompt[:prefill_tokens])
-    p.reset()
+    for _ in range(2):
+        p.forward(prompt[:prefill_tokens])
+        p.reset()
     walls = []
-    for _ in range(3):
+    for _ in range(5):
         t0 = time.perf_counter()
         p.forward(prompt[:prefill_tokens])
         walls.append(time.perf_counter() - t0)
