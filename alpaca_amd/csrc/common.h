@@ -99,7 +99,7 @@ __host__ __device__ inline int stage_scale_pitch(int rows) { return (rows + 63) 
 inline int64_t stage_scale_elems(int rows, int cols) { return (int64_t)(cols / 64) * stage_scale_pitch(rows) + 128; }
 hipError_t launch_stage_scales(const f16* s, uint32_t* s2, int rows, int cols, hipStream_t st);
 // Whether an M x N two-term prefill GEMM runs the wide (128x256) tiles.
-bool gemm_takes_wide_tiles(int m, int n);
+bool prefill_split_pays(int m, int n);
 
 // Cross-lane moves.  DPP controls (gfx9) act inside 16-lane rows without the
 // LDS crossbar: quad_perm [1,0,3,2] = 0xB1 and [2,3,0,1] = 0x4E swap lanes

@@ -730,9 +730,9 @@ __global__ __launch_bounds__(64 * (BM / WM) * (BN / WN)) void dgemm_kernel(GemmA
     // The stage buffers, in one array that the GEMM_QKV_ROPE epilogue reuses
     // for the tile's RoPE rows (BM positions x RH/2 pairs of 8 bytes: 32 KB at
     // head dim 64, so a 128x64 QKV tile keeps the two-stage footprint).
-    // 128x64 tiles pipeline two stages deep (three workgroups per CU at ~169
-    // VGPRs), the others three.
-    constexpr int NSTAGE = BM == 128 && BN == 64 ? 2 : 3;
+    // 128x64 and 64x64 tiles pipeline two stages deep (two and three workgroups
+    // per CU with two activation terms), the others three.
+    constexpr int NSTAGE = BN == 64 && BM <= 128 ? 2 : 3;
     constexpr int kStages = NSTAGE * L::BYTES;
     constexpr int kRope = MODE == GEMM_QKV_ROPE ? BM * RH * 4 : 0;
     constexpr int kSmem = kRope > kStages ? kRope : kStages;
@@ -991,9 +991,10 @@ hipError_t run_dgemm(const GemmArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// ALPACA_HIP_GEMM_TILE=256 | 128x128 | 128x64 | 128x256 forces a tile family
-// (tuning and tests; read on every launch); 256 means 256x128 (256x64 per
-// matrix for SwiGLU), 128x256 means 128x128 per matrix for SwiGLU.
+// ALPACA_HIP_GEMM_TILE=256 | 128x128 | 128x64 | 128x256 | 64x64 forces a tile
+// family (tuning and tests; read on every launch); 256 means 256x128 (256x64
+// per matrix for SwiGLU), 128x256 means 128x128 per matrix for SwiGLU, 64x64
+// is per matrix for SwiGLU too.
 int forced_tile() {
     const char* e = std::getenv("ALPACA_HIP_GEMM_TILE");
     if (!e) return 0;
@@ -1001,6 +1002,7 @@ int forced_tile() {
     if (!std::strcmp(e, "128x128")) return 2;
     if (!std::strcmp(e, "128x64")) return 3;
     if (!std::strcmp(e, "128x256")) return 4;
+    if (!std::strcmp(e, "64x64")) return 5;
     return 0;
 }
 
@@ -1057,19 +1059,31 @@ hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
     // activations stay on the narrower tiles, where the wide ones measured
     // slower: 128x64 tiles (two LDS stages) while their grid fits in one round
     // of the workgroups the device holds at once, else 128x128.  With two
-    // terms the other modes choose between 128x64 and 128x256 by the cost
-    // below.
+    // terms and quantised weights, small grids (at most 1.6 tiles of 128x64
+    // per CU, 3 for SwiGLU, whose 128x64 tiles run one per CU) take 64x64
+    // tiles (two LDS stages, three workgroups per CU): at the 135M shape over
+    // 2,048 rows the four GEMMs went 90 -> 75 us; above those counts, and at
+    // the 1.7B shape, they measured slower.  The other modes then choose
+    // between 128x64 and 128x256 by the cost below.
+    if (f == 5) return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT>(a, st);
+    auto small_grid = [&](double per_cu) {
+        return f == 0 && TT && FMT != DT_F16 && tiles(128, 64) <= per_cu * cus;
+    };
     if constexpr (MODE == GEMM_SWIGLU) {
         if constexpr (!TT)
             if (f == 1) return run_dgemm<FMT, 256, 64, 128, 32, MODE, RH, TT>(a, st);
         if constexpr (FMT != DT_F16)  // (f16 weight stages are 4x larger: no third stage fits)
             if (f == 4 || (f == 0 && TT && wide_fits(tiles(128, 128))))
                 return run_dgemm<FMT, 128, 128, 64, 32, MODE, RH, TT>(a, st);
+        if constexpr (TT && FMT != DT_F16)
+            if (small_grid(3.0)) return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT>(a, st);
         return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH, TT>(a, st);
     } else {
         if constexpr (!TT)
             if (f == 1) return run_dgemm<FMT, 256, 128, 128, 64, MODE, RH, TT>(a, st);
         const int slots = resident_per_cu<FMT, 128, 64, 64, 32, MODE, RH, TT>() * cus;
+        if constexpr (TT && FMT != DT_F16)
+            if (small_grid(1.6)) return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT>(a, st);
         if constexpr (FMT != DT_F16) {
             if (f == 4) return run_dgemm<FMT, 128, 256, 64, 64, MODE, RH, TT>(a, st);
             if (f == 0 && TT) {
@@ -1122,14 +1136,14 @@ bool dma_offsets_fit(int m, int ldx, const DevMatrix& w) {
 }
 }  // namespace
 
-// Whether an M x N two-term prefill GEMM has whole rounds of wide tiles
-// (128x256, one workgroup per CU: a multiple of the CUs, or at least three
-// rounds).  Splitting the rows of such a GEMM in two would cost the wide
-// tiles their full rounds, so those prefills stay on one stream.
-bool gemm_takes_wide_tiles(int m, int n) {
-    const int cus = device_cus();
-    const int t = ((m + 127) / 128) * ((n + 255) / 256);
-    return t >= cus && (t % cus == 0 || t >= 3 * cus);
+// Whether an m-row prefill chunk whose QKV GEMM is n columns wide is worth
+// running as two halves on two streams: that GEMM's grid of 128x64 tiles is at
+// most two rounds of two workgroups per CU, so each half's kernels leave CUs
+// idle at their tails for the other half to fill.  (At the 1.7B shape the
+// grids are larger and the halves only contend: 2,048 rows 123k tok/s on one
+// stream, 116k split.)
+bool prefill_split_pays(int m, int n) {
+    return (int64_t)((m + 127) / 128) * ((n + 63) / 64) <= 4 * (int64_t)device_cus();
 }
 
 hipError_t launch_gemm_mfma(const f16* x, const f16* xlo, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up,

@@ -768,7 +768,7 @@ struct ahip_session {
 
 // Shortest prefill chunk that may run as two halves on two streams
 // (encode_split_prefill); ALPACA_HIP_SPLIT_MIN (read per call) overrides it.
-constexpr int kSplitPrefillMin = 3072;
+constexpr int kSplitPrefillMin = 1536;
 
 // The second-half stream of split prefills, one per device, shared by the
 // sessions that split a prefill: created on the first such split, destroyed
@@ -1329,20 +1329,20 @@ static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, 
     return AHIP_OK;
 }
 
-// A fast prefill of at least this many tokens (unprofiled) whose projections
-// run the narrow GEMM tiles (grids of at most about one round of resident
-// workgroups) runs as two halves on two streams: the first half's layers on
-// the session stream, the second's on stream2, whose attention of each layer
+// A fast prefill chunk of at least kSplitPrefillMin tokens (unprofiled) whose
+// QKV GEMM has at most two rounds of 128x64 tiles (prefill_split_pays) runs as
+// two halves on two streams: the first half's layers on the session stream,
+// the second's on the shared second stream, whose attention of each layer
 // waits for the first half's K/V rows of that layer.  The halves' launches
-// overlap on the GPU, where one half alone leaves it partly idle (the GEMMs and
-// norms of such a chunk keep most waves waiting on memory): C1 at 4096 tokens
-// 775k -> 821k tok/s (at C4's 2048 tokens it measured -2% to +1%, so shorter
-// prefills keep one stream).  Where the wide tiles fill the device in
-// whole rounds (the 1.7B shape) halving the rows costs more than the overlap
-// gains (132k -> 122k), so those prefills keep one stream.  Each row goes
-// through the same kernels; only the flash kernel may pick its other key-range
-// split for the smaller grid of a half (a different float32 summation order:
-// C4 at 4096 tokens, logits within 3.5e-5).  C4 at 4096 tokens: 406k -> 441k.
+// overlap on the GPU, where one half alone leaves it partly idle (the GEMMs
+// and norms of such a chunk keep most waves waiting on memory).  Measured
+// (same box, one stream against two): C1 at 2,048 / 3,072 / 4,096 tokens
+// 702k / 726k / 795k -> 720k / 857k / 885k tok/s, C4 at 1,536 / 2,048 tokens
+// 343k / 389k -> 365k / 417k; below 1,536 tokens the split lost 5-7% at every
+// shape, and at the 1.7B shape, whose grids fill the device, it lost 3-6%.
+// Each row goes through the same kernels; only the flash kernel may pick its
+// other key-range split for the smaller grid of a half (a different float32
+// summation order: logits within 1e-5 of the peak).
 // ALPACA_HIP_PREFILL_STREAMS=1 (read per call) keeps one stream.
 
 static int encode_split_prefill(ahip_session* s, const int32_t* dtok, int n, int pos, bool logits, bool flash,
@@ -1399,7 +1399,7 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
     const bool mfma = s->fast && n >= 16 && !s->prefill_f32_gemm;
     const bool flash = s->fast && n >= 16 && !s->prefill_generic_attention && s->kv_f16 && (hd == 64 || hd == 128);
     if (mfma && n >= env_int("ALPACA_HIP_SPLIT_MIN", kSplitPrefillMin) && !s->profiling && env_int("ALPACA_HIP_PREFILL_STREAMS", 2) >= 2 &&
-        !gemm_takes_wide_tiles(n, QW + 2 * KW)) {
+        prefill_split_pays(n, QW + 2 * KW)) {
         if (!s->part_stream[1]) s->part_stream[1] = split_stream_acquire(m->device);
         if (s->part_stream[1])
             return encode_split_prefill(s, dtok, n, pos, logits, flash, env_int("ALPACA_HIP_PREFILL_STREAMS", 2));

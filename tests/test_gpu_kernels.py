@@ -107,7 +107,7 @@ def test_gemm_tile_families_agree_at_large_grids(hip_ops, name, dt):
     default takes 128x128 tiles.  Every tile family (ALPACA_HIP_GEMM_TILE,
     read per launch) accumulates each output over the same 32-weight blocks in
     the same order, so the store, residual and SwiGLU epilogues must agree bit
-    for bit across 128x64, 128x128, 128x256 and 256-row tiles.  The default is held to
+    for bit across 64x64, 128x64, 128x128, 128x256 and 256-row tiles.  The default is held to
     the analytic fast-GEMM bound (KernelTests.swift:179-217), and one-hot
     activation rows pin the weight path of every tile (Y[m] = W[:, m mod K]
     exactly)."""
@@ -120,14 +120,14 @@ def test_gemm_tile_families_agree_at_large_grids(hip_ops, name, dt):
     onehot[np.arange(m), np.arange(m) % k] = 1.0
     deq = orc.dequantize(dt, w.data, n * k).reshape(n, k)
     outs = {}
-    for tile in (None, "128x64", "128x128", "256", "128x256"):
+    for tile in (None, "128x64", "128x128", "256", "128x256", "64x64"):
         with env(ALPACA_HIP_GEMM_TILE=tile):
             outs[tile] = (hip_ops.linear(x, w, "fast"), hip_ops.linear_add(x, w, res, "fast"),
                           hip_ops.gate_up_silu(x, w, wu, "fast"))
             ident = hip_ops.linear(onehot, w, "fast")
         bad = np.argwhere(ident != deq.T[np.arange(m) % k])
         assert bad.size == 0, f"{name} tile {tile}: {len(bad)} weights differ, first at (m, n) = {bad[0]}"
-    for tile in ("128x64", "128x128", "256", "128x256"):
+    for tile in ("128x64", "128x128", "256", "128x256", "64x64"):
         for i, what in enumerate(("store", "residual", "swiglu")):
             a, b = outs[tile][i], outs[None][i]
             assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{name} {what}: tile {tile} != default"

@@ -58,12 +58,12 @@ C4_LONG = replace(synth.C4, config=replace(synth.C4.config, layer_count=2, vocab
 
 
 def test_fused_qkv_rope_with_large_tiles(hip_ctx):
-    """A 4096-token chunk at C4's layer shape: the QKV GEMM (N = 1600) has 800
-    tiles of 128x64, more than one round of resident workgroups, so it runs as
-    128x128 tiles with the RoPE epilogue (and the head-dim-64 RoPE staging).
-    Fused and unfused sessions agree bit for bit, and so do the tile families
-    forced through ALPACA_HIP_GEMM_TILE (read at every launch), since each
-    output accumulates the same blocks in the same order."""
+    """A 4096-token chunk at C4's layer shape: the QKV GEMM (N = 1600) runs the
+    RoPE epilogue (and the head-dim-64 RoPE staging) on whichever tile the
+    grid rule picks.  Fused and unfused sessions agree bit for bit, and so do
+    the tile families forced through ALPACA_HIP_GEMM_TILE (read at every
+    launch: 64x64, 128x64, 128x128 and 128x256), since each output
+    accumulates the same blocks in the same order."""
     spec = C4_LONG
     model = HIPLlamaModel(hip_ctx, spec.config, built(spec))
     prompt = synth.prompt_tokens(spec, 4096)
@@ -77,7 +77,7 @@ def test_fused_qkv_rope_with_large_tiles(hip_ctx):
         x, y = fused.decode(tok), ref.decode(tok)
         assert np.array_equal(x, y), f"decode step {step} differs: max |d| {np.abs(x - y).max():.3e}"
         tok = int(np.argmax(x))
-    for tile in ("128x64", "128x128", "128x256"):
+    for tile in ("64x64", "128x64", "128x128", "128x256"):
         fused.reset()
         with env(ALPACA_HIP_GEMM_TILE=tile):
             t = fused.forward(prompt)
