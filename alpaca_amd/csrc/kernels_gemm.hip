@@ -1059,15 +1059,16 @@ hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
     // activations stay on the narrower tiles, where the wide ones measured
     // slower: 128x64 tiles (two LDS stages) while their grid fits in one round
     // of the workgroups the device holds at once, else 128x128.  With two
-    // terms and quantised weights, small grids (at most 1.6 tiles of 128x64
-    // per CU, 3 for SwiGLU, whose 128x64 tiles run one per CU) take 64x64
-    // tiles (two LDS stages, three workgroups per CU): at the 135M shape over
-    // 2,048 rows the four GEMMs went 90 -> 75 us; above those counts, and at
-    // the 1.7B shape, they measured slower.  The other modes then choose
-    // between 128x64 and 128x256 by the cost below.
+    // terms, small grids (at most 1.6 tiles of 128x64 per CU, 3 for SwiGLU,
+    // whose 128x64 tiles run one per CU) take 64x64 tiles (two LDS stages,
+    // three workgroups per CU with quantised weights): at the 135M shape over
+    // 2,048 rows the four GEMMs went 90 -> 75 us, and with f16 weights (the
+    // prefill weight cache) the 4,096-token prefill 812k -> 864k tok/s; above
+    // those counts, and at the 1.7B shape, they measured slower.  The other
+    // modes then choose between 128x64 and 128x256 by the cost below.
     if (f == 5) return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT>(a, st);
     auto small_grid = [&](double per_cu) {
-        return f == 0 && TT && FMT != DT_F16 && tiles(128, 64) <= per_cu * cus;
+        return f == 0 && TT && tiles(128, 64) <= per_cu * cus;
     };
     if constexpr (MODE == GEMM_SWIGLU) {
         if constexpr (!TT)
@@ -1075,14 +1076,14 @@ hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
         if constexpr (FMT != DT_F16)  // (f16 weight stages are 4x larger: no third stage fits)
             if (f == 4 || (f == 0 && TT && wide_fits(tiles(128, 128))))
                 return run_dgemm<FMT, 128, 128, 64, 32, MODE, RH, TT>(a, st);
-        if constexpr (TT && FMT != DT_F16)
+        if constexpr (TT)
             if (small_grid(3.0)) return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT>(a, st);
         return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH, TT>(a, st);
     } else {
         if constexpr (!TT)
             if (f == 1) return run_dgemm<FMT, 256, 128, 128, 64, MODE, RH, TT>(a, st);
         const int slots = resident_per_cu<FMT, 128, 64, 64, 32, MODE, RH, TT>() * cus;
-        if constexpr (TT && FMT != DT_F16)
+        if constexpr (TT)
             if (small_grid(1.6)) return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT>(a, st);
         if constexpr (FMT != DT_F16) {
             if (f == 4) return run_dgemm<FMT, 128, 256, 64, 64, MODE, RH, TT>(a, st);
