@@ -99,12 +99,13 @@ def test_two_stream_prefill_matches_one_stream(hip_ctx, spec, prec):
     stream (the flash kernel may choose its other key-range split for a
     half's smaller grid, a different float32 summation order), so the logits
     and the decode steps that read the cache must agree with
-    ALPACA_HIP_PREFILL_STREAMS=1 (read per call) to 1e-5 of the logit peak: one
-    3100-token chunk (uneven halves), then a 4300-token prompt over chunks of
-    3200 (a split chunk, then a short one at position 3200)."""
+    ALPACA_HIP_PREFILL_STREAMS=1 (read per call) to 1e-5 of the logit peak: a
+    1600-token chunk (halves of 768 and 832 rows, just past the 1,536-token
+    threshold), one 3100-token chunk (uneven halves), then a 4300-token prompt
+    over chunks of 3200 (a split chunk, then a short one at position 3200)."""
     model = HIPLlamaModel(hip_ctx, spec.config, built(spec))
     prompt = synth.prompt_tokens(spec, 4300)
-    for n in (3100, 4300):
+    for n in (1600, 3100, 4300):
         out = {}
         for streams in ("1", "2"):
             s = model.make_session(capacity=4352, max_batch=3200, gemm_precision=prec)
