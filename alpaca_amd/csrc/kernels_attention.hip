@@ -9,9 +9,9 @@
 // flash_attn_kernel (prefill, f16 cache, hd 64/128): replaces the reference's
 // tensor-op and simdgroup prefill attention (tensor_attention.metal,
 // attention_prefill.metal).  A workgroup takes 64 queries of one head (16 per
-// wave; at head dim 64 two or four sets of four waves split the key range) and walks
-// 64-key blocks that move global -> LDS by DMA, three blocks in flight, K and V
-// both row-major; V^T fragments come from LDS transpose reads.
+// wave; at head dim 64 and on small grids two sets of four waves split the key
+// range) and walks 64-key blocks that move global -> LDS by DMA, K one block
+// ahead of V, both row-major; V^T fragments come from LDS transpose reads.
 // Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_f16,
 // so each lane owns one query column: the online-softmax max/sum need only
 // two cross-lane shuffles, and the probabilities already sit in the B-operand
