@@ -73,12 +73,18 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(const float* x, co
     if (row >= rows) return;  // whole waves leave together
     const int n4 = dim >> 2;
     const float4* xr = (const float4*)(x + (int64_t)row * dim);
-    float4 v[kNormV4];
+    const float4* wr = (const float4*)w;
+    // the gains load with the row, not after the reduction
+    float4 v[kNormV4], gv[kNormV4];
     float ss = 0.f;
 #pragma unroll
     for (int k = 0; k < kNormV4; k++) {
         const int i = lane + 64 * k;
         v[k] = i < n4 ? xr[i] : float4{0.f, 0.f, 0.f, 0.f};
+        gv[k] = i < n4 ? wr[i] : float4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int k = 0; k < kNormV4; k++) {
         ss += v[k].x * v[k].x;
         ss += v[k].y * v[k].y;
         ss += v[k].z * v[k].z;
@@ -86,12 +92,11 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(const float* x, co
     }
     ss = wave_sum(ss);
     const float scale = 1.0f / sqrtf(ss / (float)dim + eps);
-    const float4* wr = (const float4*)w;
 #pragma unroll
     for (int k = 0; k < kNormV4; k++) {
         const int i = lane + 64 * k;
         if (i >= n4) break;
-        const float4 g = wr[i];
+        const float4 g = gv[k];
         const float4 y = {(v[k].x * scale) * g.x, (v[k].y * scale) * g.y, (v[k].z * scale) * g.z,
                           (v[k].w * scale) * g.w};
         if (of) ((float4*)(of + (int64_t)row * dim))[i] = y;
