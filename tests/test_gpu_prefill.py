@@ -93,11 +93,13 @@ C1_2L = replace(synth.C1, config=replace(synth.C1.config, layer_count=2, context
 @pytest.mark.parametrize("spec", [C1_2L, C4_LONG, synth.with_dtype(replace(C1_2L, name="c1-shape-2l-f16"), F16)],
                          ids=lambda s: s.name)
 def test_two_stream_prefill_matches_one_stream(hip_ctx, spec, prec):
-    """A long fast prefill whose GEMMs run narrow tiles runs as two halves on two
+    """A fast prefill chunk of at least 1,536 tokens whose QKV GEMM grid is at
+    most two rounds of 128x64 tiles runs as two halves on two
     streams (the second half's attention of each layer waits for the first
-    half's K/V rows).  Every row goes through the same kernels as in one
-    stream (the flash kernel may choose its other key-range split for a
-    half's smaller grid, a different float32 summation order), so the logits
+    half's K/V rows).  Every row goes through the same arithmetic as in one
+    stream (a half's smaller grids may take other GEMM tiles, which agree bit
+    for bit; the flash kernel may choose its other key-range split, a
+    different float32 summation order), so the logits
     and the decode steps that read the cache must agree with
     ALPACA_HIP_PREFILL_STREAMS=1 (read per call) to 1e-5 of the logit peak: a
     1600-token chunk (halves of 768 and 832 rows, just past the 1,536-token
