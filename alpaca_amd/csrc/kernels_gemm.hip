@@ -640,7 +640,7 @@ __device__ __forceinline__ void acc_epilogue(const GemmArgs& p, const f32x4 (&ac
 // KVCache.write, KVCache.swift:44-63).  smem holds at least BM * hd/2 float2.
 template <int BM, int TM, int TN, bool TT>
 __device__ __forceinline__ void qkv_rope_epilogue(const GemmArgs& p, const f32x4 (&acc)[TM][TN], uint8_t* smem,
-                                                  int m0, int mb, int nb, int M, int N, int lane) {
+                                                  int m0, int mb, int nb, int M, int N, int lane, bool active = true) {
 #pragma clang fp contract(off)
     const QkvRope& o = p.qkv;
     const int hd = o.hd, half = hd / 2, QW = o.heads * hd, KW = o.kv_heads * hd;
@@ -661,6 +661,7 @@ __device__ __forceinline__ void qkv_rope_epilogue(const GemmArgs& p, const f32x4
         }
         __syncthreads();
     }
+    if (!active) return;
     const float2* cs_rows = (const float2*)smem;
     const bool full = mb + 16 * TM <= M;  // wave-uniform
     const bool odd = lane & 1;
@@ -722,24 +723,36 @@ __device__ __forceinline__ void qkv_rope_epilogue(const GemmArgs& p, const f32x4
 
 // RH: for GEMM_QKV_ROPE, the largest head dim the RoPE staging holds (64 or
 // 128); 0 for the other modes.
-template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH, bool TT>
-__global__ __launch_bounds__(64 * (BM / WM) * (BN / WN)) void dgemm_kernel(GemmArgs p) {
+// KS sets of NW waves each take a contiguous share of the K stages (their own
+// stage buffers) and add their accumulators through LDS at the end: on grids
+// of about one workgroup per CU, twice the waves per CU and half the
+// sequential stage loop per workgroup.  (The split changes the float32
+// summation order of each output, so a KS = 2 tile agrees with the others to
+// rounding, not bit for bit.)
+template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH, bool TT, int KS = 1>
+__global__ __launch_bounds__(64 * (BM / WM) * (BN / WN) * KS) void dgemm_kernel(GemmArgs p) {
     using G = DGemm<FMT, BM, BN, WM, WN, MODE, TT>;
     using L = DStage<FMT, BM, BN, G::NB, TT>;
     constexpr int NB = G::NB, TM = G::TM, TN = G::TN, PER = G::PER, NW = G::NW;
+    static_assert(KS == 1 || KS == 2, "one or two K sets");
     // The stage buffers, in one array that the GEMM_QKV_ROPE epilogue reuses
     // for the tile's RoPE rows (BM positions x RH/2 pairs of 8 bytes: 32 KB at
     // head dim 64, so a 128x64 QKV tile keeps the two-stage footprint).
     // 128x64 and 64x64 tiles pipeline two stages deep (two and three workgroups
     // per CU with two activation terms), the others three.
     constexpr int NSTAGE = BN == 64 && BM <= 128 ? 2 : 3;
-    constexpr int kStages = NSTAGE * L::BYTES;
+    constexpr int kStages = NSTAGE * L::BYTES;  // one K set's stage buffers
     constexpr int kRope = MODE == GEMM_QKV_ROPE ? BM * RH * 4 : 0;
-    constexpr int kSmem = kRope > kStages ? kRope : kStages;
+    // the second K set's accumulators go past the first set's stage buffers
+    constexpr int kRed = KS > 1 ? NB * TM * TN * 4 * 64 * NW * 4 : 0;
+    constexpr int kSet = KS * kStages > kStages + kRed ? KS * kStages : kStages + kRed;
+    constexpr int kSmem = kRope > kSet ? kRope : kSet;
     __shared__ __attribute__((aligned(16))) uint8_t smem[kSmem];
-    uint8_t* const st0 = smem;
-    uint8_t* const st1 = smem + L::BYTES;
-    uint8_t* const st2 = smem + (NSTAGE > 2 ? 2 : 0) * L::BYTES;
+    const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kset = wave_all / NW;  // K set of this wave
+    uint8_t* const st0 = smem + kset * kStages;
+    uint8_t* const st1 = st0 + L::BYTES;
+    uint8_t* const st2 = st0 + (NSTAGE > 2 ? 2 : 0) * L::BYTES;
 
     const int K = p.w.cols, N = p.w.rows, M = p.M, nb = K >> 5, spitch = stage_scale_pitch(N);
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, tiles = tiles_m * tiles_n;
@@ -747,9 +760,13 @@ __global__ __launch_bounds__(64 * (BM / WM) * (BN / WN)) void dgemm_kernel(GemmA
     const int t = xcd * q + min(xcd, rem) + b / 8;  // XCD-major tile order (bijective)
     const int m0 = (t / tiles_n) * BM, n0 = (t % tiles_n) * BN;
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = wave_all % NW;  // within the K set
     const int wm = wave / (BN / WN), wn = wave % (BN / WN);
     const int nk = K / DBK;
+    // This set's stages: [k0s, k0s + cnt); every set runs `per` steps (the
+    // same barriers), reloading its last stage past its end without using it.
+    const int per = (nk + KS - 1) / KS, k0s = kset * per, cnt = max(0, min(nk - k0s, per));
+    auto ktc = [&](int i) { return min(k0s + min(i, max(cnt, 1) - 1), nk - 1); };
 
     // Per-lane byte offsets of the DMA rows (loop-invariant, 32-bit: the host
     // checks that every operand spans less than 4 GiB); each stage adds its K
@@ -919,39 +936,68 @@ __global__ __launch_bounds__(64 * (BM / WM) * (BN / WN)) void dgemm_kernel(GemmA
     // the buffer consumed by the previous step with stage kt+2, multiply stage
     // kt.  Past the end the refill reloads the last stage into a buffer that is
     // never read again, so every step has the same wait count.
-    auto step = [&](const uint8_t* cur, uint8_t* refill, int kt) {
+    auto step = [&](const uint8_t* cur, uint8_t* refill, int i) {
         wait_stage_barrier<PER>();
-        issue(lds_addr(refill), min(kt + 2, nk - 1));
-        compute(cur);
+        issue(lds_addr(refill), ktc(i + 2));
+        if (i < cnt) compute(cur);
     };
     if constexpr (NSTAGE == 3) {
-        issue(lds_addr(st0), 0);
-        issue(lds_addr(st1), min(1, nk - 1));
-        for (int kt = 0; kt < nk; kt += 3) {
-            step(st0, st2, kt);
-            if (kt + 1 < nk) step(st1, st0, kt + 1);
-            if (kt + 2 < nk) step(st2, st1, kt + 2);
+        issue(lds_addr(st0), ktc(0));
+        issue(lds_addr(st1), ktc(1));
+        for (int i = 0; i < per; i += 3) {
+            step(st0, st2, i);
+            if (i + 1 < per) step(st1, st0, i + 1);
+            if (i + 2 < per) step(st2, st1, i + 2);
         }
     } else {
         // wait for the stage (nothing else in flight), barrier (every wave is
         // done with the other buffer), refill it with the next stage, multiply
-        auto step2 = [&](const uint8_t* cur, uint8_t* refill, int kt) {
+        auto step2 = [&](const uint8_t* cur, uint8_t* refill, int i) {
             wait_stage_barrier<0>();
-            issue(lds_addr(refill), min(kt + 1, nk - 1));
-            compute(cur);
+            issue(lds_addr(refill), ktc(i + 1));
+            if (i < cnt) compute(cur);
         };
-        issue(lds_addr(st0), 0);
-        for (int kt = 0; kt < nk; kt += 2) {
-            step2(st0, st1, kt);
-            if (kt + 1 < nk) step2(st1, st0, kt + 1);
+        issue(lds_addr(st0), ktc(0));
+        for (int i = 0; i < per; i += 2) {
+            step2(st0, st1, i);
+            if (i + 1 < per) step2(st1, st0, i + 1);
         }
     }
     // No DMA may still be writing this workgroup's LDS when its waves end.
     wait_stage_barrier<0>();
+    if constexpr (KS > 1) {
+        // The second set hands its accumulators to the first through its own
+        // (idle) stage buffers; the first adds them and runs the epilogue.
+        float* red = (float*)(smem + kStages) + wave * 64 + lane;
+        if (kset == 1) {
+#pragma unroll
+            for (int mat = 0; mat < NB; mat++)
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) red[(((mat * TM + i) * TN + j) * 4 + r) * 64 * NW] = acc[mat][i][j][r];
+        }
+        __syncthreads();
+        if (kset == 0) {
+#pragma unroll
+            for (int mat = 0; mat < NB; mat++)
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) acc[mat][i][j][r] += red[(((mat * TM + i) * TN + j) * 4 + r) * 64 * NW];
+        }
+    }
     if constexpr (MODE == GEMM_QKV_ROPE) {
-        qkv_rope_epilogue<BM, TM, TN, TT>(p, acc[0], smem, m0, m0 + wm * WM, n0 + wn * WN, M, N, lane);
+        // (every wave joins the epilogue's table copy and barrier; only the
+        // first K set stores)
+        qkv_rope_epilogue<BM, TM, TN, TT>(p, acc[0], smem, m0, m0 + wm * WM, n0 + wn * WN, M, N, lane, kset == 0);
         return;
     }
+    if (kset != 0) return;
     if constexpr (MODE == GEMM_ACC) {
         acc_epilogue<TM, TN>(p, acc[0], m0 + wm * WM, n0 + wn * WN, M, N, lane);
         return;
@@ -984,10 +1030,10 @@ __global__ __launch_bounds__(64 * (BM / WM) * (BN / WN)) void dgemm_kernel(GemmA
         }
 }
 
-template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH, bool TT>
+template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH, bool TT, int KS = 1>
 hipError_t run_dgemm(const GemmArgs& a, hipStream_t st) {
     const int tiles = ((a.M + BM - 1) / BM) * ((a.w.rows + BN - 1) / BN);
-    dgemm_kernel<FMT, BM, BN, WM, WN, MODE, RH, TT><<<tiles, 64 * (BM / WM) * (BN / WN), 0, st>>>(a);
+    dgemm_kernel<FMT, BM, BN, WM, WN, MODE, RH, TT, KS><<<tiles, 64 * (BM / WM) * (BN / WN) * KS, 0, st>>>(a);
     return hipGetLastError();
 }
 
@@ -1003,6 +1049,7 @@ int forced_tile() {
     if (!std::strcmp(e, "128x64")) return 3;
     if (!std::strcmp(e, "128x256")) return 4;
     if (!std::strcmp(e, "64x64")) return 5;
+    if (!std::strcmp(e, "64x64k2")) return 9;
     return 0;
 }
 
@@ -1064,9 +1111,14 @@ hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
     // three workgroups per CU with quantised weights): at the 135M shape over
     // 2,048 rows the four GEMMs went 90 -> 75 us, and with f16 weights (the
     // prefill weight cache) the 4,096-token prefill 812k -> 864k tok/s; above
-    // those counts, and at the 1.7B shape, they measured slower.  The other
-    // modes then choose between 128x64 and 128x256 by the cost below.
+    // those counts, and at the 1.7B shape, they measured slower.  Where the
+    // 64x64 grid is at most one tile per CU, QKV, Wo and down split each
+    // tile's K stages over two sets of four waves (C1 at 1,024 rows: QKV 13.2
+    // -> 12.2 us, Wo 10.9 -> 10.1, down 18.0 -> 15.1; C4 Wo 15.2 -> 13.1, down
+    // 28.9 -> 22.9; slower on larger grids and for SwiGLU).  The other modes
+    // then choose between 128x64 and 128x256 by the cost below.
     if (f == 5) return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT>(a, st);
+    if (f == 9) return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT, 2>(a, st);
     auto small_grid = [&](double per_cu) {
         return f == 0 && TT && tiles(128, 64) <= per_cu * cus;
     };
@@ -1084,7 +1136,11 @@ hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
             if (f == 1) return run_dgemm<FMT, 256, 128, 128, 64, MODE, RH, TT>(a, st);
         const int slots = resident_per_cu<FMT, 128, 64, 64, 32, MODE, RH, TT>() * cus;
         if constexpr (TT)
-            if (small_grid(1.6)) return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT>(a, st);
+            if (small_grid(1.6)) {
+                // at most one 64x64 tile per CU (quantised weights): two K sets
+                if (FMT != DT_F16 && tiles(64, 64) <= cus) return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT, 2>(a, st);
+                return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT>(a, st);
+            }
         if constexpr (FMT != DT_F16) {
             if (f == 4) return run_dgemm<FMT, 128, 256, 64, 64, MODE, RH, TT>(a, st);
             if (f == 0 && TT) {

@@ -131,6 +131,15 @@ def test_gemm_tile_families_agree_at_large_grids(hip_ops, name, dt):
         for i, what in enumerate(("store", "residual", "swiglu")):
             a, b = outs[tile][i], outs[None][i]
             assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{name} {what}: tile {tile} != default"
+    # Two K sets per 64x64 tile sum each output's blocks in two partial sums:
+    # equal to the others to float32 rounding, and exact on one-hot rows.
+    with env(ALPACA_HIP_GEMM_TILE="64x64k2"):
+        k2 = (hip_ops.linear(x, w, "fast"), hip_ops.linear_add(x, w, res, "fast"), hip_ops.gate_up_silu(x, w, wu, "fast"))
+        ident = hip_ops.linear(onehot, w, "fast")
+    assert np.array_equal(ident, deq.T[np.arange(m) % k]), f"{name}: two K sets, one-hot rows"
+    for i, what in enumerate(("store", "residual", "swiglu")):
+        a, b = k2[i], outs[None][i]
+        assert np.abs(a - b).max() <= 1e-5 * max(1.0, float(np.abs(b).max())), f"{name} {what}: two K sets"
     cpu = orc.linear(x, dt, w.data, n).astype(np.float64)
     bound = np.abs(x.astype(np.float64)) @ np.abs(deq.astype(np.float64)).T / 1024 + 1e-5
     err = np.abs(outs[None][0].astype(np.float64) - cpu)
