@@ -298,7 +298,7 @@ hipError_t launch_gemm_f32(const float* x, int ldx, int m, const DevMatrix& w, c
 
 // persistent single-token decode (kernels_decode.hip)
 //
-// One cooperative launch computes one token: every decoder layer, the logits
+// One launch computes one token: every decoder layer, the logits
 // and the greedy arg-max.  Phases hand data to each other through exchange
 // words (8 bytes: f32 value in the low half, the launch's tag in the high
 // half) written and polled with agent-scope atomics; see kernels_decode.hip.
@@ -358,10 +358,11 @@ size_t decode_static_lds(int fmt, int hd, int heads, int kv_heads);
 size_t decode_logits_stage_offset(const DecodeParams& p, int grid);
 int decode_logits_stage_rows(const DecodeParams& p, size_t lds_limit);
 hipError_t decode_kernel_occupancy(int fmt, int hd, int heads, int kv_heads, size_t lds, int* blocks_per_cu);
-// cooperative = 0 launches the same grid as an ordinary kernel (for profilers
-// that cannot follow cooperative launches); residency is then not guaranteed
-// by the runtime, and a workgroup that never starts makes the others' bounded
-// waits expire, so the launch still ends, with an error.
+// cooperative = 1 launches the grid with hipLaunchCooperativeKernel, 0 as an
+// ordinary kernel (the default; the host orders persistent launches one at a
+// time).  Residency of all workgroups is then not checked by the runtime: a
+// workgroup that never starts makes the others' bounded waits expire, so the
+// launch still ends, with an error.
 hipError_t launch_decode_step(int fmt, const DecodeParams& p, int grid, size_t lds, int cooperative, hipStream_t st);
 
 // attention (kernels_attention.hip).  Cache layout [kv_heads][capacity][hd].

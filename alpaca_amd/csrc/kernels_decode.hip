@@ -1,4 +1,4 @@
-// Persistent single-token decode for gfx950: one cooperative launch runs a
+// Persistent single-token decode for gfx950: one launch runs a
 // whole decode step of the Llama forward pass (every layer, the logits and the
 // greedy arg-max) for one token.
 //
@@ -58,7 +58,8 @@
 // Every wait is bounded: past `timeout_ticks` of the wall clock, or when any
 // workgroup has raised the shared abort word, a workgroup raises the abort
 // word and the mapped status word and returns, so a launch always drains.  The
-// launch is cooperative, so all workgroups are resident at once.
+// grid is one workgroup per CU, all resident at once on a device that no other
+// long-lived grid holds (the host orders persistent launches one at a time).
 #include "common.h"
 #include "gemv_chunks.h"
 

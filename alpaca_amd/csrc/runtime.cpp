@@ -667,9 +667,9 @@ struct ahip_session {
     int dec_split_len = 0, dec_splits = 0;
     hipGraphExec_t greedy_graph = nullptr;
     bool graph_failed = false;
-    // persistent single-token decode (kernels_decode.hip): one cooperative launch per token
+    // persistent single-token decode (kernels_decode.hip): one launch per token
     bool pdec = false;
-    int pdec_fmt = 0, pdec_grid = 0, pdec_coop = 1;
+    int pdec_fmt = 0, pdec_grid = 0, pdec_coop = 0;
     size_t pdec_lds = 0;
     DecodeParams pdec_params;
     DevBuf pdec_layers, pdec_xbuf, pdec_ctl;  // ctl: [0] epoch, [1] abort word
@@ -821,8 +821,8 @@ static void split_stream_release(int device) {
 }
 
 // Persistent decode launches of all sessions on one device run one at a time.
-// Each launch needs every one of its workgroups resident at once (one per CU,
-// cooperative), so two launches on two sessions' streams could each hold part
+// Each launch needs every one of its workgroups resident at once (one per CU),
+// so two launches on two sessions' streams could each hold part
 // of the chip and spin in their bounded waits until both abort.  The device
 // remembers the stream of its last persistent launch; a launch from another
 // session first records an event at the tail of that stream and makes its own
@@ -858,8 +858,18 @@ static int pdec_reset_words(ahip_session* s) {
 // per CU); ALPACA_HIP_DECODE_ITEMS the attention items aimed for;
 // ALPACA_HIP_DECODE_TIMEOUT_US the bound on each wait inside the kernel;
 // ALPACA_HIP_DECODE_ABORT_LAYER (failure-path tests) makes every launch abort
-// at that layer; ALPACA_HIP_DECODE_COOPERATIVE=0 uses ordinary launches (for
-// profilers that cannot follow cooperative ones).
+// at that layer; ALPACA_HIP_DECODE_COOPERATIVE=1 launches it with
+// hipLaunchCooperativeKernel instead of an ordinary launch.
+//
+// Ordinary launches are the default.  What residency needs is that no other
+// long-lived grid holds CUs while a step runs: persistent launches of every
+// session of this process are ordered one after another on the GPU
+// (PdecOrder), every other kernel of the library ends on its own, and every
+// wait inside the persistent kernel is bounded, so a workgroup that cannot get
+// a CU for the whole bound (another process's long grid) ends the launch with
+// AHIP_ERR_COMMAND_FAILED rather than a hang.  A cooperative launch adds the
+// runtime's own occupancy check and exclusion against other processes'
+// cooperative grids, at 12-18 us per token on MI355X (C1 602 against 588 us).
 static int setup_persistent_decode(ahip_session* s) {
     ahip_model* m = s->m;
     const ahip_llama_config& c = m->c;
@@ -981,7 +991,7 @@ static int setup_persistent_decode(ahip_session* s) {
     p.abort_at_layer = env_int("ALPACA_HIP_DECODE_ABORT_LAYER", -1);  // failure-path tests
     s->pdec_params = p;
     s->pdec_clock_khz = clock_khz;
-    s->pdec_coop = env_int("ALPACA_HIP_DECODE_COOPERATIVE", 1);
+    s->pdec_coop = env_int("ALPACA_HIP_DECODE_COOPERATIVE", 0);
     s->pdec_fmt = fmt;
     s->pdec_grid = grid;
     s->pdec_lds = lds;
@@ -1018,13 +1028,11 @@ static int pdec_launch(ahip_session* s, bool logits, bool emitted) {
     }
     hipError_t le = launch_decode_step(s->pdec_fmt, p, s->pdec_grid, s->pdec_lds, s->pdec_coop, s->stream);
     if (le != hipSuccess && s->pdec_coop) {
-        // The runtime refuses cooperative launches in a process while another
-        // process on the device holds its cooperative-launch resource
-        // (hipErrorIllegalState).  The session then launches the same kernel
-        // the ordinary way for the rest of its life: its workgroups (one per
-        // CU) are all resident on a device that is otherwise idle, and every
-        // wait inside the kernel is bounded, so a launch that cannot get the
-        // whole chip aborts with AHIP_ERR_COMMAND_FAILED instead of hanging.
+        // Cooperative launches (ALPACA_HIP_DECODE_COOPERATIVE=1): the runtime
+        // refuses them in a process while another process on the device holds
+        // its cooperative-launch resource (hipErrorIllegalState).  The session
+        // then launches the same kernel the ordinary way, the default mode,
+        // for the rest of its life.
         hipGetLastError();
         s->pdec_coop = 0;
         le = launch_decode_step(s->pdec_fmt, p, s->pdec_grid, s->pdec_lds, 0, s->stream);
@@ -1482,7 +1490,7 @@ extern "C" int ahip_session_forward(ahip_session* s, const int32_t* tokens, int 
     HIP_OR(hipEventRecord(s->ev_begin, s->stream), "hipEventRecord");
     const bool persistent = n == 1 && s->pdec;
     if (persistent) {
-        // one cooperative launch: token in `chain`, position in `dpos`
+        // one persistent launch: token in `chain`, position in `dpos`
         s->tokens_host[1] = s->length;
         HIP_OR(hipMemcpyAsync(s->chain.p, s->tokens_host, 4, hipMemcpyHostToDevice, s->stream), "token upload");
         HIP_OR(hipMemcpyAsync(s->dpos.p, s->tokens_host + 1, 4, hipMemcpyHostToDevice, s->stream), "position upload");

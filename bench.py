@@ -411,7 +411,8 @@ def main() -> int:
     achieved = tok_bytes / avg_launch / 1e9
     traffic, traffic_note = (measured_traffic(os.path.dirname(os.path.abspath(__file__))) if args.config == "C1"
                              else (None, "counters are summarised for C1 only"))
-    roof = {"bound": "hbm", "kernel": "decode_step_kernel (persistent, one cooperative launch per token)",
+    mode = "cooperative" if os.environ.get("ALPACA_HIP_DECODE_COOPERATIVE", "0") not in ("", "0") else "ordinary"
+    roof = {"bound": "hbm", "kernel": f"decode_step_kernel (persistent, one {mode} launch per token)",
             "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 5),
             "traffic": traffic, "traffic_source": traffic_note,

@@ -1,4 +1,4 @@
-"""The persistent single-token decode kernel (one cooperative launch per token).
+"""The persistent single-token decode kernel (one launch per token).
 
 Sessions pick it for single-token forward calls and the greedy chain when the
 model allows it; ALPACA_HIP_PERSISTENT_DECODE=0 (read at session creation)
@@ -157,6 +157,26 @@ def test_persistent_greedy_chain_matches_stepwise_decode(hip_ctx):
     d.forward(prompt)
     fed = d.decode_greedy(first, 500, lambda t: True, depth=2)
     assert fed == 70 and d.length == 100
+
+
+def test_cooperative_launch_mode_matches_default(hip_ctx):
+    """ALPACA_HIP_DECODE_COOPERATIVE=1 (read at session creation) launches the
+    same kernel with hipLaunchCooperativeKernel instead of an ordinary launch:
+    single-token logits and greedy tokens are bit-identical to the default."""
+    spec = synth.TINY
+    model = HIPLlamaModel(hip_ctx, spec.config, built(spec))
+    prompt = synth.prompt_tokens(spec, 30)
+    with env(ALPACA_HIP_DECODE_COOPERATIVE=1):
+        coop = model.make_session(capacity=100)
+    plain = model.make_session(capacity=100)
+    firsts = [int(np.argmax(s.forward(prompt))) for s in (coop, plain)]
+    assert firsts[0] == firsts[1]
+    la, lb = coop.decode(firsts[0]), plain.decode(firsts[0])
+    assert np.array_equal(la, lb)
+    ta, tb = [], []
+    coop.decode_greedy(int(np.argmax(la)), 24, lambda t: ta.append(t) or True)
+    plain.decode_greedy(int(np.argmax(lb)), 24, lambda t: tb.append(t) or True)
+    assert ta == tb and len(ta) == 24
 
 
 def test_persistent_decode_abort_is_reported_and_session_recovers(hip_ctx):
