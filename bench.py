@@ -110,9 +110,11 @@ def prefill_stage_flops(c, T: int) -> dict:
     }
 
 
-def other_config(ctx, spec, ctx_len: int, prefill_tokens: int, steps: int = 64) -> dict:
+def other_config(ctx, spec, ctx_len: int, prefill_tokens: int, steps: int = 64, profile: bool = True) -> dict:
     """Decode at ctx_len and a prefill of prefill_tokens on another BASELINE config
-    (random-init weights of its shape): tok/s and the fraction of the roofline."""
+    (random-init weights of its shape): tok/s and the fraction of the roofline.
+    With profile, one more (profiled, one-stream) prefill gives each GEMM's and
+    the attention's algorithmic TFLOP/s and fraction of the f16 MFMA peak."""
     import numpy as np
 
     from alpaca_amd import synth
@@ -141,14 +143,31 @@ def other_config(ctx, spec, ctx_len: int, prefill_tokens: int, steps: int = 64) 
         p.reset()
     wall = float(np.median(walls))
     # the stage FLOPs are per layer
-    flops = c.layer_count * sum(prefill_stage_flops(c, prefill_tokens).values()) + 2 * c.vocab_size * c.hidden_size
+    fl = prefill_stage_flops(c, prefill_tokens)
+    flops = c.layer_count * sum(fl.values()) + 2 * c.vocab_size * c.hidden_size
+    stages = None
+    if profile:
+        p.profiling_enabled = True
+        p.forward(prompt[:prefill_tokens])
+        prof = p.last_profile
+        p.reset()
+        stages = {}
+        for label, st in prof.items():
+            if label in fl and st.dispatches:
+                avg = st.seconds / st.dispatches
+                stages[label] = {"avg_us": round(avg * 1e6, 2), "TFLOPs": round(fl[label] / avg / 1e12, 1),
+                                 "frac": round(fl[label] / avg / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
     p.close()
     model.close()
     return {"decode_ctx": ctx_len, "decode_tok_s": round(steps / el, 1), "decode_avg_launch_us": round(launch * 1e6, 1),
             "decode_hbm_frac": round(tok_bytes / launch / 1e9 / HBM_PEAK_GBS, 4),
             "prefill_tokens": prefill_tokens, "prefill_tok_s": round(prefill_tokens / wall, 1),
             "prefill_mfma_frac": round(flops / wall / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
-            "prefill_note": "wall clock of forward, GEMMs + causal attention + last-token logits"}
+            "prefill_note": "wall clock of forward, GEMMs + causal attention + last-token logits",
+            "prefill_stages": stages,
+            "prefill_stages_note": ("one profiled one-stream prefill; frac = algorithmic 2*M*N*K (attention: "
+                                    "causal QK^T + PV) per launch / launch time / 2.5 PFLOP/s; the two-term "
+                                    "activations issue twice that MFMA work") if stages else None}
 
 
 def stage_table(profile: dict, units: dict, scale: float, unit: str, per: int = 1) -> dict:
@@ -518,7 +537,7 @@ def main() -> int:
         others = {}
         for key, sp, ctx_len, pre in (("C4 360M-shape Q4_0", synth.C4, 2048, 2048),
                                       ("C5 1.7B-shape Q8_0", synth.C5, 4096, 4096)):
-            others[key] = other_config(ctx, sp, ctx_len, pre)
+            others[key] = other_config(ctx, sp, ctx_len, pre, profile=not args.no_profile)
             log(f"{key}: decode {others[key]['decode_tok_s']} tok/s at ctx {ctx_len} "
                 f"({100 * others[key]['decode_hbm_frac']:.1f}% of HBM), prefill {others[key]['prefill_tok_s']} tok/s")
 
