@@ -939,13 +939,19 @@ static int setup_persistent_decode(ahip_session* s) {
     // The logits phase stages the leading rows of each workgroup's output share
     // in whatever LDS the device leaves beyond the kernel's static arrays
     // (ALPACA_HIP_DECODE_LOGIT_STAGE_ROWS caps the count; 0 streams every row
-    // through registers).
+    // through registers).  The copy's loads sit ahead of the QKV input polls of
+    // the last eight layers in each wave's in-order load queue (C1 0.4 us, C5
+    // 0.9 us more per such layer), so by default rows are staged only where at
+    // least half of a workgroup's share fits: C4 765 against 771 us per step
+    // with all rows staged, C1 even, C5 (a quarter fits) 1,177 against 1,171.
     {
         const size_t stat = decode_static_lds(fmt, hd, c.head_count, c.kv_head_count);
         const size_t limit = (size_t)max_lds > stat ? (size_t)max_lds - stat : 0;
         p.out_lds_off = (int)decode_logits_stage_offset(p, grid);
-        p.out_lds_rows = std::max(0, std::min(env_int("ALPACA_HIP_DECODE_LOGIT_STAGE_ROWS", 1 << 30),
-                                              decode_logits_stage_rows(p, limit)));
+        const int fit = decode_logits_stage_rows(p, limit);
+        p.out_lds_rows = std::max(0, std::min(env_int("ALPACA_HIP_DECODE_LOGIT_STAGE_ROWS",
+                                                      2 * fit >= p.rows_out ? fit : 0),
+                                              fit));
     }
     lds = decode_lds_bytes(p, grid);
     if (decode_kernel_occupancy(fmt, hd, c.head_count, c.kv_head_count, lds, &per_cu) != hipSuccess ||

@@ -276,12 +276,14 @@ def test_persistent_decode_staged_logit_rows(hip_ctx, spec):
     creation, caps how many) and streams the rest through registers.  Both
     paths form a row's sum with the same lane mapping, chunk order and lane
     reduction, so the logits and greedy ids must be bit-identical whatever the
-    split: none staged, one, an odd count, and the default (as many as fit)."""
+    split: none staged, one, an odd count, as many as fit (a cap above the
+    share), and the default (as many as fit where that is at least half the
+    share, else none)."""
     c = spec.config
     model = HIPLlamaModel(hip_ctx, c, built(spec))
     prompt = synth.prompt_tokens(spec, 29)
     runs = {}
-    for cap in ("0", "1", "7", None):
+    for cap in ("0", "1", "7", "100000", None):
         with env(ALPACA_HIP_DECODE_LOGIT_STAGE_ROWS=cap):
             s = model.make_session(capacity=96)
         tok = int(np.argmax(s.forward(prompt)))
