@@ -1,6 +1,6 @@
 """Builds libalpaca_hip.so in-tree with hipcc for gfx950.
 
-Usage: python -m alpaca_amd.build [-j N]
+Usage: python -m alpaca_amd.build [-j N] [--incremental]
 Each source compiles to an object under alpaca_amd/_build/ in parallel, then
 the objects link into alpaca_amd/libalpaca_hip.so.
 """
@@ -47,9 +47,20 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def _compile(item) -> str:
+def _stale(src: str, obj: str) -> bool:
+    """An object is stale when it is older than its source or any header in csrc/."""
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    deps = [os.path.join(CSRC, src)] + [os.path.join(CSRC, h) for h in os.listdir(CSRC) if h.endswith(".h")]
+    return any(os.path.getmtime(d) > t for d in deps)
+
+
+def _compile(item, incremental: bool = False) -> str:
     src, name, defines = item
     obj = os.path.join(BUILD, name + ".o")
+    if incremental and not _stale(src, obj):
+        return obj
     cmd = [hipcc(), *FLAGS, *defines, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -71,13 +82,19 @@ def _code_object() -> str:
     return SHIM_CO
 
 
-def build(jobs: int = 0) -> str:
+def build(jobs: int = 0, incremental: bool = False) -> str:
+    """Compiles every source (incremental: only objects older than their
+    source or a csrc/ header) and links the library."""
     os.makedirs(BUILD, exist_ok=True)
     jobs = jobs or min(8, os.cpu_count() or 1)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        co = ex.submit(_code_object)
-        objs = list(ex.map(_compile, SOURCES))
-        co.result()
+        co = None
+        if not (incremental and os.path.exists(SHIM_CO) and
+                os.path.getmtime(SHIM_CO) > os.path.getmtime(os.path.join(CSRC, SHIM_SRC))):
+            co = ex.submit(_code_object)
+        objs = list(ex.map(lambda it: _compile(it, incremental), SOURCES))
+        if co:
+            co.result()
     tmp = LIB + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -90,6 +107,7 @@ def build(jobs: int = 0) -> str:
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("-j", type=int, default=0)
+    ap.add_argument("--incremental", action="store_true", help="recompile only stale objects")
     a = ap.parse_args()
-    print(build(a.j))
+    print(build(a.j, a.incremental))
     sys.exit(0)

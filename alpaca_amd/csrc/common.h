@@ -367,12 +367,13 @@ hipError_t launch_decode_step(int fmt, const DecodeParams& p, int grid, size_t l
 
 // attention (kernels_attention.hip).  Cache layout [kv_heads][capacity][hd].
 // q rows are [tokens][heads][hd] with row stride ldq (elements).
-// q (and with qlo its second term: two-term Q and P, float32-grade scores and
-// P.V) f16 [tokens][heads*hd]; writes out_f32, or out_f16 (with out_f16_lo the
-// second term when qlo is set).
+// q (and with qlo its second term: two-term Q, float32-grade scores) f16
+// [tokens][heads*hd]; P enters as p_terms f16 terms (0: two with qlo, else
+// one); writes out_f32, or out_f16 (and, when out_f16_lo is set, its second
+// term).
 hipError_t launch_flash_attention(const f16* q, const f16* qlo, int ldq, const f16* kc, const f16* vc, int capacity,
                                   int tokens, int heads, int kv_heads, int hd, int start, float* out_f32, f16* out_f16,
-                                  f16* out_f16_lo, hipStream_t st);
+                                  f16* out_f16_lo, hipStream_t st, int p_terms = 0);
 // Generic online-softmax attention, any hd <= 256, f16 or f32 cache, keys
 // split into `splits` ranges merged by a second kernel when splits > 1.
 int attention_splits(int length, int heads, int tokens);

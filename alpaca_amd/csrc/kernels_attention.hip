@@ -22,9 +22,9 @@
 // to ~2^-22 so that scores and P.V keep float32 accuracy at twice the MFMA
 // work; P enters as P * 2^14, which keeps small probabilities (and the second
 // term) out of the f16 subnormals.  Accumulation and the softmax statistics
-// are float32.  ALPACA_HIP_FLASH_P_TERMS=1 keeps Q two-term but P single-term
-// (faster; measured past the logit bound at the 1.7B shape's 4096-token
-// prompt).
+// are float32.  Q's and P's term counts are chosen independently per launch
+// (PT: two-term P), and the f16 output's second term is written only where the
+// caller asks for it (the next GEMM takes two terms).
 //
 // attn_generic_kernel: one wave per (query, head, key split) with an online
 // softmax in float32 over an f16 or f32 cache; splits are merged by
@@ -48,7 +48,7 @@ struct FlashArgs {
     float scale_log2;
     float* out32;
     f16* out16;
-    f16* out16lo;  // second term of the f16 output (TT)
+    f16* out16lo;  // second term of the f16 output, or null
 };
 
 constexpr int BQ = 64, BKV = 64;
@@ -423,7 +423,7 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
             const float o0 = oacc[d][0] * inv, o1 = oacc[d][1] * inv, o2 = oacc[d][2] * inv, o3 = oacc[d][3] * inv;
             const f16x4 v = {(f16)o0, (f16)o1, (f16)o2, (f16)o3};
             *(f16x4*)(a.out16 + o) = v;
-            if constexpr (TT)
+            if (a.out16lo)
                 *(f16x4*)(a.out16lo + o) = f16x4{(f16)(o0 - (float)v[0]), (f16)(o1 - (float)v[1]),
                                                  (f16)(o2 - (float)v[2]), (f16)(o3 - (float)v[3])};
         } else {
@@ -701,9 +701,8 @@ hipError_t flash_dispatch(const FlashArgs& a, dim3 grid, int hd, bool out16, hip
 
 hipError_t launch_flash_attention(const f16* q, const f16* qlo, int ldq, const f16* kc, const f16* vc, int capacity,
                                   int tokens, int heads, int kv_heads, int hd, int start, float* out_f32, f16* out_f16,
-                                  f16* out_f16_lo, hipStream_t st) {
+                                  f16* out_f16_lo, hipStream_t st, int p_terms) {
     if (tokens <= 0) return hipSuccess;
-    if (qlo && out_f16 && !out_f16_lo) return hipErrorInvalidValue;  // two-term in, two-term out
     FlashArgs a;
     a.q = q;
     a.qlo = qlo;
@@ -720,10 +719,10 @@ hipError_t launch_flash_attention(const f16* q, const f16* qlo, int ldq, const f
     a.out16 = out_f16;
     a.out16lo = out_f16_lo;
     dim3 grid(heads, (tokens + BQ - 1) / BQ);
-    if (!qlo) return flash_dispatch<false, false>(a, grid, hd, out_f16, st);
-    const char* pe = std::getenv("ALPACA_HIP_FLASH_P_TERMS");
-    if (pe && pe[0] == '1') return flash_dispatch<true, false>(a, grid, hd, out_f16, st);
-    return flash_dispatch<true, true>(a, grid, hd, out_f16, st);
+    const bool pt = p_terms ? p_terms == 2 : qlo != nullptr;
+    if (!qlo) return pt ? flash_dispatch<false, true>(a, grid, hd, out_f16, st)
+                        : flash_dispatch<false, false>(a, grid, hd, out_f16, st);
+    return pt ? flash_dispatch<true, true>(a, grid, hd, out_f16, st) : flash_dispatch<true, false>(a, grid, hd, out_f16, st);
 }
 
 // Splits for the generic kernel: decode spreads the context over >= 64-key

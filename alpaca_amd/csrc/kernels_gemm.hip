@@ -248,7 +248,7 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmArgs p) {
                     const float v = (g / (1.0f + __expf(-g))) * u;
                     const f16 hv = (f16)v;
                     p.yh[o] = hv;
-                    if constexpr (TT) p.yhlo[o] = (f16)(v - (float)hv);
+                    if (p.yhlo) p.yhlo[o] = (f16)(v - (float)hv);
                 }
             }
         }
@@ -678,7 +678,7 @@ __device__ __forceinline__ void qkv_rope_epilogue(const GemmArgs& p, const f32x4
         int stride;
         if (region == 0) {
             dst = p.yh + g0 + (lane & 15);
-            if constexpr (TT) dlo = p.yhlo + g0 + (lane & 15);
+            if (p.yhlo) dlo = p.yhlo + g0 + (lane & 15);
             stride = p.ldy;
         } else {
             dst = (region == 1 ? o.kc : o.vc) + ((int64_t)h * o.capacity + o.pos) * hd + d;
@@ -706,7 +706,7 @@ __device__ __forceinline__ void qkv_rope_epilogue(const GemmArgs& p, const f32x4
                     if (FULL || m < M) {
                         const f16 ho = (f16)out;
                         dst[m * stride] = ho;
-                        if (TT && region == 0) dlo[m * stride] = (f16)(out - (float)ho);
+                        if (dlo) dlo[m * stride] = (f16)(out - (float)ho);
                     }
                 }
             }
@@ -990,6 +990,10 @@ __global__ __launch_bounds__(64 * (BM / WM) * (BN / WN) * KS) void dgemm_kernel(
 #pragma unroll
                         for (int r = 0; r < 4; r++) acc[mat][i][j][r] += red[(((mat * TM + i) * TN + j) * 4 + r) * 64 * NW];
         }
+        // The RoPE epilogue's table copy writes smem from offset 0, which can
+        // reach into `red` (single-term stages at head dim 128 are smaller than
+        // the table): every wave of the first set must be done reading first.
+        if constexpr (MODE == GEMM_QKV_ROPE && kRope > kStages) __syncthreads();
     }
     if constexpr (MODE == GEMM_QKV_ROPE) {
         // (every wave joins the epilogue's table copy and barrier; only the
@@ -1024,7 +1028,7 @@ __global__ __launch_bounds__(64 * (BM / WM) * (BN / WN) * KS) void dgemm_kernel(
                     const float v = (g / (1.0f + __expf(-g))) * u;
                     const f16 hv = (f16)v;
                     p.yh[o] = hv;
-                    if constexpr (TT) p.yhlo[o] = (f16)(v - (float)hv);
+                    if (p.yhlo) p.yhlo[o] = (f16)(v - (float)hv);
                 }
             }
         }
@@ -1206,7 +1210,6 @@ bool prefill_split_pays(int m, int n) {
 hipError_t launch_gemm_mfma(const f16* x, const f16* xlo, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up,
                             float* y, f16* yh, f16* yhlo, int ldy, int mode, hipStream_t st) {
     if (m <= 0) return hipSuccess;
-    if (mode == GEMM_SWIGLU && xlo && !yhlo) return hipErrorInvalidValue;  // two-term in, two-term out
     // The DMA kernel needs 64-wide K stages, 16-byte aligned activation rows and,
     // for quantised weights, the stage-major scales.
     const bool quant = w.dtype != DT_F16;
@@ -1240,7 +1243,7 @@ hipError_t launch_gemm_qkv_rope(const f16* x, const f16* xlo, int ldx, int m, co
     if (w.cols % DBK || ldx % 8 || ((uintptr_t)x & 15) || ((uintptr_t)xlo & 15) || (quant && !w.s2) ||
         !dma_offsets_fit(m, ldx, w) || o.hd % 16 ||
         o.hd > 128 || o.heads <= 0 || o.kv_heads <= 0 || w.rows != (o.heads + 2 * o.kv_heads) * o.hd || !o.rope ||
-        !o.qh || !o.kc || !o.vc || (xlo && !o.qlo))
+        !o.qh || !o.kc || !o.vc)
         return hipErrorNotSupported;
     GemmArgs a;
     a.x = x;

@@ -300,6 +300,23 @@ static int env_int(const char* name, int dflt) {
     return std::atoi(v);
 }
 
+// Operands of the two-term fast prefill that carry the second f16 term
+// (lo = f16(x - f16(x))): the inputs of the QKV, Wo, gate/up and down GEMMs,
+// and attention's Q and P.  An operand without it enters its MFMAs as one f16
+// term (half the MFMA work and, for the GEMM inputs, half the activation
+// bytes), and its producer writes no second plane.
+enum : int { kLoQkv = 1, kLoWo = 2, kLoGateUp = 4, kLoDown = 8, kLoQ = 16, kLoP = 32, kLoAll = 63 };
+
+// The second-term operands of a model's two-term prefill.  ALPACA_HIP_LO_TERMS
+// (a kLo* bit mask, read at session creation) overrides the choice;
+// ALPACA_HIP_FLASH_P_TERMS=1 takes P single-term.
+static int lo_terms_for(const ahip_llama_config& c) {
+    (void)c;
+    int lo = env_int("ALPACA_HIP_LO_TERMS", kLoAll) & kLoAll;
+    if (env_int("ALPACA_HIP_FLASH_P_TERMS", 2) == 1) lo &= ~kLoP;
+    return lo;
+}
+
 // A weight matrix uploaded in the split quant/scale layout of DevMatrix.
 struct OwnedMatrix {
     DevMatrix m;
@@ -642,6 +659,7 @@ struct ahip_session {
     ahip_model* m = nullptr;
     int capacity = 0, max_batch = 0, kv_f16 = 1, fast = 1;
     int two_term = 1;  // fast prefill with two-term activations (AHIP_GEMM_FAST); 0: one f16 term (FAST_F16)
+    int lo_terms = 0;  // with two_term: which operands carry the second term (kLo* bits)
     int fuse_qkv_rope = 1;  // ALPACA_HIP_FUSE_QKV_ROPE at creation; 0: RoPE + KV append as their own kernel
     // Numerics diagnostics, read at creation: ALPACA_HIP_PREFILL_ATTENTION=generic runs the fast prefill's
     // attention as the float32 kernel the exact prefill uses; ALPACA_HIP_PREFILL_GEMM=f32 its projections as
@@ -1128,6 +1146,7 @@ extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, i
     s->kv_f16 = kv_precision == AHIP_KV_F16;
     s->fast = gemm_precision != AHIP_GEMM_EXACT;
     s->two_term = gemm_precision == AHIP_GEMM_FAST;
+    s->lo_terms = s->two_term ? lo_terms_for(c) : 0;
     s->fuse_qkv_rope = env_int("ALPACA_HIP_FUSE_QKV_ROPE", 1) != 0;
     {
         const char* a = std::getenv("ALPACA_HIP_PREFILL_ATTENTION");
@@ -1286,14 +1305,19 @@ static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, 
     f16* qh = s->qh.as<f16>() + r * QW;
     f16* ctxh = s->ctxh.as<f16>() + r * QW;
     f16* ffnh = s->ffnh.as<f16>() + r * F;
-    // second-term planes of the f16 activation buffers (two-term prefill), after the first planes
-    f16* xhlo = s->two_term ? s->xh.as<f16>() + B * H + r * H : nullptr;
-    f16* qhlo = s->two_term ? s->qh.as<f16>() + B * QW + r * QW : nullptr;
-    f16* ctxhlo = s->two_term ? s->ctxh.as<f16>() + B * QW + r * QW : nullptr;
-    f16* ffnhlo = s->two_term ? s->ffnh.as<f16>() + B * F + r * F : nullptr;
+    // Second-term planes of the f16 activation buffers (two-term prefill),
+    // after the first planes; null where the operand takes one term (the
+    // producer then writes no second term and the consumer reads none).
+    const int lo = s->two_term ? s->lo_terms : 0;
+    f16* xhlo_qkv = lo & kLoQkv ? s->xh.as<f16>() + B * H + r * H : nullptr;
+    f16* xhlo_ffn = lo & kLoGateUp ? s->xh.as<f16>() + B * H + r * H : nullptr;
+    f16* qhlo = lo & kLoQ ? s->qh.as<f16>() + B * QW + r * QW : nullptr;
+    f16* ctxhlo = lo & kLoWo ? s->ctxh.as<f16>() + B * QW + r * QW : nullptr;
+    f16* ffnhlo = lo & kLoDown ? s->ffnh.as<f16>() + B * F + r * F : nullptr;
+    const int p_terms = lo & kLoP ? 2 : 1;
     float* ctx = s->ctx.as<float>() + r * QW;
     s->stage("rmsnorm");
-    LAUNCH(launch_rmsnorm(x, L.attn_norm.as<float>(), nullptr, xh, xhlo, n, H, c.rms_norm_eps, st));
+    LAUNCH(launch_rmsnorm(x, L.attn_norm.as<float>(), nullptr, xh, xhlo_qkv, n, H, c.rms_norm_eps, st));
     s->stage("qkv projections");
     hipError_t fused = hipErrorNotSupported;
     if (flash && s->fuse_qkv_rope) {
@@ -1309,11 +1333,11 @@ static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, 
         o.hd = hd;
         o.pos = pos;
         o.capacity = s->capacity;
-        fused = launch_gemm_qkv_rope(xh, xhlo, H, n, L.pre(L.qkv, L.qkv16), o, st);
+        fused = launch_gemm_qkv_rope(xh, xhlo_qkv, H, n, L.pre(L.qkv, L.qkv16), o, st);
         if (fused != hipErrorNotSupported) LAUNCH(fused);
     }
     if (fused == hipErrorNotSupported) {
-        LAUNCH(launch_gemm_mfma(xh, xhlo, H, n, L.pre(L.qkv, L.qkv16), nullptr, qkv, nullptr, nullptr, LDQKV,
+        LAUNCH(launch_gemm_mfma(xh, xhlo_qkv, H, n, L.pre(L.qkv, L.qkv16), nullptr, qkv, nullptr, nullptr, LDQKV,
                                 GEMM_STORE, st));
         s->stage("rope + kv store");
         LAUNCH(launch_rope_store(qkv, LDQKV, n, c.head_count, c.kv_head_count, hd, pos, rope, 1, flash ? 0 : 1,
@@ -1324,7 +1348,7 @@ static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, 
     s->stage("attention");
     if (flash) {
         LAUNCH(launch_flash_attention(qh, qhlo, QW, (const f16*)kc, (const f16*)vc, s->capacity, n, c.head_count,
-                                      c.kv_head_count, hd, pos, nullptr, ctxh, ctxhlo, st));
+                                      c.kv_head_count, hd, pos, nullptr, ctxh, ctxhlo, st, p_terms));
     } else {
         LAUNCH(launch_attention_generic(qkv, LDQKV, kc, vc, s->kv_f16, s->capacity, n, c.head_count, c.kv_head_count,
                                         hd, pos, 1, nullptr, ctx, st));
@@ -1333,9 +1357,9 @@ static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, 
     s->stage("attn out projection (+residual)");
     LAUNCH(launch_gemm_mfma(ctxh, ctxhlo, QW, n, L.pre(L.wo, L.wo16), nullptr, x, nullptr, nullptr, H, GEMM_ACC, st));
     s->stage("rmsnorm");
-    LAUNCH(launch_rmsnorm(x, L.ffn_norm.as<float>(), nullptr, xh, xhlo, n, H, c.rms_norm_eps, st));
+    LAUNCH(launch_rmsnorm(x, L.ffn_norm.as<float>(), nullptr, xh, xhlo_ffn, n, H, c.rms_norm_eps, st));
     s->stage("ffn gate+up+silu");
-    LAUNCH(launch_gemm_mfma(xh, xhlo, H, n, L.pre(L.gate, L.gate16), &L.pre(L.up, L.up16), nullptr, ffnh, ffnhlo, F,
+    LAUNCH(launch_gemm_mfma(xh, xhlo_ffn, H, n, L.pre(L.gate, L.gate16), &L.pre(L.up, L.up16), nullptr, ffnh, ffnhlo, F,
                             GEMM_SWIGLU, st));
     s->stage("ffn down (+residual)");
     LAUNCH(launch_gemm_mfma(ffnh, ffnhlo, F, n, L.pre(L.down, L.down16), nullptr, x, nullptr, nullptr, H, GEMM_ACC,
@@ -1354,9 +1378,12 @@ static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, 
 // 702k / 726k / 795k -> 720k / 857k / 885k tok/s, C4 at 1,536 / 2,048 tokens
 // 343k / 389k -> 365k / 417k; below 1,536 tokens the split lost 5-7% at every
 // shape, and at the 1.7B shape, whose grids fill the device, it lost 3-6%.
-// Each row goes through the same kernels; only the flash kernel may pick its
-// other key-range split for the smaller grid of a half (a different float32
-// summation order: logits within 1e-5 of the peak).
+// Each row goes through the same arithmetic, but a half's smaller grids may
+// take other tiles than the whole chunk's: the GEMM's two-K-set 64x64 tiles
+// (where a half's grid is at most one tile per CU) and the flash kernel's
+// other key-range split both change the float32 summation order, so the
+// halves agree with one stream to rounding (logits within 1e-5 of the peak),
+// not bit for bit.
 // ALPACA_HIP_PREFILL_STREAMS=1 (read per call) keeps one stream.
 
 static int encode_split_prefill(ahip_session* s, const int32_t* dtok, int n, int pos, bool logits, bool flash,
@@ -1379,25 +1406,37 @@ static int encode_split_prefill(ahip_session* s, const int32_t* dtok, int n, int
     r[parts] = n;
     HIP_OR(hipEventRecord(s->part_start, s->stream), "hipEventRecord");
     float* x = s->x.as<float>();
-    for (int k = 0; k < parts; k++) {
-        hipStream_t st = s->part_stream[k];
-        if (k) HIP_OR(hipStreamWaitEvent(st, s->part_start, 0), "hipStreamWaitEvent");
-        LAUNCH(launch_embed(dtok + r[k], r[k + 1] - r[k], m->embed.m, x + (int64_t)r[k] * H, st));
-    }
-    for (int li = 0; li < c.layer_count; li++)
-        for (int k = 0; k < parts; k++)
-            if (int rc = encode_mfma_layer(s, li, r[k], r[k + 1] - r[k], pos + r[k], flash, s->part_stream[k],
-                                           k + 1 < parts ? s->part_qkv[k] : nullptr, s->part_qkv, k))
-                return rc;
-    hipStream_t last = s->part_stream[parts - 1];
-    if (logits)
-        LAUNCH(launch_gemv(m->out_matrix(), nullptr, x + (int64_t)(n - 1) * H, m->output_norm.as<float>(),
-                           c.rms_norm_eps, s->logits.as<float>(), GEMV_STORE, last));
-    for (int k = 1; k < parts; k++) {
+    int joined = 1;  // parts whose stream has waited on part_start (the session stream's own part needs none)
+    auto body = [&]() -> int {
+        for (int k = 0; k < parts; k++) {
+            hipStream_t st = s->part_stream[k];
+            if (k) {
+                HIP_OR(hipStreamWaitEvent(st, s->part_start, 0), "hipStreamWaitEvent");
+                joined = k + 1;
+            }
+            LAUNCH(launch_embed(dtok + r[k], r[k + 1] - r[k], m->embed.m, x + (int64_t)r[k] * H, st));
+        }
+        for (int li = 0; li < c.layer_count; li++)
+            for (int k = 0; k < parts; k++)
+                if (int rc = encode_mfma_layer(s, li, r[k], r[k + 1] - r[k], pos + r[k], flash, s->part_stream[k],
+                                               k + 1 < parts ? s->part_qkv[k] : nullptr, s->part_qkv, k))
+                    return rc;
+        if (logits)
+            LAUNCH(launch_gemv(m->out_matrix(), nullptr, x + (int64_t)(n - 1) * H, m->output_norm.as<float>(),
+                               c.rms_norm_eps, s->logits.as<float>(), GEMV_STORE, s->part_stream[parts - 1]));
+        return AHIP_OK;
+    };
+    const int rc = body();
+    // The session stream joins every part stream that took work, also when
+    // encoding failed part way: whatever was queued there reads and writes
+    // the session's activations and KV cache, so later calls on the session
+    // (and its teardown, which synchronises the session stream) must come
+    // after it.
+    for (int k = 1; k < joined; k++) {
         HIP_OR(hipEventRecord(s->part_done[k], s->part_stream[k]), "hipEventRecord");
         HIP_OR(hipStreamWaitEvent(s->stream, s->part_done[k], 0), "hipStreamWaitEvent");
     }
-    return AHIP_OK;
+    return rc;
 }
 
 static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bool logits,
@@ -1422,10 +1461,7 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
     LAUNCH(launch_embed(dtok, n, m->embed.m, x, st));
     // Second-term planes of the f16 activation buffers (two-term prefill), after the first planes.
     const int64_t B = s->max_batch;
-    f16* xhlo = s->two_term ? s->xh.as<f16>() + B * H : nullptr;
-    f16* qhlo = s->two_term ? s->qh.as<f16>() + B * QW : nullptr;
-    f16* ctxhlo = s->two_term ? s->ctxh.as<f16>() + B * QW : nullptr;
-    f16* ffnhlo = s->two_term ? s->ffnh.as<f16>() + B * F : nullptr;
+    f16* qhlo = s->two_term && (s->lo_terms & kLoQ) ? s->qh.as<f16>() + B * QW : nullptr;
     for (int li = 0; li < c.layer_count; li++) {
         ahip_model::Layer& L = *m->layers[li];
         void* kc = s->kc[li]->p;
@@ -1448,7 +1484,7 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
             if (flash) {
                 LAUNCH(launch_flash_attention(s->qh.as<f16>(), qhlo, QW, (const f16*)kc, (const f16*)vc, s->capacity,
                                               n, c.head_count, c.kv_head_count, hd, pos, s->ctx.as<float>(), nullptr,
-                                              nullptr, st));
+                                              nullptr, st, s->two_term && (s->lo_terms & kLoP) ? 2 : 1));
             } else {
                 LAUNCH(launch_attention_generic(qkv, LDQKV, kc, vc, s->kv_f16, s->capacity, n, c.head_count,
                                                 c.kv_head_count, hd, pos, 1, nullptr, s->ctx.as<float>(), st));

@@ -21,7 +21,9 @@ exactly as bench.py times them, with full logit vectors (float32):
   * C1L: C1 decode at context 2048: a 2045-token prompt, then 131 greedy
     steps (3 that bring the context to 2048, then 128 timed ones);
   * C4W: C4's 2048-token prompt, then 256 greedy steps (context 2048-2303);
-  * C5W: C5's 4096-token prompt, then 256 greedy steps (context 4096-4351).
+  * C5W: C5's 4096-token prompt, then 256 greedy steps (context 4096-4351);
+  * C1P: C1's 4096-token prompt (the benched prefill, split over two streams
+    on the GPU), then 8 greedy steps.
 
 Per case: the greedy ids and top-2 margins of every step, and the full
 logits of the prefill (step 0) and of greedy steps 1-8 and the last one.
@@ -128,7 +130,8 @@ def c3_case() -> dict:
 
 
 # (key, spec, prompt length, greedy steps): the decode workloads bench.py times
-WORKLOAD_CASES = [("C1L", synth.C1, 2045, 131), ("C4W", synth.C4, 2048, 256), ("C5W", synth.C5, 4096, 256)]
+WORKLOAD_CASES = [("C1L", synth.C1, 2045, 131), ("C4W", synth.C4, 2048, 256), ("C5W", synth.C5, 4096, 256),
+                  ("C1P", synth.C1, 4096, 8)]
 FULL_LOGIT_STEPS = 8  # greedy steps 1..8 (and the last) keep their full logits
 
 

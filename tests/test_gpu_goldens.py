@@ -83,19 +83,29 @@ def test_model_matches_golden(hip_ctx, key, spec):
 
 @pytest.mark.parametrize("idx", [0, 1])
 def test_c2_gemm_matches_golden(hip_ops, idx):
+    """C2's isolated Q8_0 GEMMs: the exact GEMM bit for bit (SHA-256 of the
+    golden output); the default fast GEMM (two f16 activation terms) within the
+    exact GEMM's tolerance 2e-4 + 1e-4 |y| on every element of the output,
+    against the oracle's output recomputed here and itself checked against the
+    golden sample; the single-term fast-f16 GEMM within the reference's
+    fast-path bound 2^-10 sum |x w| + 1e-5 (KernelTests.swift:179-217)."""
     case = G["c2"][idx]
-    x, w = synth.c2_gemm_case(case["n"], case["k"])
+    m, n, k = case["m"], case["n"], case["k"]
+    x, w = synth.c2_gemm_case(n, k)
     assert sha(hip_ops.linear(x, w, "exact")) == case["y_sha256"]
-    fast = hip_ops.linear(x, w, "fast").ravel()[::case["y_sample_stride"]].astype(np.float64)
-    ref = np.array(case["y_sample"])
-    # analytic bound at the sampled elements (flat index -> row m, column n)
-    idx_flat = np.arange(0, case["m"] * case["n"], case["y_sample_stride"])
-    wd = np.abs(orc.dequantize(w.dtype, w.data, case["n"] * case["k"]).reshape(case["n"], case["k"]).astype(np.float64))
-    ax = np.abs(x.astype(np.float64))
-    bound = np.einsum("ik,ik->i", ax[idx_flat // case["n"]], wd[idx_flat % case["n"]]) / 1024 + 1e-5
-    err = np.abs(fast - ref)
-    print(f"[metrics] C2 {case['n']}x{case['k']} fast: worst error / bound {float((err / bound).max()):.3f}")
-    assert (err <= bound).all()
+    cpu32 = orc.linear(x, w.dtype, w.data, n)
+    assert sha(cpu32) == case["y_sha256"]  # the oracle reproduces the golden bits
+    cpu = cpu32.astype(np.float64)
+    err = np.abs(hip_ops.linear(x, w, "fast").astype(np.float64) - cpu)
+    tol = 2e-4 + 1e-4 * np.abs(cpu)
+    print(f"[metrics] C2 {m}x{n}x{k} fast (two terms): max |err| {err.max():.3e}, worst error / "
+          f"(2e-4 + 1e-4|y|) {float((err / tol).max()):.4f} over all {err.size} outputs")
+    assert (err <= tol).all()
+    wd = np.abs(orc.dequantize(w.dtype, w.data, n * k).reshape(n, k).astype(np.float64))
+    bound = np.abs(x.astype(np.float64)) @ wd.T / 1024 + 1e-5
+    err1 = np.abs(hip_ops.linear(x, w, "fast-f16").astype(np.float64) - cpu)
+    print(f"[metrics] C2 {m}x{n}x{k} fast-f16: worst error / analytic bound {float((err1 / bound).max()):.3f}")
+    assert (err1 <= bound).all()
 
 
 def test_c3_attention_matches_golden(hip_ops):

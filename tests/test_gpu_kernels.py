@@ -107,10 +107,11 @@ def test_gemm_tile_families_agree_at_large_grids(hip_ops, name, dt):
     default takes 128x128 tiles.  Every tile family (ALPACA_HIP_GEMM_TILE,
     read per launch) accumulates each output over the same 32-weight blocks in
     the same order, so the store, residual and SwiGLU epilogues must agree bit
-    for bit across 64x64, 128x64, 128x128, 128x256 and 256-row tiles.  The default is held to
-    the analytic fast-GEMM bound (KernelTests.swift:179-217), and one-hot
-    activation rows pin the weight path of every tile (Y[m] = W[:, m mod K]
-    exactly)."""
+    for bit across 64x64, 128x64, 128x128, 128x256 and 256-row tiles.  The
+    default (two f16 activation terms) is held to the exact GEMM's tolerance
+    2e-4 + 1e-4 |y| against the oracle on every output of the three
+    epilogues, and one-hot activation rows pin the weight path of every tile
+    (Y[m] = W[:, m mod K] exactly)."""
     m, k, n = 4096, 576, 1600
     w = encode(rand((n, k), 4242 + dt, 0.3), dt)
     wu = encode(rand((n, k), 4343 + dt, 0.3), dt)
@@ -140,11 +141,16 @@ def test_gemm_tile_families_agree_at_large_grids(hip_ops, name, dt):
     for i, what in enumerate(("store", "residual", "swiglu")):
         a, b = k2[i], outs[None][i]
         assert np.abs(a - b).max() <= 1e-5 * max(1.0, float(np.abs(b).max())), f"{name} {what}: two K sets"
-    cpu = orc.linear(x, dt, w.data, n).astype(np.float64)
-    bound = np.abs(x.astype(np.float64)) @ np.abs(deq.astype(np.float64)).T / 1024 + 1e-5
-    err = np.abs(outs[None][0].astype(np.float64) - cpu)
-    print(f"[metrics] fast GEMM {name} M={m} K={k} N={n}: worst error / bound = {(err / bound).max():.3f}")
-    assert (err <= bound).all()
+    y = orc.linear(x, dt, w.data, n)
+    u = orc.linear(x, dt, wu.data, n)
+    cpu = {"store": y, "residual": orc.add(res, y), "swiglu": orc.mul(orc.silu(y), u)}
+    for i, what in enumerate(("store", "residual", "swiglu")):
+        e = cpu[what].astype(np.float64)
+        err = np.abs(outs[None][i].astype(np.float64) - e)
+        tol = 2e-4 + 1e-4 * np.abs(e)
+        print(f"[metrics] fast GEMM {name} {what} M={m} K={k} N={n}: max |err| {err.max():.3e}, "
+              f"worst error / (2e-4 + 1e-4|y|) = {(err / tol).max():.4f}")
+        assert (err <= tol).all(), f"{name} {what}: worst error / tolerance {(err / tol).max():.3f}"
 
 
 def test_fused_gate_up_silu(hip_ops):  # KernelTests.swift:219-244

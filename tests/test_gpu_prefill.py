@@ -84,6 +84,35 @@ def test_fused_qkv_rope_with_large_tiles(hip_ctx):
         assert np.array_equal(t, a), f"tile {tile}: prefill logits differ: max |d| {np.abs(t - a).max():.3e}"
 
 
+HD128_1K = replace(synth.TINY, config=replace(synth.TINY.config, head_count=4, kv_head_count=1, head_dim=128,
+                                              context_length=1100), name="tiny-hd128-g4-1k")
+
+
+@pytest.mark.parametrize("prec", ["fast", "fast-f16"])
+@pytest.mark.parametrize("spec", [HD128_1K, C4_LONG], ids=lambda s: s.name)
+def test_fused_qkv_rope_under_each_forced_tile(hip_ctx, spec, prec):
+    """Fused and unfused sessions agree bit for bit under every tile family
+    forced alike for both, including the two-K-set 64x64 tile, whose RoPE
+    table copy (32 KB at head dim 128) is larger than one K set's
+    single-term stage buffers and so overlaps the buffer through which the
+    second set hands its accumulators to the first."""
+    model = HIPLlamaModel(hip_ctx, spec.config, built(spec))
+    prompt = synth.prompt_tokens(spec, 1024)
+    with env(ALPACA_HIP_FUSE_QKV_ROPE=0):
+        ref = model.make_session(capacity=1100, max_batch=1024, gemm_precision=prec)
+    fused = model.make_session(capacity=1100, max_batch=1024, gemm_precision=prec)
+    for tile in ("64x64", "64x64k2", "128x64", "128x128"):
+        fused.reset()
+        ref.reset()
+        with env(ALPACA_HIP_GEMM_TILE=tile, ALPACA_HIP_PREFILL_STREAMS=1):
+            a, b = fused.forward(prompt), ref.forward(prompt)
+        assert np.array_equal(a, b), f"{spec.name} {prec} tile {tile}: max |d| {np.abs(a - b).max():.3e}"
+        tok = int(np.argmax(a))
+        x, y = fused.decode(tok), ref.decode(tok)
+        assert np.array_equal(x, y), f"{spec.name} {prec} tile {tile}: decode max |d| {np.abs(x - y).max():.3e}"
+    model.close()
+
+
 # ------------------------------------------------------------------ two-stream prefill
 
 C1_2L = replace(synth.C1, config=replace(synth.C1.config, layer_count=2, context_length=4352), name="c1-shape-2l")
@@ -97,9 +126,10 @@ def test_two_stream_prefill_matches_one_stream(hip_ctx, spec, prec):
     most two rounds of 128x64 tiles runs as two halves on two
     streams (the second half's attention of each layer waits for the first
     half's K/V rows).  Every row goes through the same arithmetic as in one
-    stream (a half's smaller grids may take other GEMM tiles, which agree bit
-    for bit; the flash kernel may choose its other key-range split, a
-    different float32 summation order), so the logits
+    stream, but a half's smaller grids may take other tiles: the GEMM's
+    two-K-set 64x64 tiles and the flash kernel's other key-range split each
+    change the float32 summation order, so the halves agree to rounding, not
+    bit for bit.  So the logits
     and the decode steps that read the cache must agree with
     ALPACA_HIP_PREFILL_STREAMS=1 (read per call) to 1e-5 of the logit peak: a
     1600-token chunk (halves of 768 and 832 rows, just past the 1,536-token

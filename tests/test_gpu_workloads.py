@@ -5,16 +5,25 @@ written by tests/golden/make_synthetic_goldens.py --workloads):
   * C1L: C1 (135M-shape Q8_0) prefilled with 2045 tokens, then 131 greedy
     steps: the bench's headline decode at context 2048 onward;
   * C4W: C4 (360M-shape Q4_0), 2048-token prompt, 256 greedy steps;
-  * C5W: C5 (1.7B-shape Q8_0), 4096-token prompt, 256 greedy steps.
+  * C5W: C5 (1.7B-shape Q8_0), 4096-token prompt, 256 greedy steps;
+  * C1P: C1 with the benched 4096-token prompt (two streams on the GPU),
+    then 8 greedy steps.
 
 Each runs in the default configuration the bench uses (fast f16-MFMA
 prefill in one 4096-row chunk with two-term activations, f16 KV cache,
-persistent decode kernel) and is held to the BASELINE north star: every one of the 49,152 logits within
-2e-3 absolute + 1e-3 relative of the oracle's (an f16-rounded cache, as the
-GPU keeps) at the prefill and at greedy steps 1-8 and the last, and greedy
-ids identical at every step.  A greedy id may differ only where the oracle's
-top-2 margin is below twice the logit bound (the two candidates are then
-within the tolerance of each other); the comparison stops there and says so.
+persistent decode kernel) and is held to the BASELINE north star: every one
+of the 49,152 logits within 2e-3 absolute + 1e-3 relative of the oracle's
+(an f16-rounded cache, as the GPU keeps) at the prefill, at greedy steps 1-8
+and at the last step, and the greedy id of every step compared with the
+oracle's.  Steps 1-8 and the last run through decode() with the oracle's id
+fed; the steps between run through the device-resident greedy chain (the
+benched path).  When the chain's id differs from the oracle's, the chain is
+stopped there (emit returns 0) and restarted from the oracle's id, so every
+step is compared whatever happens before it (the reference's real-model
+tests use the same top-2 margin rule, CPURealModelTests.swift:35-39).  A
+differing id (a "flip") is accepted only where the oracle's top-2 margin is
+below twice the largest max-abs logit error measured on the checked steps:
+the two candidates are then closer than the measured error can separate.
 """
 import json
 import os
@@ -29,7 +38,7 @@ from tests.helpers import assert_close, metrics
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "workload_goldens.npz")
-SPECS = {"C1L": synth.C1, "C4W": synth.C4, "C5W": synth.C5}
+SPECS = {"C1L": synth.C1, "C4W": synth.C4, "C5W": synth.C5, "C1P": synth.C1}
 ATOL, RTOL = 2e-3, 1e-3
 
 
@@ -41,12 +50,6 @@ def load(key):
                 json.loads(str(z[key + "_meta"])))
 
 
-def near_tie(margin: float, top: float) -> bool:
-    """Two candidates whose oracle logits are closer than twice the per-logit
-    bound may legitimately swap under it."""
-    return margin < 2 * (ATOL + RTOL * abs(top))
-
-
 @pytest.mark.parametrize("key", sorted(SPECS))
 def test_workload_matches_oracle_logits(hip_ctx, key):
     g, meta = load(key)
@@ -54,48 +57,59 @@ def test_workload_matches_oracle_logits(hip_ctx, key):
     n, steps = meta["prompt_len"], meta["greedy_steps"]
     ids, margins = g["ids"].tolist(), g["margins"].tolist()
     kept = dict(zip(g["logit_steps"].tolist(), g["logits"]))
-    peak = max(float(np.abs(v).max()) for v in kept.values())  # bounds the top logit of unkept steps
     model = HIPLlamaModel(hip_ctx, spec.config, synth.build_weights(spec))
     s = model.make_session(capacity=n + steps + 16, max_batch=4096)
     prompt = synth.prompt_tokens(spec, n)
-    worst = {}
+    worst, ratio = {}, {}  # per checked step: max |d|, max |d| / (atol + rtol |e|)
+    flips = []  # (step, oracle margin, GPU id)
+    compared = set()
 
     def check(step, logits):
         e = kept[step]
         m = assert_close(logits, e, ATOL, RTOL, f"{key} step {step}")
         worst[step] = m["max_abs"]
+        ratio[step] = float((np.abs(logits.astype(np.float64) - e) / (ATOL + RTOL * np.abs(e.astype(np.float64)))).max())
         got = int(np.argmax(logits))
         if got != ids[step]:
-            assert near_tie(margins[step], float(e[ids[step]])), \
-                f"{key} step {step}: greedy {got} != oracle {ids[step]} (margin {margins[step]:.3e})"
-            return False
-        return True
+            flips.append((step, margins[step], got))
+        compared.add(step)
 
-    ok = check(0, s.forward(prompt))
+    check(0, s.forward(prompt))
     last_direct = max(k for k in kept if k <= 8)
-    step = 1
-    while ok and step <= last_direct:
-        ok = check(step, s.decode(ids[step - 1]))
-        step += 1
-    # the rest through the device-resident greedy chain (the benched path), then
-    # the last step through decode for its logits
-    if ok and step < steps:
+    for step in range(1, last_direct + 1):
+        check(step, s.decode(ids[step - 1]))  # the oracle's id is fed whatever the GPU chose
+    # steps last_direct+1 .. steps-1 through the greedy chain, restarted from
+    # the oracle's id after any flip; the last step through decode for its logits
+    j = last_direct + 1
+    chain_runs = 0
+    while j < steps:
         got = []
-        s.decode_greedy(ids[step - 1], steps - step, lambda t: got.append(t) or True)
+
+        def emit(t, j=j):
+            got.append(t)
+            return t == ids[j + len(got) - 1]
+
+        fed = s.decode_greedy(ids[j - 1], steps - j, emit)
+        chain_runs += 1
+        assert fed == len(got) and got, f"{key}: chain from step {j} fed {fed}, emitted {len(got)}"
         for k, t in enumerate(got):
-            j = step + k
-            if t != ids[j]:
-                assert near_tie(margins[j], peak), \
-                    f"{key} greedy step {j}: {t} != oracle {ids[j]} (margin {margins[j]:.3e})"
-                print(f"[metrics] {key}: greedy ids identical through step {j - 1}; step {j} is a near tie "
-                      f"(margin {margins[j]:.3e}), comparison stops there")
-                ok = False
-                break
-        step = steps
-    if ok and steps in kept:
+            compared.add(j + k)
+            if t != ids[j + k]:
+                assert k == len(got) - 1, f"{key}: the chain went on past a flip at step {j + k}"
+                flips.append((j + k, margins[j + k], t))
+        j += len(got)
+    if steps > last_direct:
         check(steps, s.decode(ids[steps - 1]))
-    print(f"[metrics] {key}: worst max-abs per checked step {dict((k, f'{v:.2e}') for k, v in worst.items())}; "
-          f"logit peak {peak:.3f}; min top-2 margin {min(margins):.3e}")
+    assert s.length == n + steps
+    assert compared == set(range(steps + 1)), f"{key}: steps not compared {sorted(set(range(steps + 1)) - compared)}"
+    err = max(worst.values())
+    print(f"[metrics] {key}: {len(compared)} steps compared (prefill, {last_direct} direct, {chain_runs} chain "
+          f"run(s), last); flips {[(st, f'{mg:.2e}') for st, mg, _ in flips]}; largest max-abs {err:.3e}; "
+          f"worst/bound per checked step {dict((k, round(v, 4)) for k, v in ratio.items())}; "
+          f"min top-2 margin {min(margins):.3e}")
+    for st, mg, t in flips:
+        assert mg < 2 * err, (f"{key} step {st}: greedy {t} != oracle {ids[st]} with top-2 margin {mg:.3e}, "
+                              f"not below twice the measured max-abs error {err:.3e}")
     s.close()
     model.close()
 
