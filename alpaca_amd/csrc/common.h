@@ -218,8 +218,9 @@ hipError_t launch_silu_mul(const float* g, const float* u, float* out, int64_t n
 // f16 outputs with a second-term pointer (lo) write hi = f16(v) and, when lo is
 // set, lo = f16(v - hi): the two-term activations of the MFMA prefill.
 hipError_t launch_f32_to_f16(const float* x, f16* out, f16* out_lo, int64_t n, hipStream_t st);
+// With out_f16_lo, the second term is written for rows >= lo_row0.
 hipError_t launch_rmsnorm(const float* x, const float* w, float* out_f32, f16* out_f16, f16* out_f16_lo, int rows,
-                          int dim, float eps, hipStream_t st);
+                          int dim, float eps, hipStream_t st, int lo_row0 = 0);
 hipError_t launch_embed(const int32_t* tokens, int count, const DevMatrix& table, float* out, hipStream_t st);
 hipError_t launch_dequant(const DevMatrix& m, float* out, hipStream_t st);
 // f16 copy of a matrix (the prefill weight cache): f16(d*q) per weight, cols % 8 == 0.
@@ -271,12 +272,16 @@ hipError_t launch_gemv(const DevMatrix& w, const DevMatrix* w_up, const float* x
 // prefill GEMM (kernels_gemm.hip)
 enum { GEMM_STORE = 0, GEMM_ACC = 1, GEMM_SWIGLU = 2, GEMM_QKV_ROPE = 3 };
 // fast: x f16 [m][k] (row stride ldx); MFMA f16 with f32 accumulate.  With
-// xlo (the activations' second term, same layout) the activations enter as
-// x + xlo (two-term: float32-grade inputs at twice the MFMA work).
+// xlo (the activations' second term, same layout) the tiles holding a row at
+// or past lo_row0 take the activations as x + xlo (two-term: float32-grade
+// inputs at twice the MFMA work), the others x alone; xlo must hold valid
+// second terms for those tiles' rows (a tile's first row is a multiple of its
+// height, at most 256, so rows from (lo_row0 / 256) * 256 on suffice).
 //   STORE/ACC write y f32 (row stride ldy); SWIGLU writes yh f16 (row stride
-//   ldy), and with xlo its second term to yhlo.
+//   ldy), and when yhlo is set its second term for rows >= lo_out_row0.
 hipError_t launch_gemm_mfma(const f16* x, const f16* xlo, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up,
-                            float* y, f16* yh, f16* yhlo, int ldy, int mode, hipStream_t st);
+                            float* y, f16* yh, f16* yhlo, int ldy, int mode, hipStream_t st, int lo_row0 = 0,
+                            int lo_out_row0 = 0);
 // The stacked [q|k|v] projection of m tokens at positions pos.. with the RoPE
 // (interleaved pairs) and KV-cache append in its epilogue: q rotated to qh f16
 // [m][heads*hd], k rotated and v copied to the f16 caches [kv_heads][capacity][hd].
@@ -285,13 +290,16 @@ hipError_t launch_gemm_mfma(const f16* x, const f16* xlo, int ldx, int m, const 
 struct QkvRope {
     const float2* rope = nullptr;  // (cos, sin) [positions][hd/2]
     f16* qh = nullptr;
-    f16* qlo = nullptr;  // q's second term (two-term activations)
+    f16* qlo = nullptr;  // q's second term, written for rows >= lo_out_row0
     f16* kc = nullptr;
     f16* vc = nullptr;
     int heads = 0, kv_heads = 0, hd = 0, pos = 0, capacity = 0;
 };
+// With xlo, the tiles holding a row >= lo_row0 or a column >= lo_col0 take
+// the second term (tiles are 16-column aligned: lo_col0 = heads * hd leaves q
+// one-term before lo_row0 and k, v two-term throughout).
 hipError_t launch_gemm_qkv_rope(const f16* x, const f16* xlo, int ldx, int m, const DevMatrix& w, const QkvRope& o,
-                                hipStream_t st);
+                                hipStream_t st, int lo_row0 = 0, int lo_out_row0 = 0, int lo_col0 = 1 << 30);
 // exact: x f32; float32 FMA in the reference's per-block order.  SWIGLU writes y f32.
 hipError_t launch_gemm_f32(const float* x, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up, float* y,
                            int ldy, int mode, hipStream_t st);
@@ -370,10 +378,11 @@ hipError_t launch_decode_step(int fmt, const DecodeParams& p, int grid, size_t l
 // q (and with qlo its second term: two-term Q, float32-grade scores) f16
 // [tokens][heads*hd]; P enters as p_terms f16 terms (0: two with qlo, else
 // one); writes out_f32, or out_f16 (and, when out_f16_lo is set, its second
-// term).
+// term for rows >= lo_out0).  The second terms of Q and P are taken only in
+// the 64-query blocks holding a row >= lo_q0 (qlo must be valid there).
 hipError_t launch_flash_attention(const f16* q, const f16* qlo, int ldq, const f16* kc, const f16* vc, int capacity,
                                   int tokens, int heads, int kv_heads, int hd, int start, float* out_f32, f16* out_f16,
-                                  f16* out_f16_lo, hipStream_t st, int p_terms = 0);
+                                  f16* out_f16_lo, hipStream_t st, int p_terms = 0, int lo_q0 = 0, int lo_out0 = 0);
 // Generic online-softmax attention, any hd <= 256, f16 or f32 cache, keys
 // split into `splits` ranges merged by a second kernel when splits > 1.
 int attention_splits(int length, int heads, int tokens);

@@ -48,7 +48,10 @@ struct FlashArgs {
     float scale_log2;
     float* out32;
     f16* out16;
-    f16* out16lo;  // second term of the f16 output, or null
+    f16* out16lo;  // second term of the f16 output (rows >= lo_out0), or null
+    // two-term launches: query blocks holding a row >= lo_q0 take the second
+    // terms of Q and P
+    int lo_q0, lo_out0;
 };
 
 constexpr int BQ = 64, BKV = 64;
@@ -117,8 +120,14 @@ __device__ __forceinline__ float vmax3(float a, float b, float c) {
 // the ranges merge at the end.  It costs LDS (32 KB per set: two workgroups
 // per CU with two sets, one with four), so the launcher uses it only when
 // one-set workgroups would not fill the chip.
+template <int HD, int NSET>
+struct FlashLds {
+    // with several sets the pipeline is two stages deep, with one three
+    static constexpr int BYTES = NSET * (NSET > 1 ? 2 : 3) * 2 * (BKV * HD * 2);
+};
+
 template <int HD, int NSET, bool OUT16, bool TT, bool PT>
-__global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
+__device__ __forceinline__ void flash_attn_body(const FlashArgs& a, uint8_t* stage_lds) {
     static_assert(NSET == 1 || ((NSET == 2 || NSET == 4) && HD == 64), "several wave-sets fit LDS at head dim 64 only");
     constexpr int KS = HD / 32, DT = HD / 16;
     constexpr int ROWB = HD * 2;          // bytes per key row
@@ -131,7 +140,7 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
     // swizzled.  With several sets the pipeline is two stages deep (32 KB per
     // set); with one set, three (48 KB, three workgroups per CU).
     constexpr int NSTAGE = NSET > 1 ? 2 : 3;
-    __shared__ __attribute__((aligned(16))) uint8_t stage_lds[NSET * NSTAGE * 2 * TILE];
+    static_assert(FlashLds<HD, NSET>::BYTES == NSET * NSTAGE * 2 * TILE, "stage buffer size");
 
     const int h = blockIdx.x;
     const int qb = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks first
@@ -423,13 +432,27 @@ __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
             const float o0 = oacc[d][0] * inv, o1 = oacc[d][1] * inv, o2 = oacc[d][2] * inv, o3 = oacc[d][3] * inv;
             const f16x4 v = {(f16)o0, (f16)o1, (f16)o2, (f16)o3};
             *(f16x4*)(a.out16 + o) = v;
-            if (a.out16lo)
+            if (a.out16lo && qi >= a.lo_out0)
                 *(f16x4*)(a.out16lo + o) = f16x4{(f16)(o0 - (float)v[0]), (f16)(o1 - (float)v[1]),
                                                  (f16)(o2 - (float)v[2]), (f16)(o3 - (float)v[3])};
         } else {
             *(float4*)(a.out32 + o) = make_float4(oacc[d][0] * inv, oacc[d][1] * inv, oacc[d][2] * inv,
                                                   oacc[d][3] * inv);
         }
+    }
+}
+
+// Query blocks holding a row at or past a.lo_q0 take Q and P as TT / PT
+// terms; the others (of a two-term launch) as one f16 term each.
+template <int HD, int NSET, bool OUT16, bool TT, bool PT>
+__global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t stage_lds[FlashLds<HD, NSET>::BYTES];
+    if constexpr (TT || PT) {
+        const int qb = gridDim.y - 1 - blockIdx.y;
+        if ((qb + 1) * BQ > a.lo_q0) flash_attn_body<HD, NSET, OUT16, TT, PT>(a, stage_lds);
+        else flash_attn_body<HD, NSET, OUT16, false, false>(a, stage_lds);
+    } else {
+        flash_attn_body<HD, NSET, OUT16, false, false>(a, stage_lds);
     }
 }
 
@@ -701,7 +724,7 @@ hipError_t flash_dispatch(const FlashArgs& a, dim3 grid, int hd, bool out16, hip
 
 hipError_t launch_flash_attention(const f16* q, const f16* qlo, int ldq, const f16* kc, const f16* vc, int capacity,
                                   int tokens, int heads, int kv_heads, int hd, int start, float* out_f32, f16* out_f16,
-                                  f16* out_f16_lo, hipStream_t st, int p_terms) {
+                                  f16* out_f16_lo, hipStream_t st, int p_terms, int lo_q0, int lo_out0) {
     if (tokens <= 0) return hipSuccess;
     FlashArgs a;
     a.q = q;
@@ -718,6 +741,8 @@ hipError_t launch_flash_attention(const f16* q, const f16* qlo, int ldq, const f
     a.out32 = out_f32;
     a.out16 = out_f16;
     a.out16lo = out_f16_lo;
+    a.lo_q0 = lo_q0;
+    a.lo_out0 = lo_out0;
     dim3 grid(heads, (tokens + BQ - 1) / BQ);
     const bool pt = p_terms ? p_terms == 2 : qlo != nullptr;
     if (!qlo) return pt ? flash_dispatch<false, true>(a, grid, hd, out_f16, st)

@@ -48,8 +48,12 @@ struct GemmArgs {
     DevMatrix w, u;
     float* y;
     f16* yh;
-    f16* yhlo = nullptr;  // f16 outputs' second term (two-term kernels)
+    f16* yhlo = nullptr;  // f16 outputs' second term, written for rows >= lo_out_row0
     int ldy;
+    // Two-term kernels: tiles holding a row >= lo_row0 or a column >= lo_col0
+    // take the activations' second term, the others one term; the second term
+    // of f16 outputs is written for rows >= lo_out_row0 only.
+    int lo_row0 = 0, lo_out_row0 = 0, lo_col0 = 1 << 30;
     QkvRope qkv;  // GEMM_QKV_ROPE only (yh = qkv.qh, ldy = heads * hd)
 };
 
@@ -126,6 +130,9 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmArgs p) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
     const int nk = (K + BK - 1) / BK;
+    // Tiles before lo_row0 take one term: their second-term rows are not read
+    // (they may hold stale data) and enter as zeros, which add nothing.
+    const bool use_lo = m0 + BM > p.lo_row0;
 
     int4 ra[SA], rl[TT ? SA : 1];
     BUnit<FMT> rb[NB][UB];
@@ -138,7 +145,8 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmArgs p) {
             int4 v = {0, 0, 0, 0}, vl = {0, 0, 0, 0};
             if (m0 + r < M && k0 + c < K) {
                 v = *(const int4*)(p.x + (int64_t)(m0 + r) * p.ldx + k0 + c);
-                if constexpr (TT) vl = *(const int4*)(p.xlo + (int64_t)(m0 + r) * p.ldx + k0 + c);
+                if constexpr (TT)
+                    if (use_lo) vl = *(const int4*)(p.xlo + (int64_t)(m0 + r) * p.ldx + k0 + c);
             }
             ra[i] = v;
             if constexpr (TT) rl[i] = vl;
@@ -248,7 +256,7 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmArgs p) {
                     const float v = (g / (1.0f + __expf(-g))) * u;
                     const f16 hv = (f16)v;
                     p.yh[o] = hv;
-                    if (p.yhlo) p.yhlo[o] = (f16)(v - (float)hv);
+                    if (p.yhlo && m >= p.lo_out_row0) p.yhlo[o] = (f16)(v - (float)hv);
                 }
             }
         }
@@ -450,7 +458,7 @@ hipError_t run_f32(const GemmF32Args& a, int mode, hipStream_t st) {
 // multiple of 64, activation rows not 16-byte aligned).
 static hipError_t launch_gemm_mfma_staged(const f16* x, const f16* xlo, int ldx, int m, const DevMatrix& w,
                                          const DevMatrix* w_up, float* y, f16* yh, f16* yhlo, int ldy, int mode,
-                                         hipStream_t st) {
+                                         hipStream_t st, int lo_row0, int lo_out_row0) {
     if (m <= 0) return hipSuccess;
     GemmArgs a;
     a.x = x;
@@ -463,6 +471,8 @@ static hipError_t launch_gemm_mfma_staged(const f16* x, const f16* xlo, int ldx,
     a.y = y;
     a.yh = yh;
     a.ldy = ldy;
+    a.lo_row0 = lo_row0;
+    a.lo_out_row0 = lo_out_row0;
     switch (w.dtype) {
     case DT_Q8_0: return pick_tile_terms<DT_Q8_0>(a, mode, st);
     case DT_Q4_0: return pick_tile_terms<DT_Q4_0>(a, mode, st);
@@ -706,7 +716,7 @@ __device__ __forceinline__ void qkv_rope_epilogue(const GemmArgs& p, const f32x4
                     if (FULL || m < M) {
                         const f16 ho = (f16)out;
                         dst[m * stride] = ho;
-                        if (dlo) dlo[m * stride] = (f16)(out - (float)ho);
+                        if (dlo && m >= p.lo_out_row0) dlo[m * stride] = (f16)(out - (float)ho);
                     }
                 }
             }
@@ -729,11 +739,18 @@ __device__ __forceinline__ void qkv_rope_epilogue(const GemmArgs& p, const f32x4
 // sequential stage loop per workgroup.  (The split changes the float32
 // summation order of each output, so a KS = 2 tile agrees with the others to
 // rounding, not bit for bit.)
-template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH, bool TT, int KS = 1>
+// TAIL (one-term kernels): the tiles holding rows from p.lo_row0 on (a
+// multiple of BM) make a second pass over K with the activations' second term
+// as A, adding x_lo * W to the accumulators: the two-term result of those
+// rows, in the one-term kernel's LDS footprint and occupancy.  They take the
+// first blockIdx values, one tile per workgroup, so they spread over the
+// XCDs and start before the other tiles (which follow in XCD-major order).
+template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH, bool TT, int KS = 1, bool TAIL = false>
 __global__ __launch_bounds__(64 * (BM / WM) * (BN / WN) * KS) void dgemm_kernel(GemmArgs p) {
+    static_assert(!(TT && TAIL), "the second pass belongs to one-term kernels");
     using G = DGemm<FMT, BM, BN, WM, WN, MODE, TT>;
     using L = DStage<FMT, BM, BN, G::NB, TT>;
-    constexpr int NB = G::NB, TM = G::TM, TN = G::TN, PER = G::PER, NW = G::NW;
+    constexpr int NB = G::NB, TM = G::TM, TN = G::TN, NW = G::NW;
     static_assert(KS == 1 || KS == 2, "one or two K sets");
     // The stage buffers, in one array that the GEMM_QKV_ROPE epilogue reuses
     // for the tile's RoPE rows (BM positions x RH/2 pairs of 8 bytes: 32 KB at
@@ -755,9 +772,26 @@ __global__ __launch_bounds__(64 * (BM / WM) * (BN / WN) * KS) void dgemm_kernel(
     uint8_t* const st2 = st0 + (NSTAGE > 2 ? 2 : 0) * L::BYTES;
 
     const int K = p.w.cols, N = p.w.rows, M = p.M, nb = K >> 5, spitch = stage_scale_pitch(N);
-    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, tiles = tiles_m * tiles_n;
-    const int b = blockIdx.x, xcd = b % 8, q = tiles / 8, rem = tiles % 8;
-    const int t = xcd * q + min(xcd, rem) + b / 8;  // XCD-major tile order (bijective)
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    int main_m = tiles_m, b = blockIdx.x, t = 0;
+    bool tail_tile = false;
+    if constexpr (TAIL) {
+        // blockIdx [0, pad): the tail tiles (grid padded to a multiple of 8
+        // there, so the others keep blockIdx % 8 as their XCD)
+        main_m = min(tiles_m, p.lo_row0 / BM);
+        const int ntail = (tiles_m - main_m) * tiles_n, pad = (ntail + 7) & ~7;
+        if (b < pad) {
+            if (b >= ntail) return;  // padding
+            tail_tile = true;
+            t = main_m * tiles_n + b;
+        } else {
+            b -= pad;
+        }
+    }
+    if (!tail_tile) {
+        const int tiles = main_m * tiles_n, xcd = b % 8, q = tiles / 8, rem = tiles % 8;
+        t = xcd * q + min(xcd, rem) + b / 8;  // XCD-major tile order (bijective)
+    }
     const int m0 = (t / tiles_n) * BM, n0 = (t % tiles_n) * BN;
     const int lane = threadIdx.x & 63;
     const int wave = wave_all % NW;  // within the K set
@@ -799,38 +833,6 @@ __global__ __launch_bounds__(64 * (BM / WM) * (BN / WN) * KS) void dgemm_kernel(
         }
     if constexpr (FMT != DT_F16) soff = (uint32_t)((n0 + wave * (BN / NW) + lane * 4) * 4);
 
-    auto issue = [&](uint32_t sg, int kt) {  // sg: LDS byte address of the stage buffer
-        const int k0 = kt * DBK;
-#pragma unroll
-        for (int i = 0; i < G::A_I; i++) {
-            const int r0 = (i * NW + wave) * 8;
-            dma16s(p.x + k0, aoff[i], sg + r0 * DBK * 2);
-            if constexpr (TT) dma16s(p.xlo + k0, aoff[i], sg + L::A_LO + r0 * DBK * 2);
-        }
-#pragma unroll
-        for (int mat = 0; mat < NB; mat++) {
-            const DevMatrix& w = mat ? p.u : p.w;
-            const uint32_t bq = sg + L::B_OFF + mat * BN * L::BROW;
-#pragma unroll
-            for (int i = 0; i < G::B_I; i++) {
-                if constexpr (FMT == DT_Q8_0) {
-                    dma16s(w.q + k0, boff[mat][i], bq + (i * NW + wave) * 16 * 64);
-                } else if constexpr (FMT == DT_Q4_0) {
-                    if constexpr (G::Q4_16) dma16s(w.q + kt * 32, boff[mat][i], bq + (i * NW + wave) * 32 * 32);
-                    else dma4s(w.q + kt * 32, boff[mat][i], bq + (i * NW + wave) * 8 * 32);
-                } else {
-                    dma16s(w.q + k0 * 2, boff[mat][i], bq + (i * NW + wave) * 8 * 128);
-                }
-            }
-            if constexpr (FMT != DT_F16) {
-                // The tile's BN scale pairs are contiguous in s2: each wave moves
-                // 1/NW of them, 16 bytes (4 rows) per active lane.
-                if (lane < BN / (4 * NW))
-                    dma16s(w.s2 + (int64_t)kt * spitch, soff, sg + L::S_OFF + mat * BN * 4 + wave * (BN / NW) * 4);
-            }
-        }
-    };
-
     f32x4 acc[NB][TM][TN];
 #pragma unroll
     for (int mat = 0; mat < NB; mat++)
@@ -839,132 +841,186 @@ __global__ __launch_bounds__(64 * (BM / WM) * (BN / WN) * KS) void dgemm_kernel(
 #pragma unroll
             for (int j = 0; j < TN; j++) acc[mat][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int jj = lane >> 4;  // which 8 of the fragment's 32 k values this lane holds
-    // Quantised weights, one 32-weight block (kk) of a stage: each MFMA result
-    // is scaled by the block's d before it is accumulated.  The MFMAs of column
-    // j+1 are issued before the scaling of column j, so the VALU work of one
-    // column runs under the MFMAs of the next instead of waiting on them.
-    auto compute_block_quant = [&](const uint8_t* sg, int kk, const f16x8 (&af)[TM], const f16x8 (&al)[TT ? TM : 1]) {
-        // The raw quants of every column are read first; each becomes f16 just
-        // before its MFMAs (8 bytes live per column instead of 16).
-        uint2 raw[NB * TN];
-        float d[NB * TN];
-#pragma unroll
-        for (int c = 0; c < NB * TN; c++) {
-            const int mat = c / TN, j = c % TN;
-            const int r = wn * WN + 16 * j + (lane & 15);
-            const uint8_t* bq = sg + L::B_OFF + mat * BN * L::BROW;
-            if constexpr (FMT == DT_Q8_0) {
-                const int u = 4 * kk + jj;
-                raw[c] = *(const uint2*)(bq + r * 64 + ((u >> 1) ^ swz_q8(r)) * 16 + (u & 1) * 8);
-            } else {
-                raw[c] = *(const uint2*)(bq + r * 32 + (kk ^ swz_q4(r)) * 16 + (jj & 1) * 8);
+    // The K loop, with the activations' second term (T2) or without it.  A
+    // two-term kernel takes the second term only in tiles holding a row at or
+    // past p.lo_row0 (the workgroup's choice, so each loop keeps its own DMA
+    // counts and LDS layout); the other tiles multiply one f16 term.
+    const f16* abase = p.x;  // the A plane of the pass
+    auto kloop = [&](auto tt_c) {
+        constexpr bool T2 = decltype(tt_c)::value;
+        using L2 = DStage<FMT, BM, BN, NB, T2>;
+        constexpr int PER2 = DGemm<FMT, BM, BN, WM, WN, MODE, T2>::PER;
+        auto issue = [&](uint32_t sg, int kt) {  // sg: LDS byte address of the stage buffer
+            const int k0 = kt * DBK;
+    #pragma unroll
+            for (int i = 0; i < G::A_I; i++) {
+                const int r0 = (i * NW + wave) * 8;
+                dma16s(abase + k0, aoff[i], sg + r0 * DBK * 2);
+                if constexpr (T2) dma16s(p.xlo + k0, aoff[i], sg + L2::A_LO + r0 * DBK * 2);
             }
-            d[c] = (float)*(const f16*)(sg + L::S_OFF + mat * BN * 4 + r * 4 + kk * 2);
-        }
-        auto bfrag = [&](int c) {
-            uint32_t o[4];
-            if constexpr (FMT == DT_Q8_0) {
-                int8x4_to_f16(raw[c].x, o[0], o[1]);
-                int8x4_to_f16(raw[c].y, o[2], o[3]);
-            } else {
-                const int sh = (jj >> 1) * 4;
-                nib4_to_f16((raw[c].x >> sh) & 0x0F0F0F0Fu, o[0], o[1]);
-                nib4_to_f16((raw[c].y >> sh) & 0x0F0F0F0Fu, o[2], o[3]);
-            }
-            return __builtin_bit_cast(f16x8, make_uint4(o[0], o[1], o[2], o[3]));
-        };
-        f32x4 prev[TM], cur[TM];
-        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-        // the block's product: both activation terms times the exact quants, summed in float32
-        auto block = [&](int i, const f16x8& b) {
-            f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], b, zero, 0, 0, 0);
-            if constexpr (TT) t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b, t, 0, 0, 0);
-            return t;
-        };
-        {
-            const f16x8 b0 = bfrag(0);
-#pragma unroll
-            for (int i = 0; i < TM; i++) prev[i] = block(i, b0);
-        }
-#pragma unroll
-        for (int c = 1; c <= NB * TN; c++) {
-            if (c < NB * TN) {
-                const f16x8 bc = bfrag(c);
-#pragma unroll
-                for (int i = 0; i < TM; i++) cur[i] = block(i, bc);
-            }
-            const int pc = c - 1, mat = pc / TN, j = pc % TN;
-#pragma unroll
-            for (int i = 0; i < TM; i++) acc[mat][i][j] += d[pc] * prev[i];
-#pragma unroll
-            for (int i = 0; i < TM; i++) prev[i] = cur[i];
-        }
-    };
-    auto compute = [&](const uint8_t* sg) {
-#pragma unroll
-        for (int kk = 0; kk < 2; kk++) {
-            f16x8 af[TM], al[TT ? TM : 1];
-#pragma unroll
-            for (int i = 0; i < TM; i++) {
-                const int r = wm * WM + 16 * i + (lane & 15);
-                const int o = r * DBK * 2 + ((4 * kk + jj) ^ swz_a(r)) * 16;
-                af[i] = *(const f16x8*)(sg + o);
-                if constexpr (TT) al[i] = *(const f16x8*)(sg + L::A_LO + o);
-            }
-#pragma unroll
-            for (int mat = 0; mat < NB; mat++)
-#pragma unroll
-                for (int j = 0; j < TN; j++) {
-                    const int r = wn * WN + 16 * j + (lane & 15);
-                    const uint8_t* bq = sg + L::B_OFF + mat * BN * L::BROW;
-                    if constexpr (FMT == DT_F16) {
-                        const f16x8 bf = *(const f16x8*)(bq + r * 128 + ((4 * kk + jj) ^ swz_a(r)) * 16);
-#pragma unroll
-                        for (int i = 0; i < TM; i++) {
-                            acc[mat][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, acc[mat][i][j], 0, 0, 0);
-                            if constexpr (TT)
-                                acc[mat][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bf, acc[mat][i][j], 0, 0, 0);
-                        }
+    #pragma unroll
+            for (int mat = 0; mat < NB; mat++) {
+                const DevMatrix& w = mat ? p.u : p.w;
+                const uint32_t bq = sg + L2::B_OFF + mat * BN * L2::BROW;
+    #pragma unroll
+                for (int i = 0; i < G::B_I; i++) {
+                    if constexpr (FMT == DT_Q8_0) {
+                        dma16s(w.q + k0, boff[mat][i], bq + (i * NW + wave) * 16 * 64);
+                    } else if constexpr (FMT == DT_Q4_0) {
+                        if constexpr (G::Q4_16) dma16s(w.q + kt * 32, boff[mat][i], bq + (i * NW + wave) * 32 * 32);
+                        else dma4s(w.q + kt * 32, boff[mat][i], bq + (i * NW + wave) * 8 * 32);
+                    } else {
+                        dma16s(w.q + k0 * 2, boff[mat][i], bq + (i * NW + wave) * 8 * 128);
                     }
                 }
-            if constexpr (FMT != DT_F16) compute_block_quant(sg, kk, af, al);
-        }
-    };
+                if constexpr (FMT != DT_F16) {
+                    // The tile's BN scale pairs are contiguous in s2: each wave moves
+                    // 1/NW of them, 16 bytes (4 rows) per active lane.
+                    if (lane < BN / (4 * NW))
+                        dma16s(w.s2 + (int64_t)kt * spitch, soff, sg + L2::S_OFF + mat * BN * 4 + wave * (BN / NW) * 4);
+                }
+            }
+        };
 
-    // One step: wait for stage kt (stage kt+1 stays in flight), barrier, refill
-    // the buffer consumed by the previous step with stage kt+2, multiply stage
-    // kt.  Past the end the refill reloads the last stage into a buffer that is
-    // never read again, so every step has the same wait count.
-    auto step = [&](const uint8_t* cur, uint8_t* refill, int i) {
-        wait_stage_barrier<PER>();
-        issue(lds_addr(refill), ktc(i + 2));
-        if (i < cnt) compute(cur);
-    };
-    if constexpr (NSTAGE == 3) {
-        issue(lds_addr(st0), ktc(0));
-        issue(lds_addr(st1), ktc(1));
-        for (int i = 0; i < per; i += 3) {
-            step(st0, st2, i);
-            if (i + 1 < per) step(st1, st0, i + 1);
-            if (i + 2 < per) step(st2, st1, i + 2);
-        }
-    } else {
-        // wait for the stage (nothing else in flight), barrier (every wave is
-        // done with the other buffer), refill it with the next stage, multiply
-        auto step2 = [&](const uint8_t* cur, uint8_t* refill, int i) {
-            wait_stage_barrier<0>();
-            issue(lds_addr(refill), ktc(i + 1));
+        const int jj = lane >> 4;  // which 8 of the fragment's 32 k values this lane holds
+        // Quantised weights, one 32-weight block (kk) of a stage: each MFMA result
+        // is scaled by the block's d before it is accumulated.  The MFMAs of column
+        // j+1 are issued before the scaling of column j, so the VALU work of one
+        // column runs under the MFMAs of the next instead of waiting on them.
+        auto compute_block_quant = [&](const uint8_t* sg, int kk, const f16x8 (&af)[TM], const f16x8 (&al)[T2 ? TM : 1]) {
+            // The raw quants of every column are read first; each becomes f16 just
+            // before its MFMAs (8 bytes live per column instead of 16).
+            uint2 raw[NB * TN];
+            float d[NB * TN];
+    #pragma unroll
+            for (int c = 0; c < NB * TN; c++) {
+                const int mat = c / TN, j = c % TN;
+                const int r = wn * WN + 16 * j + (lane & 15);
+                const uint8_t* bq = sg + L2::B_OFF + mat * BN * L2::BROW;
+                if constexpr (FMT == DT_Q8_0) {
+                    const int u = 4 * kk + jj;
+                    raw[c] = *(const uint2*)(bq + r * 64 + ((u >> 1) ^ swz_q8(r)) * 16 + (u & 1) * 8);
+                } else {
+                    raw[c] = *(const uint2*)(bq + r * 32 + (kk ^ swz_q4(r)) * 16 + (jj & 1) * 8);
+                }
+                d[c] = (float)*(const f16*)(sg + L2::S_OFF + mat * BN * 4 + r * 4 + kk * 2);
+            }
+            auto bfrag = [&](int c) {
+                uint32_t o[4];
+                if constexpr (FMT == DT_Q8_0) {
+                    int8x4_to_f16(raw[c].x, o[0], o[1]);
+                    int8x4_to_f16(raw[c].y, o[2], o[3]);
+                } else {
+                    const int sh = (jj >> 1) * 4;
+                    nib4_to_f16((raw[c].x >> sh) & 0x0F0F0F0Fu, o[0], o[1]);
+                    nib4_to_f16((raw[c].y >> sh) & 0x0F0F0F0Fu, o[2], o[3]);
+                }
+                return __builtin_bit_cast(f16x8, make_uint4(o[0], o[1], o[2], o[3]));
+            };
+            f32x4 prev[TM], cur[TM];
+            const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+            // the block's product: both activation terms times the exact quants, summed in float32
+            auto block = [&](int i, const f16x8& b) {
+                f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], b, zero, 0, 0, 0);
+                if constexpr (T2) t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b, t, 0, 0, 0);
+                return t;
+            };
+            {
+                const f16x8 b0 = bfrag(0);
+    #pragma unroll
+                for (int i = 0; i < TM; i++) prev[i] = block(i, b0);
+            }
+    #pragma unroll
+            for (int c = 1; c <= NB * TN; c++) {
+                if (c < NB * TN) {
+                    const f16x8 bc = bfrag(c);
+    #pragma unroll
+                    for (int i = 0; i < TM; i++) cur[i] = block(i, bc);
+                }
+                const int pc = c - 1, mat = pc / TN, j = pc % TN;
+    #pragma unroll
+                for (int i = 0; i < TM; i++) acc[mat][i][j] += d[pc] * prev[i];
+    #pragma unroll
+                for (int i = 0; i < TM; i++) prev[i] = cur[i];
+            }
+        };
+        auto compute = [&](const uint8_t* sg) {
+    #pragma unroll
+            for (int kk = 0; kk < 2; kk++) {
+                f16x8 af[TM], al[T2 ? TM : 1];
+    #pragma unroll
+                for (int i = 0; i < TM; i++) {
+                    const int r = wm * WM + 16 * i + (lane & 15);
+                    const int o = r * DBK * 2 + ((4 * kk + jj) ^ swz_a(r)) * 16;
+                    af[i] = *(const f16x8*)(sg + o);
+                    if constexpr (T2) al[i] = *(const f16x8*)(sg + L2::A_LO + o);
+                }
+    #pragma unroll
+                for (int mat = 0; mat < NB; mat++)
+    #pragma unroll
+                    for (int j = 0; j < TN; j++) {
+                        const int r = wn * WN + 16 * j + (lane & 15);
+                        const uint8_t* bq = sg + L2::B_OFF + mat * BN * L2::BROW;
+                        if constexpr (FMT == DT_F16) {
+                            const f16x8 bf = *(const f16x8*)(bq + r * 128 + ((4 * kk + jj) ^ swz_a(r)) * 16);
+    #pragma unroll
+                            for (int i = 0; i < TM; i++) {
+                                acc[mat][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, acc[mat][i][j], 0, 0, 0);
+                                if constexpr (T2)
+                                    acc[mat][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bf, acc[mat][i][j], 0, 0, 0);
+                            }
+                        }
+                    }
+                if constexpr (FMT != DT_F16) compute_block_quant(sg, kk, af, al);
+            }
+        };
+
+        // One step: wait for stage kt (stage kt+1 stays in flight), barrier, refill
+        // the buffer consumed by the previous step with stage kt+2, multiply stage
+        // kt.  Past the end the refill reloads the last stage into a buffer that is
+        // never read again, so every step has the same wait count.
+        auto step = [&](const uint8_t* cur, uint8_t* refill, int i) {
+            wait_stage_barrier<PER2>();
+            issue(lds_addr(refill), ktc(i + 2));
             if (i < cnt) compute(cur);
         };
-        issue(lds_addr(st0), ktc(0));
-        for (int i = 0; i < per; i += 2) {
-            step2(st0, st1, i);
-            if (i + 1 < per) step2(st1, st0, i + 1);
+        if constexpr (NSTAGE == 3) {
+            issue(lds_addr(st0), ktc(0));
+            issue(lds_addr(st1), ktc(1));
+            for (int i = 0; i < per; i += 3) {
+                step(st0, st2, i);
+                if (i + 1 < per) step(st1, st0, i + 1);
+                if (i + 2 < per) step(st2, st1, i + 2);
+            }
+        } else {
+            // wait for the stage (nothing else in flight), barrier (every wave is
+            // done with the other buffer), refill it with the next stage, multiply
+            auto step2 = [&](const uint8_t* cur, uint8_t* refill, int i) {
+                wait_stage_barrier<0>();
+                issue(lds_addr(refill), ktc(i + 1));
+                if (i < cnt) compute(cur);
+            };
+            issue(lds_addr(st0), ktc(0));
+            for (int i = 0; i < per; i += 2) {
+                step2(st0, st1, i);
+                if (i + 1 < per) step2(st1, st0, i + 1);
+            }
+        }
+        // No DMA may still be writing this workgroup's LDS when its waves end.
+        wait_stage_barrier<0>();
+    };
+    if constexpr (TT) {
+        if (m0 + BM > p.lo_row0 || n0 + BN > p.lo_col0) kloop(std::true_type{});
+        else kloop(std::false_type{});
+    } else {
+        kloop(std::false_type{});
+        if constexpr (TAIL) {
+            if (tail_tile) {  // every stage buffer is free: the loop ends on a full wait and barrier
+                abase = p.xlo;
+                kloop(std::false_type{});
+            }
         }
     }
-    // No DMA may still be writing this workgroup's LDS when its waves end.
-    wait_stage_barrier<0>();
     if constexpr (KS > 1) {
         // The second set hands its accumulators to the first through its own
         // (idle) stage buffers; the first adds them and runs the epilogue.
@@ -1028,16 +1084,22 @@ __global__ __launch_bounds__(64 * (BM / WM) * (BN / WN) * KS) void dgemm_kernel(
                     const float v = (g / (1.0f + __expf(-g))) * u;
                     const f16 hv = (f16)v;
                     p.yh[o] = hv;
-                    if (p.yhlo) p.yhlo[o] = (f16)(v - (float)hv);
+                    if (p.yhlo && m >= p.lo_out_row0) p.yhlo[o] = (f16)(v - (float)hv);
                 }
             }
         }
 }
 
-template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH, bool TT, int KS = 1>
+template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH, bool TT, int KS = 1, bool TAIL = false>
 hipError_t run_dgemm(const GemmArgs& a, hipStream_t st) {
-    const int tiles = ((a.M + BM - 1) / BM) * ((a.w.rows + BN - 1) / BN);
-    dgemm_kernel<FMT, BM, BN, WM, WN, MODE, RH, TT, KS><<<tiles, 64 * (BM / WM) * (BN / WN) * KS, 0, st>>>(a);
+    const int tm = (a.M + BM - 1) / BM, tn = (a.w.rows + BN - 1) / BN;
+    int grid = tm * tn;
+    if constexpr (TAIL) {
+        if (a.lo_row0 % BM) return hipErrorInvalidValue;  // tail tiles start at lo_row0
+        const int main_m = std::min(tm, a.lo_row0 / BM);
+        grid = ((tm - main_m) * tn + 7) / 8 * 8 + main_m * tn;
+    }
+    dgemm_kernel<FMT, BM, BN, WM, WN, MODE, RH, TT, KS, TAIL><<<grid, 64 * (BM / WM) * (BN / WN) * KS, 0, st>>>(a);
     return hipGetLastError();
 }
 
@@ -1088,7 +1150,7 @@ int resident_per_cu() {
 }
 
 // Tile choice, counted in rounds of resident workgroups over the device's CUs.
-template <int FMT, int MODE, int RH, bool TT>
+template <int FMT, int MODE, int RH, bool TT, bool TAIL = false>
 hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
     const int M = a.M, N = a.w.rows, cus = device_cus();
     auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
@@ -1121,32 +1183,32 @@ hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
     // -> 12.2 us, Wo 10.9 -> 10.1, down 18.0 -> 15.1; C4 Wo 15.2 -> 13.1, down
     // 28.9 -> 22.9; slower on larger grids and for SwiGLU).  The other modes
     // then choose between 128x64 and 128x256 by the cost below.
-    if (f == 5) return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT>(a, st);
-    if (f == 9) return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT, 2>(a, st);
+    if (f == 5) return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT, 1, TAIL>(a, st);
+    if (f == 9) return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT, 2, TAIL>(a, st);
     auto small_grid = [&](double per_cu) {
         return f == 0 && TT && tiles(128, 64) <= per_cu * cus;
     };
     if constexpr (MODE == GEMM_SWIGLU) {
         if constexpr (!TT)
-            if (f == 1) return run_dgemm<FMT, 256, 64, 128, 32, MODE, RH, TT>(a, st);
+            if (f == 1) return run_dgemm<FMT, 256, 64, 128, 32, MODE, RH, TT, 1, TAIL>(a, st);
         if constexpr (FMT != DT_F16)  // (f16 weight stages are 4x larger: no third stage fits)
             if (f == 4 || (f == 0 && TT && wide_fits(tiles(128, 128))))
-                return run_dgemm<FMT, 128, 128, 64, 32, MODE, RH, TT>(a, st);
+                return run_dgemm<FMT, 128, 128, 64, 32, MODE, RH, TT, 1, TAIL>(a, st);
         if constexpr (TT)
-            if (small_grid(3.0)) return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT>(a, st);
-        return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH, TT>(a, st);
+            if (small_grid(3.0)) return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT, 1, TAIL>(a, st);
+        return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH, TT, 1, TAIL>(a, st);
     } else {
         if constexpr (!TT)
-            if (f == 1) return run_dgemm<FMT, 256, 128, 128, 64, MODE, RH, TT>(a, st);
+            if (f == 1) return run_dgemm<FMT, 256, 128, 128, 64, MODE, RH, TT, 1, TAIL>(a, st);
         const int slots = resident_per_cu<FMT, 128, 64, 64, 32, MODE, RH, TT>() * cus;
         if constexpr (TT)
             if (small_grid(1.6)) {
                 // at most one 64x64 tile per CU (quantised weights): two K sets
-                if (FMT != DT_F16 && tiles(64, 64) <= cus) return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT, 2>(a, st);
-                return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT>(a, st);
+                if (FMT != DT_F16 && tiles(64, 64) <= cus) return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT, 2, TAIL>(a, st);
+                return run_dgemm<FMT, 64, 64, 32, 32, MODE, RH, TT, 1, TAIL>(a, st);
             }
         if constexpr (FMT != DT_F16) {
-            if (f == 4) return run_dgemm<FMT, 128, 256, 64, 64, MODE, RH, TT>(a, st);
+            if (f == 4) return run_dgemm<FMT, 128, 256, 64, 64, MODE, RH, TT, 1, TAIL>(a, st);
             if (f == 0 && TT) {
                 // Two terms: 128x64 tiles (two per CU) or 128x256 (one per CU),
                 // by a cost in rounds of resident workgroups.  A 128x64 round
@@ -1158,12 +1220,12 @@ hipError_t pick_dgemm(const GemmArgs& a, hipStream_t st) {
                 const int t64 = tiles(128, 64), rem = t64 % slots;
                 const double c64 = t64 / slots + (rem ? (rem <= cus ? 0.6 : 1.0) : 0.0);
                 const double cw = ((tiles(128, 256) + cus - 1) / cus) * (a.w.cols >= 1536 ? 1.87 : 1.32);
-                if (cw < c64) return run_dgemm<FMT, 128, 256, 64, 64, MODE, RH, TT>(a, st);
-                return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH, TT>(a, st);
+                if (cw < c64) return run_dgemm<FMT, 128, 256, 64, 64, MODE, RH, TT, 1, TAIL>(a, st);
+                return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH, TT, 1, TAIL>(a, st);
             }
         }
-        if (f == 2 || (f == 0 && tiles(128, 64) > slots)) return run_dgemm<FMT, 128, 128, 64, 64, MODE, RH, TT>(a, st);
-        return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH, TT>(a, st);
+        if (f == 2 || (f == 0 && tiles(128, 64) > slots)) return run_dgemm<FMT, 128, 128, 64, 64, MODE, RH, TT, 1, TAIL>(a, st);
+        return run_dgemm<FMT, 128, 64, 64, 32, MODE, RH, TT, 1, TAIL>(a, st);
     }
 }
 
@@ -1178,8 +1240,44 @@ hipError_t dgemm_mode_terms(const GemmArgs& a, int mode, hipStream_t st) {
     return pick_dgemm<FMT, GEMM_SWIGLU, 0, TT>(a, st);
 }
 
+// Second terms of the activations for the rows from lo_row0 on only: the
+// one-term kernel with a second pass over the tail tiles.
+template <int FMT>
+hipError_t dgemm_mode_tail(const GemmArgs& a, int mode, hipStream_t st) {
+    if (mode == GEMM_STORE) return pick_dgemm<FMT, GEMM_STORE, 0, false, true>(a, st);
+    if (mode == GEMM_ACC) return pick_dgemm<FMT, GEMM_ACC, 0, false, true>(a, st);
+    if (mode == GEMM_SWIGLU) return pick_dgemm<FMT, GEMM_SWIGLU, 0, false, true>(a, st);
+    return hipErrorNotSupported;
+}
+
+// With the second term on the rows from lo_row0 on only, two forms: the
+// one-term kernel with a second K pass over the tail tiles (dispatched first),
+// or the two-term kernel taking the second term tile by tile.  The second pass
+// doubles a tail tile's time, which a grid of one round of resident
+// workgroups waits for in full, while over a longer grid the tail tiles
+// overlap the later rounds and the other tiles run at the one-term kernel's
+// occupancy and tile shape.  Measured per call at 4,096 rows (us, second pass
+// against per tile): 1.7B shape Wo 67 / 70, gate+up 390 / 446, down 238 / 246
+// (1.3-5.3 rounds); 135M shape Wo 18.6 / 15.1, gate+up 37.7 / 36.6, down
+// 34.7 / 25.6 (0.4-1.0 rounds).  So the second pass is taken where the
+// one-term grid of 128x64 tiles exceeds one round.  ALPACA_HIP_LO_PASS=tile |
+// tail (read per launch) forces one form.
+template <int FMT>
+bool tail_pass_pays(const GemmArgs& a, int mode) {
+    const char* e = std::getenv("ALPACA_HIP_LO_PASS");
+    if (e && !std::strcmp(e, "tile")) return false;
+    if (e && !std::strcmp(e, "tail")) return true;
+    const int cus = device_cus(), rows = (a.M + 127) / 128, cols = (a.w.rows + 63) / 64;
+    const int per_cu = mode == GEMM_SWIGLU ? resident_per_cu<FMT, 128, 64, 64, 32, GEMM_SWIGLU, 0, false>()
+                       : mode == GEMM_ACC  ? resident_per_cu<FMT, 128, 64, 64, 32, GEMM_ACC, 0, false>()
+                                           : resident_per_cu<FMT, 128, 64, 64, 32, GEMM_STORE, 0, false>();
+    return (int64_t)rows * cols > (int64_t)per_cu * cus;
+}
+
 template <int FMT>
 hipError_t dgemm_mode(const GemmArgs& a, int mode, hipStream_t st) {
+    if (a.xlo && a.lo_row0 > 0 && mode != GEMM_QKV_ROPE && tail_pass_pays<FMT>(a, mode))
+        return dgemm_mode_tail<FMT>(a, mode, st);
     return a.xlo ? dgemm_mode_terms<FMT, true>(a, mode, st) : dgemm_mode_terms<FMT, false>(a, mode, st);
 }
 
@@ -1208,14 +1306,15 @@ bool prefill_split_pays(int m, int n) {
 }
 
 hipError_t launch_gemm_mfma(const f16* x, const f16* xlo, int ldx, int m, const DevMatrix& w, const DevMatrix* w_up,
-                            float* y, f16* yh, f16* yhlo, int ldy, int mode, hipStream_t st) {
+                            float* y, f16* yh, f16* yhlo, int ldy, int mode, hipStream_t st, int lo_row0,
+                            int lo_out_row0) {
     if (m <= 0) return hipSuccess;
     // The DMA kernel needs 64-wide K stages, 16-byte aligned activation rows and,
     // for quantised weights, the stage-major scales.
     const bool quant = w.dtype != DT_F16;
     if (w.cols % DBK || ldx % 8 || ((uintptr_t)x & 15) || ((uintptr_t)xlo & 15) ||
         (quant && (!w.s2 || (w_up && !w_up->s2))) || !dma_offsets_fit(m, ldx, w))
-        return launch_gemm_mfma_staged(x, xlo, ldx, m, w, w_up, y, yh, yhlo, ldy, mode, st);
+        return launch_gemm_mfma_staged(x, xlo, ldx, m, w, w_up, y, yh, yhlo, ldy, mode, st, lo_row0, lo_out_row0);
     GemmArgs a;
     a.x = x;
     a.xlo = xlo;
@@ -1227,6 +1326,8 @@ hipError_t launch_gemm_mfma(const f16* x, const f16* xlo, int ldx, int m, const 
     a.y = y;
     a.yh = yh;
     a.ldy = ldy;
+    a.lo_row0 = lo_row0;
+    a.lo_out_row0 = lo_out_row0;
     switch (w.dtype) {
     case DT_Q8_0: return dgemm_mode<DT_Q8_0>(a, mode, st);
     case DT_Q4_0: return dgemm_mode<DT_Q4_0>(a, mode, st);
@@ -1235,7 +1336,7 @@ hipError_t launch_gemm_mfma(const f16* x, const f16* xlo, int ldx, int m, const 
 }
 
 hipError_t launch_gemm_qkv_rope(const f16* x, const f16* xlo, int ldx, int m, const DevMatrix& w, const QkvRope& o,
-                                hipStream_t st) {
+                                hipStream_t st, int lo_row0, int lo_out_row0, int lo_col0) {
     if (m <= 0) return hipSuccess;
     const bool quant = w.dtype != DT_F16;
     // the pipelined kernel's conditions (as in launch_gemm_mfma); RoPE pairs and
@@ -1257,6 +1358,9 @@ hipError_t launch_gemm_qkv_rope(const f16* x, const f16* xlo, int ldx, int m, co
     a.yh = o.qh;
     a.ldy = o.heads * o.hd;
     a.qkv = o;
+    a.lo_row0 = lo_row0;
+    a.lo_out_row0 = lo_out_row0;
+    a.lo_col0 = lo_col0;
     switch (w.dtype) {
     case DT_Q8_0: return dgemm_mode<DT_Q8_0>(a, GEMM_QKV_ROPE, st);
     case DT_Q4_0: return dgemm_mode<DT_Q4_0>(a, GEMM_QKV_ROPE, st);

@@ -49,7 +49,8 @@ __global__ void f32_to_f16_kernel(const float* x, f16* o, f16* ol, int64_t n) {
 // CPUOps.rmsNorm (CPUOps.swift:144-159): y = x * (1/sqrt(mean(x^2) + eps)) * w,
 // one block per row, optionally writing f16 for the MFMA GEMM.
 __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const float* x, const float* w, float* of, f16* oh,
-                                                         f16* ol, int dim, float eps) {
+                                                         f16* ol, int dim, float eps, int lo_row0) {
+    if ((int)blockIdx.x < lo_row0) ol = nullptr;
     __shared__ float red[16];
     const float* xr = x + (int64_t)blockIdx.x * dim;
     float ss = 0.f;
@@ -68,9 +69,10 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const float* x, const f
 // 8-byte f16 stores, and no block barrier.
 constexpr int kNormV4 = 8;
 __global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(const float* x, const float* w, float* of, f16* oh,
-                                                              f16* ol, int rows, int dim, float eps) {
+                                                              f16* ol, int rows, int dim, float eps, int lo_row0) {
     const int row = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= rows) return;  // whole waves leave together
+    if (row < lo_row0) ol = nullptr;
     const int n4 = dim >> 2;
     const float4* xr = (const float4*)(x + (int64_t)row * dim);
     const float4* wr = (const float4*)w;
@@ -262,12 +264,12 @@ hipError_t launch_f32_to_f16(const float* x, f16* out, f16* out_lo, int64_t n, h
     return hipGetLastError();
 }
 hipError_t launch_rmsnorm(const float* x, const float* w, float* of, f16* oh, f16* ol, int rows, int dim, float eps,
-                          hipStream_t st) {
+                          hipStream_t st, int lo_row0) {
     if (rows <= 0) return hipSuccess;
     const bool vec = dim % 4 == 0 && dim <= 64 * 4 * kNormV4 && !((uintptr_t)x & 15) && !((uintptr_t)w & 15) &&
                      !((uintptr_t)of & 15) && !((uintptr_t)oh & 7) && !((uintptr_t)ol & 7);
-    if (vec) rmsnorm_rows_kernel<<<(rows + 3) / 4, kBlock, 0, st>>>(x, w, of, oh, ol, rows, dim, eps);
-    else rmsnorm_kernel<<<rows, kBlock, 0, st>>>(x, w, of, oh, ol, dim, eps);
+    if (vec) rmsnorm_rows_kernel<<<(rows + 3) / 4, kBlock, 0, st>>>(x, w, of, oh, ol, rows, dim, eps, lo_row0);
+    else rmsnorm_kernel<<<rows, kBlock, 0, st>>>(x, w, of, oh, ol, dim, eps, lo_row0);
     return hipGetLastError();
 }
 hipError_t launch_embed(const int32_t* tokens, int count, const DevMatrix& table, float* out, hipStream_t st) {

@@ -660,6 +660,8 @@ struct ahip_session {
     int capacity = 0, max_batch = 0, kv_f16 = 1, fast = 1;
     int two_term = 1;  // fast prefill with two-term activations (AHIP_GEMM_FAST); 0: one f16 term (FAST_F16)
     int lo_terms = 0;  // with two_term: which operands carry the second term (kLo* bits)
+    bool lo_all_rows = false;  // second terms on every row, not only the last row's tiles
+    bool qkv_lo_all = false;   // the QKV GEMM's q columns take the second term on every row too
     int fuse_qkv_rope = 1;  // ALPACA_HIP_FUSE_QKV_ROPE at creation; 0: RoPE + KV append as their own kernel
     // Numerics diagnostics, read at creation: ALPACA_HIP_PREFILL_ATTENTION=generic runs the fast prefill's
     // attention as the float32 kernel the exact prefill uses; ALPACA_HIP_PREFILL_GEMM=f32 its projections as
@@ -1147,6 +1149,12 @@ extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, i
     s->fast = gemm_precision != AHIP_GEMM_EXACT;
     s->two_term = gemm_precision == AHIP_GEMM_FAST;
     s->lo_terms = s->two_term ? lo_terms_for(c) : 0;
+    {
+        const char* r = std::getenv("ALPACA_HIP_LO_ROWS");
+        s->lo_all_rows = r && !std::strcmp(r, "all");
+        const char* q = std::getenv("ALPACA_HIP_QKV_LO");
+        s->qkv_lo_all = s->lo_all_rows || !(q && !std::strcmp(q, "kv"));
+    }
     s->fuse_qkv_rope = env_int("ALPACA_HIP_FUSE_QKV_ROPE", 1) != 0;
     {
         const char* a = std::getenv("ALPACA_HIP_PREFILL_ATTENTION");
@@ -1288,7 +1296,8 @@ static int encode_decode_layer(ahip_session* s, int li, int pos, const int* pos_
 // [row0, row0 + n) and positions [pos, pos + n), on stream st.  after_qkv (if
 // set) is recorded once these rows' K/V are in the cache; the attention first
 // waits for the n_before events of before_attn (earlier rows' K/V).
-static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, bool flash, hipStream_t st,
+// `last`: these rows end with the row whose logits the call returns.
+static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, bool flash, bool last, hipStream_t st,
                              hipEvent_t after_qkv, const hipEvent_t* before_attn = nullptr, int n_before = 0) {
     ahip_model* m = s->m;
     const ahip_llama_config& c = m->c;
@@ -1308,13 +1317,26 @@ static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, 
     // Second-term planes of the f16 activation buffers (two-term prefill),
     // after the first planes; null where the operand takes one term (the
     // producer then writes no second term and the consumer reads none).
+    // The QKV input keeps its second term on every row: k and v go to the
+    // cache, which every later position reads.  The other operands (Wo,
+    // gate/up and down inputs, attention's Q and P) carry it only where the
+    // returned logits depend on them row by row: on the rows [tail0, n) of a
+    // call's last rows, tail0 being the last row rounded down to a multiple of
+    // 256.  Tiles (at most 256 rows, starting at multiples of their height)
+    // and 64-query blocks then either lie wholly in that range or wholly
+    // before it, so the same rows take two terms whatever tile a GEMM picks.
+    // With lo_all_rows every row takes them.
     const int lo = s->two_term ? s->lo_terms : 0;
+    const bool all = s->lo_all_rows;
+    const int tail0 = all ? 0 : last ? (n - 1) / 256 * 256 : n;
+    const int lo_tile = tail0;
+    auto want = [&](int bit) { return (lo & bit) && (all || last); };
     f16* xhlo_qkv = lo & kLoQkv ? s->xh.as<f16>() + B * H + r * H : nullptr;
-    f16* xhlo_ffn = lo & kLoGateUp ? s->xh.as<f16>() + B * H + r * H : nullptr;
-    f16* qhlo = lo & kLoQ ? s->qh.as<f16>() + B * QW + r * QW : nullptr;
-    f16* ctxhlo = lo & kLoWo ? s->ctxh.as<f16>() + B * QW + r * QW : nullptr;
-    f16* ffnhlo = lo & kLoDown ? s->ffnh.as<f16>() + B * F + r * F : nullptr;
-    const int p_terms = lo & kLoP ? 2 : 1;
+    f16* xhlo_ffn = want(kLoGateUp) ? s->xh.as<f16>() + B * H + r * H : nullptr;
+    f16* qhlo = want(kLoQ) ? s->qh.as<f16>() + B * QW + r * QW : nullptr;
+    f16* ctxhlo = want(kLoWo) ? s->ctxh.as<f16>() + B * QW + r * QW : nullptr;
+    f16* ffnhlo = want(kLoDown) ? s->ffnh.as<f16>() + B * F + r * F : nullptr;
+    const int p_terms = want(kLoP) ? 2 : 1;
     float* ctx = s->ctx.as<float>() + r * QW;
     s->stage("rmsnorm");
     LAUNCH(launch_rmsnorm(x, L.attn_norm.as<float>(), nullptr, xh, xhlo_qkv, n, H, c.rms_norm_eps, st));
@@ -1333,7 +1355,11 @@ static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, 
         o.hd = hd;
         o.pos = pos;
         o.capacity = s->capacity;
-        fused = launch_gemm_qkv_rope(xh, xhlo_qkv, H, n, L.pre(L.qkv, L.qkv16), o, st);
+        // k and v take the second term on every row; q too unless ALPACA_HIP_QKV_LO=kv (read at
+        // session creation), which keeps it to the tail rows: 1% faster at the 1.7B shape, and
+        // the 135M shape's logit error 0.13 -> 0.20 of the bound, so it is off by default
+        fused = launch_gemm_qkv_rope(xh, xhlo_qkv, H, n, L.pre(L.qkv, L.qkv16), o, st, s->qkv_lo_all ? 0 : tail0,
+                                     tail0, s->qkv_lo_all ? 0 : QW);
         if (fused != hipErrorNotSupported) LAUNCH(fused);
     }
     if (fused == hipErrorNotSupported) {
@@ -1347,23 +1373,27 @@ static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, 
     for (int k = 0; k < n_before; k++) HIP_OR(hipStreamWaitEvent(st, before_attn[k], 0), "hipStreamWaitEvent");
     s->stage("attention");
     if (flash) {
+        // Q and P take their second terms only in the query block of the last row (the
+        // longest of the causal walk; a two-term block takes twice the MFMA work).
         LAUNCH(launch_flash_attention(qh, qhlo, QW, (const f16*)kc, (const f16*)vc, s->capacity, n, c.head_count,
-                                      c.kv_head_count, hd, pos, nullptr, ctxh, ctxhlo, st, p_terms));
+                                      c.kv_head_count, hd, pos, nullptr, ctxh, ctxhlo, st, p_terms,
+                                      all ? 0 : n - 1, tail0));
     } else {
         LAUNCH(launch_attention_generic(qkv, LDQKV, kc, vc, s->kv_f16, s->capacity, n, c.head_count, c.kv_head_count,
                                         hd, pos, 1, nullptr, ctx, st));
         LAUNCH(launch_f32_to_f16(ctx, ctxh, ctxhlo, (int64_t)n * QW, st));
     }
     s->stage("attn out projection (+residual)");
-    LAUNCH(launch_gemm_mfma(ctxh, ctxhlo, QW, n, L.pre(L.wo, L.wo16), nullptr, x, nullptr, nullptr, H, GEMM_ACC, st));
+    LAUNCH(launch_gemm_mfma(ctxh, ctxhlo, QW, n, L.pre(L.wo, L.wo16), nullptr, x, nullptr, nullptr, H, GEMM_ACC, st,
+                            lo_tile));
     s->stage("rmsnorm");
-    LAUNCH(launch_rmsnorm(x, L.ffn_norm.as<float>(), nullptr, xh, xhlo_ffn, n, H, c.rms_norm_eps, st));
+    LAUNCH(launch_rmsnorm(x, L.ffn_norm.as<float>(), nullptr, xh, xhlo_ffn, n, H, c.rms_norm_eps, st, tail0));
     s->stage("ffn gate+up+silu");
     LAUNCH(launch_gemm_mfma(xh, xhlo_ffn, H, n, L.pre(L.gate, L.gate16), &L.pre(L.up, L.up16), nullptr, ffnh, ffnhlo, F,
-                            GEMM_SWIGLU, st));
+                            GEMM_SWIGLU, st, lo_tile, tail0));
     s->stage("ffn down (+residual)");
     LAUNCH(launch_gemm_mfma(ffnh, ffnhlo, F, n, L.pre(L.down, L.down16), nullptr, x, nullptr, nullptr, H, GEMM_ACC,
-                            st));
+                            st, lo_tile));
     return AHIP_OK;
 }
 
@@ -1400,9 +1430,11 @@ static int encode_split_prefill(ahip_session* s, const int32_t* dtok, int n, int
             HIP_OR(hipEventCreateWithFlags(&s->part_done[k], hipEventDisableTiming), "hipEventCreate");
         }
     }
-    // part k: rows [r[k], r[k+1]); every boundary but the last a multiple of 64
+    // part k: rows [r[k], r[k+1]); every boundary but the last a multiple of
+    // 256, so the last part's rows that take the second terms (from the last
+    // row rounded down to a multiple of 256) are those of one stream
     int r[ahip_session::kMaxParts + 1];
-    for (int k = 0; k < parts; k++) r[k] = (int)((int64_t)n * k / parts / 64 * 64);
+    for (int k = 0; k < parts; k++) r[k] = (int)((int64_t)n * k / parts / 256 * 256);
     r[parts] = n;
     HIP_OR(hipEventRecord(s->part_start, s->stream), "hipEventRecord");
     float* x = s->x.as<float>();
@@ -1418,7 +1450,8 @@ static int encode_split_prefill(ahip_session* s, const int32_t* dtok, int n, int
         }
         for (int li = 0; li < c.layer_count; li++)
             for (int k = 0; k < parts; k++)
-                if (int rc = encode_mfma_layer(s, li, r[k], r[k + 1] - r[k], pos + r[k], flash, s->part_stream[k],
+                if (int rc = encode_mfma_layer(s, li, r[k], r[k + 1] - r[k], pos + r[k], flash,
+                                               logits && k + 1 == parts, s->part_stream[k],
                                                k + 1 < parts ? s->part_qkv[k] : nullptr, s->part_qkv, k))
                     return rc;
         if (logits)
@@ -1469,7 +1502,7 @@ static int encode_chunk(ahip_session* s, const int32_t* dtok, int n, int pos, bo
         if (n == 1) {
             if (int rc = encode_decode_layer(s, li, pos, pos_dev)) return rc;
         } else if (mfma) {
-            if (int rc = encode_mfma_layer(s, li, 0, n, pos, flash, st, nullptr, nullptr)) return rc;
+            if (int rc = encode_mfma_layer(s, li, 0, n, pos, flash, logits, st, nullptr, nullptr)) return rc;
         } else {
             float* xn = s->xn.as<float>();
             s->stage("rmsnorm");
@@ -1916,8 +1949,11 @@ static int op_project(ahip_context* ctx, const float* x, int m, int k, int dtype
             const int gm = mode == GEMM_STORE ? GEMV_STORE : mode == GEMM_ACC ? GEMV_ADD : GEMV_SWIGLU;
             LAUNCH(launch_gemv(W.m, up, dx.as<float>(), nullptr, 0.f, dy.as<float>(), gm, st));
         } else if (precision != AHIP_GEMM_EXACT && m >= 16) {
-            // f16 activations: two planes (hi, lo) for the two-term default, one for FAST_F16
+            // f16 activations: two planes (hi, lo) for the two-term default, one for FAST_F16.
+            // ALPACA_HIP_OP_LO_ROW0 (read per call; a multiple of 256) has the GEMM take the
+            // second term only from that row on, as the prefill does for a call's last rows.
             const bool tt = precision == AHIP_GEMM_FAST;
+            const int lo_row0 = tt ? env_int("ALPACA_HIP_OP_LO_ROW0", 0) : 0;
             DevBuf xh, yh;
             if (int rc = xh.alloc((size_t)m * k * 2 * (tt ? 2 : 1))) return rc;
             f16* xlo = tt ? xh.as<f16>() + (size_t)m * k : nullptr;
@@ -1925,7 +1961,8 @@ static int op_project(ahip_context* ctx, const float* x, int m, int k, int dtype
             if (mode == GEMM_SWIGLU) {
                 if (int rc = yh.alloc((size_t)m * n * 2 * (tt ? 2 : 1))) return rc;
                 f16* ylo = tt ? yh.as<f16>() + (size_t)m * n : nullptr;
-                LAUNCH(launch_gemm_mfma(xh.as<f16>(), xlo, k, m, W.m, up, nullptr, yh.as<f16>(), ylo, n, mode, st));
+                LAUNCH(launch_gemm_mfma(xh.as<f16>(), xlo, k, m, W.m, up, nullptr, yh.as<f16>(), ylo, n, mode, st,
+                                        lo_row0, 0));
                 // the result as the next GEMM takes it: hi + lo (two-term) or hi
                 std::vector<uint16_t> h((size_t)m * n * (tt ? 2 : 1));
                 if (int rc = download(h.data(), yh, h.size() * 2, st)) return rc;
@@ -1934,7 +1971,7 @@ static int op_project(ahip_context* ctx, const float* x, int m, int k, int dtype
                 return AHIP_OK;
             }
             LAUNCH(launch_gemm_mfma(xh.as<f16>(), xlo, k, m, W.m, nullptr, dy.as<float>(), nullptr, nullptr, n, mode,
-                                    st));
+                                    st, lo_row0, 0));
         } else {
             LAUNCH(launch_gemm_f32(dx.as<float>(), k, m, W.m, up, dy.as<float>(), n, mode, st));
         }

@@ -309,3 +309,50 @@ def test_argmax_rules(hip_ops):
     v[31337] = 10.0
     v[40000] = 10.0
     assert hip_ops.argmax(v) == 31337 == orc.argmax(v)
+
+
+@pytest.mark.parametrize("name,dt", FORMATS)
+def test_gemm_second_term_from_a_row_on(hip_ops, name, dt):
+    """The prefill takes the activations' second term only on a call's last
+    rows: a one-term kernel whose tiles from row lo_row0 on (a multiple of
+    256) make a second pass over K with the second term as A
+    (ALPACA_HIP_OP_LO_ROW0, read per call).  Rows before lo_row0 are the
+    one-term (fast-f16) GEMM's bit for bit, as the same one-term tiles compute
+    them (SwiGLU's f16 output to its second term); rows from lo_row0 on are
+    within the two-term GEMM's tolerance
+    2e-4 + 1e-4 |y| of the oracle, in the store, residual and SwiGLU
+    epilogues, at M = 4096 (the C1 and C4 prompt length) and one 256-row
+    tail, at M = 1000 with a partial last tile."""
+    k, n = 576, 1600
+    w = encode(rand((n, k), 5151 + dt, 0.3), dt)
+    wu = encode(rand((n, k), 5252 + dt, 0.3), dt)
+    for m, lo_row0 in ((4096, 3840), (4096, 256), (1000, 768)):
+        x = rand((m, k), 5353 + m)
+        res = rand((m, n), 5454, 5)
+        one = (hip_ops.linear(x, w, "fast-f16"), hip_ops.linear_add(x, w, res, "fast-f16"),
+               hip_ops.gate_up_silu(x, w, wu, "fast-f16"))
+        with env(ALPACA_HIP_OP_LO_ROW0=lo_row0):
+            tail = (hip_ops.linear(x, w, "fast"), hip_ops.linear_add(x, w, res, "fast"),
+                    hip_ops.gate_up_silu(x, w, wu, "fast"))
+        y = orc.linear(x, dt, w.data, n)
+        u = orc.linear(x, dt, wu.data, n)
+        cpu = (y, orc.add(res, y), orc.mul(orc.silu(y), u))
+        for i, what in enumerate(("store", "residual", "swiglu")):
+            a, b = tail[i][:lo_row0], one[i][:lo_row0]
+            if what == "swiglu":
+                # the two-term op returns hi + lo of its f16 output, hi being the one-term op's
+                # value and |lo| at most half the ulp of the binade [2^e, 2^(e+1)) that |hi|
+                # starts (a power of two rounds from above too), or 2^-24 where hi is
+                # subnormal and lo a multiple of 2^-24
+                e = np.frexp(np.abs(b.astype(np.float64)))[1] - 1
+                half = np.maximum(np.ldexp(0.5, e - 10), 2.0 ** -24)
+                d = np.abs(a.astype(np.float64) - b)
+                assert (d <= half).all(), f"{name} {what} m={m}: one-term rows differ by {(d / half).max():.2f} half-ulps"
+                continue
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{name} {what} m={m}: one-term rows differ"
+            e = cpu[i][lo_row0:].astype(np.float64)
+            err = np.abs(tail[i][lo_row0:].astype(np.float64) - e)
+            tol = 2e-4 + 1e-4 * np.abs(e)
+            print(f"[metrics] {name} {what} m={m} rows {lo_row0}..: worst error / (2e-4 + 1e-4|y|) "
+                  f"{(err / tol).max():.4f}")
+            assert (err <= tol).all(), f"{name} {what} m={m}: two-term rows off by {(err / tol).max():.3f} of tol"

@@ -118,29 +118,39 @@ def test_fused_qkv_rope_under_each_forced_tile(hip_ctx, spec, prec):
 C1_2L = replace(synth.C1, config=replace(synth.C1.config, layer_count=2, context_length=4352), name="c1-shape-2l")
 
 
-@pytest.mark.parametrize("prec", ["fast", "fast-f16"])
+@pytest.mark.parametrize("prec,rows", [("fast", "all"), ("fast", "last"), ("fast-f16", "last")])
 @pytest.mark.parametrize("spec", [C1_2L, C4_LONG, synth.with_dtype(replace(C1_2L, name="c1-shape-2l-f16"), F16)],
                          ids=lambda s: s.name)
-def test_two_stream_prefill_matches_one_stream(hip_ctx, spec, prec):
+def test_two_stream_prefill_matches_one_stream(hip_ctx, spec, prec, rows):
     """A fast prefill chunk of at least 1,536 tokens whose QKV GEMM grid is at
     most two rounds of 128x64 tiles runs as two halves on two
     streams (the second half's attention of each layer waits for the first
     half's K/V rows).  Every row goes through the same arithmetic as in one
     stream, but a half's smaller grids may take other tiles: the GEMM's
     two-K-set 64x64 tiles and the flash kernel's other key-range split each
-    change the float32 summation order, so the halves agree to rounding, not
-    bit for bit.  So the logits
-    and the decode steps that read the cache must agree with
-    ALPACA_HIP_PREFILL_STREAMS=1 (read per call) to 1e-5 of the logit peak: a
-    1600-token chunk (halves of 768 and 832 rows, just past the 1,536-token
-    threshold), one 3100-token chunk (uneven halves), then a 4300-token prompt
-    over chunks of 3200 (a split chunk, then a short one at position 3200)."""
+    change the float32 summation order.  With every row's activations in two
+    f16 terms (ALPACA_HIP_LO_ROWS=all) that order is all that differs, so the
+    logits and the decode steps that read the cache agree with
+    ALPACA_HIP_PREFILL_STREAMS=1 (read per call) to 1e-5 of the logit peak.
+    By default only the QKV input and the rows from the last row rounded down
+    to a multiple of 256 (the same rows in both runs: the split point is a
+    multiple of 256) take two terms; a float32 value that differs in its last
+    bit can then round to the neighbouring f16 (2^-11 relative) in the one-term
+    rows, so the runs agree to 2.5e-4 of the peak, and each is held to the
+    CPU oracle at full size by the C1P workload test.  (One-term activations
+    throughout, fast-f16, never take the two-K-set tiles, and agree to 1e-5.)
+    Cases: a 1600-token
+    chunk (halves of 768 and 832 rows, just past the 1,536-token threshold),
+    one 3100-token chunk (uneven halves), then a 4300-token prompt over chunks
+    of 3200 (a split chunk, then a short one at position 3200)."""
+    tol = 1e-5 if rows == "all" or prec == "fast-f16" else 2.5e-4
     model = HIPLlamaModel(hip_ctx, spec.config, built(spec))
     prompt = synth.prompt_tokens(spec, 4300)
     for n in (1600, 3100, 4300):
         out = {}
         for streams in ("1", "2"):
-            s = model.make_session(capacity=4352, max_batch=3200, gemm_precision=prec)
+            with env(ALPACA_HIP_LO_ROWS=rows):
+                s = model.make_session(capacity=4352, max_batch=3200, gemm_precision=prec)
             with env(ALPACA_HIP_PREFILL_STREAMS=streams):
                 g = s.forward(prompt[:n])
             tok = int(np.argmax(g))
@@ -152,8 +162,9 @@ def test_two_stream_prefill_matches_one_stream(hip_ctx, spec, prec):
             s.close()
         for k, (a, b) in enumerate(zip(out["1"], out["2"])):
             d = float(np.abs(a - b).max())
-            print(f"[metrics] {spec.name} {prec} n={n} step {k}: two streams vs one max |d| {d:.2e}")
-            assert d <= 1e-5 * float(np.abs(a).max()), f"{spec.name} {prec} n={n} step {k}: max |d| {d:.3e}"
+            print(f"[metrics] {spec.name} {prec} rows={rows} n={n} step {k}: two streams vs one max |d| {d:.2e} "
+                  f"({d / float(np.abs(a).max()):.2e} of the peak)")
+            assert d <= tol * float(np.abs(a).max()), f"{spec.name} {prec} {rows} n={n} step {k}: max |d| {d:.3e}"
             assert int(np.argmax(a)) == int(np.argmax(b))
     model.close()
 
