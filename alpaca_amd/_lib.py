@@ -188,6 +188,8 @@ SIGNATURES = {
     "ahip_dev_gemv": (i, [vp, vp, vp, vp, i, dp]),
     "ahip_dev_gemm": (i, [vp, vp, vp, i, vp, i, i, dp]),
     "ahip_dev_attention": (i, [vp, vp, vp, vp, i, i, i, i, i, vp, i, dp]),
+    "ahip_dev_gemv_cycle": (i, [vp, C.POINTER(vp), i, vp, vp, i, dp]),
+    "ahip_dev_attention_decode": (i, [vp, vp, vp, vp, i, i, i, i, i, vp, i, dp]),
 }
 
 _lib = None

@@ -524,23 +524,32 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const float* q, int ld
     }
 }
 
-// Merges per-split (max, sum, unnormalised output) triples.
+// Merges per-split (max, sum, unnormalised output) triples (at most 64
+// splits): the first wave takes one split per lane for the weights
+// exp(m_s - M) and the weighted sum of the row sums, so the splits' statistics
+// load in parallel; then each thread sums its output element over the splits
+// with the weights from LDS, several splits' loads in flight at a time.
 __global__ void attn_merge_kernel(const float* partials, int H, int hd, int splits, float* out) {
+    __shared__ float wsh[64];
+    __shared__ float lsh;
     const int th = blockIdx.x;  // t * H + h
     const float* pp = partials + (int64_t)th * splits * (hd + 2);
-    float mx = -INFINITY;
-    for (int s = 0; s < splits; s++) mx = fmaxf(mx, pp[s * (hd + 2)]);
-    float l = 0.f;
-    for (int s = 0; s < splits; s++) {
-        const float ms = pp[s * (hd + 2)];
-        if (ms != -INFINITY) l += pp[s * (hd + 2) + 1] * expf(ms - mx);
+    if (threadIdx.x < 64) {
+        const int s = threadIdx.x;
+        const float ms = s < splits ? pp[s * (hd + 2)] : -INFINITY;
+        const float ls = s < splits ? pp[s * (hd + 2) + 1] : 0.f;
+        const float mx = wave_max(ms);
+        const float w = ms == -INFINITY ? 0.f : expf(ms - mx);
+        wsh[s] = w;
+        const float l = wave_sum(ls * w);
+        if (s == 0) lsh = l;
     }
+    __syncthreads();
+    const float l = lsh;
     for (int d = threadIdx.x; d < hd; d += blockDim.x) {
         float acc = 0.f;
-        for (int s = 0; s < splits; s++) {
-            const float ms = pp[s * (hd + 2)];
-            if (ms != -INFINITY) acc += pp[s * (hd + 2) + 2 + d] * expf(ms - mx);
-        }
+#pragma unroll 8
+        for (int s = 0; s < splits; s++) acc += pp[s * (hd + 2) + 2 + d] * wsh[s];
         out[(int64_t)th * hd + d] = acc / l;
     }
 }
@@ -768,6 +777,7 @@ hipError_t launch_attention_decode(const float* q, const void* kc, const void* v
 }
 
 hipError_t launch_attention_merge(const float* partials, int heads, int hd, int splits, float* out, hipStream_t st) {
+    if (splits < 1 || splits > 64) return hipErrorInvalidValue;  // one split per lane of a wave
     int bt = hd < 64 ? 64 : (hd > 256 ? 256 : (hd + 63) / 64 * 64);
     attn_merge_kernel<<<heads, bt, 0, st>>>(partials, heads, hd, splits, out);
     return hipGetLastError();
@@ -800,7 +810,7 @@ hipError_t launch_attention_generic(const float* q, int ldq, const void* kc, con
                                     int capacity, int tokens, int heads, int kv_heads, int hd, int start,
                                     int splits, float* partials, float* out, hipStream_t st) {
     if (tokens <= 0) return hipSuccess;
-    if (hd > kMaxHD) return hipErrorInvalidValue;
+    if (hd > kMaxHD || splits < 1 || splits > 64) return hipErrorInvalidValue;
     const int max_len = start + tokens;
     int split_len = (max_len + splits - 1) / splits;
     split_len = (split_len + 63) / 64 * 64;

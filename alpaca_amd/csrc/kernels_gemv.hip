@@ -23,6 +23,9 @@
 #include "common.h"
 #include "gemv_chunks.h"
 
+#include <algorithm>
+#include <cstdlib>
+
 namespace {
 
 using gemv::RowStream;
@@ -167,6 +170,115 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     }
 }
 
+// Tall matrices (the logits, large FFN matrices): a grid of resident
+// workgroups walks tiles of kWaves * 64 / LPR rows.  LPR lanes own a row and
+// each takes CPL chunks of it (LPR * CPL covers the row with few clamped
+// extra loads), so one batch of CPL 16-byte loads per lane holds the whole
+// tile; the batch of the workgroup's next tile is issued before the current
+// one is multiplied, so every wave keeps a batch in flight while it computes,
+// and the input row is staged once per workgroup instead of once per tile.
+template <int FMT, int LPR, int CPL, int MODE, int INP>
+__global__ __launch_bounds__(kThreads) void gemv_tall_kernel(GemvArgs a, int tiles) {
+    extern __shared__ float xs[];
+    __shared__ float red[16];
+    constexpr int RPW = 64 / LPR, RT = kWaves * RPW;
+    const int K = a.w.cols, nch = chunks_of<FMT>(K), rows = a.w.rows;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane % LPR;
+    const int rin = wave * RPW + lane / LPR;  // this lane group's row within a tile
+    constexpr int NM = MODE == GEMV_SWIGLU ? 2 : 1;
+    int4 q[2][NM][CPL];
+    float d[2][NM][CPL];
+    auto load = [&](int t, int b) {
+        const int64_t row = min((int64_t)t * RT + rin, (int64_t)rows - 1);
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int u = 0; u < CPL; u++) {
+                const int c = li + u * LPR;
+                gemv::load_chunk<FMT>(m ? a.u : a.w, row, K, c < nch ? c : nch - 1, q[b][m][u], d[b][m][u]);
+            }
+    };
+    int t = blockIdx.x;
+    if (t < tiles) load(t, 0);
+    stage_input<INP>(a.in, K, xs, red);
+    auto step = [&](int b) {
+        const int nt = t + gridDim.x;
+        if (nt < tiles) load(nt, b ^ 1);
+        float acc[NM];
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            acc[m] = 0.f;
+#pragma unroll
+            for (int u = 0; u < CPL; u++) {
+                const int c = li + u * LPR;
+                if (c < nch) acc[m] += gemv::chunk_dot<FMT>(q[b][m][u], d[b][m][u], c, xs);
+            }
+            acc[m] = lane_sum<LPR>(acc[m]);
+        }
+        const int64_t row = (int64_t)t * RT + rin;
+        if (row < rows && li == 0) {
+            if (MODE == GEMV_STORE) a.out[row] = acc[0];
+            else if (MODE == GEMV_ADD) a.out[row] += acc[0];
+            else a.out[row] = (acc[0] / (1.0f + expf(-acc[0]))) * acc[NM - 1];
+        }
+        t = nt;
+    };
+    // the two register sets alternate; the loop is unrolled over both so they stay in registers
+    while (t < tiles) {
+        step(0);
+        if (t >= tiles) break;
+        step(1);
+    }
+}
+
+// (LPR, CPL) for a row of nch chunks: the fewest lanes per row whose batch of
+// at most 8 chunks per lane covers the row (tiles of more rows, more loads per
+// lane in flight), CPL then as small as that allows.
+struct TallShape {
+    int lpr = 0, cpl = 0;
+};
+inline TallShape tall_shape(int nch) {
+    for (int lpr = 4; lpr <= 64; lpr *= 2) {
+        const int cpl = (nch + lpr - 1) / lpr;
+        if (cpl <= 8) return {lpr, cpl <= 4 ? 4 : cpl <= 5 ? 5 : 8};
+    }
+    return {};
+}
+
+template <int FMT, int LPR, int CPL, int MODE, int INP>
+hipError_t run_tall(const GemvArgs& a, hipStream_t st) {
+    static int per_cu[64] = {0};
+    int dev = 0;
+    hipGetDevice(&dev);
+    const size_t lds = (size_t)a.w.cols * sizeof(float);
+    int& occ = per_cu[dev & 63];
+    if (!occ) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_tall_kernel<FMT, LPR, CPL, MODE, INP>, kThreads,
+                                                         lds) != hipSuccess || n < 1) {
+            hipGetLastError();
+            n = 1;
+        }
+        occ = n;
+    }
+    int cus = 0;
+    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    const int rt = kWaves * (64 / LPR), tiles = (a.w.rows + rt - 1) / rt;
+    const int grid = std::min(tiles, std::max(1, cus) * occ);
+    gemv_tall_kernel<FMT, LPR, CPL, MODE, INP><<<grid, kThreads, lds, st>>>(a, tiles);
+    return hipGetLastError();
+}
+
+template <int FMT, int MODE, int INP>
+hipError_t dispatch_tall(const TallShape& ts, const GemvArgs& a, hipStream_t st) {
+#define TALL(L, CP) \
+    if (ts.lpr == L && ts.cpl == CP) return run_tall<FMT, L, CP, MODE, INP>(a, st);
+    TALL(4, 4) TALL(4, 5) TALL(4, 8) TALL(8, 4) TALL(8, 5) TALL(8, 8) TALL(16, 4) TALL(16, 5) TALL(16, 8)
+    TALL(32, 4) TALL(32, 5) TALL(32, 8) TALL(64, 4) TALL(64, 5) TALL(64, 8)
+#undef TALL
+    return hipErrorInvalidValue;
+}
+
 template <int FMT, int MODE, int INP>
 hipError_t dispatch(int lpr, const GemvArgs& a, hipStream_t st) {
     const int rows_per_block = kWaves * (64 / lpr);
@@ -194,6 +306,11 @@ hipError_t dispatch_fmt(int lpr, int mode, int inp, const GemvArgs& a, hipStream
 
 }  // namespace
 
+template <int FMT>
+constexpr int gemv_nch(int K) {
+    return FMT == DT_Q8_0 ? K / 16 : FMT == DT_Q4_0 ? K / 32 : K / 8;
+}
+
 // Lanes per row: enough workgroups to cover the chip for tall matrices, whole
 // waves per row for short ones (the decode matrices of small models are
 // latency-bound, so more rows in flight matter more than lane utilisation).
@@ -201,6 +318,28 @@ static int pick_lpr(int rows) {
     if ((rows + 15) / 16 >= 1024) return 16;
     if ((rows + 7) / 8 >= 1024) return 32;
     return 64;
+}
+
+// Whether a matrix takes the tall kernel: at least 4 MB of weights, and a row
+// that one batch of at most 8 chunks per lane on 64 lanes covers.
+static bool tall_pays(const DevMatrix& w) {
+    const int64_t bytes = w.dtype == DT_Q8_0   ? (int64_t)w.rows * w.cols / 32 * 34
+                          : w.dtype == DT_Q4_0 ? (int64_t)w.rows * w.cols / 32 * 18
+                                               : (int64_t)w.rows * w.cols * 2;
+    const int nch = w.dtype == DT_Q8_0 ? w.cols / 16 : w.dtype == DT_Q4_0 ? w.cols / 32 : w.cols / 8;
+    const char* e = std::getenv("ALPACA_HIP_GEMV_TALL");  // tuning: 0 keeps the one-tile-per-workgroup kernel
+    if (e && e[0] == '0') return false;
+    return bytes >= (4 << 20) && nch <= 64 * 8;
+}
+
+template <int FMT>
+hipError_t dispatch_tall_fmt(int mode, int inp, const GemvArgs& a, hipStream_t st) {
+    const TallShape ts = tall_shape(gemv_nch<FMT>(a.w.cols));
+    if (mode == GEMV_STORE) return inp == IN_NORM ? dispatch_tall<FMT, GEMV_STORE, IN_NORM>(ts, a, st)
+                                                  : dispatch_tall<FMT, GEMV_STORE, IN_X>(ts, a, st);
+    if (mode == GEMV_ADD) return dispatch_tall<FMT, GEMV_ADD, IN_X>(ts, a, st);
+    return inp == IN_NORM ? dispatch_tall<FMT, GEMV_SWIGLU, IN_NORM>(ts, a, st)
+                          : dispatch_tall<FMT, GEMV_SWIGLU, IN_X>(ts, a, st);
 }
 
 hipError_t launch_gemv_ex(const DevMatrix& w, const DevMatrix* w_up, const GemvInput& in, const GemvRope* rope,
@@ -216,6 +355,13 @@ hipError_t launch_gemv_ex(const DevMatrix& w, const DevMatrix* w_up, const GemvI
     a.in = in;
     if (rope) a.rope = *rope;
     a.out = out;
+    if (mode != GEMV_QKV_ROPE && inp != IN_MERGE && tall_pays(w)) {
+        switch (w.dtype) {
+        case DT_Q8_0: return dispatch_tall_fmt<DT_Q8_0>(mode, inp, a, st);
+        case DT_Q4_0: return dispatch_tall_fmt<DT_Q4_0>(mode, inp, a, st);
+        default: return dispatch_tall_fmt<DT_F16>(mode, inp, a, st);
+        }
+    }
     const int lpr = pick_lpr(w.rows);
     switch (w.dtype) {
     case DT_Q8_0: return dispatch_fmt<DT_Q8_0>(lpr, mode, inp, a, st);

@@ -2218,6 +2218,40 @@ extern "C" int ahip_dev_gemv(ahip_context* ctx, void* weight, const float* dx, f
     });
 }
 
+extern "C" int ahip_dev_gemv_cycle(ahip_context* ctx, void* const* weights, int count, const float* dx, float* dy,
+                                   int iters, double* avg) {
+    if (!ctx || !weights || count <= 0 || !dx || !dy || iters < 0) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad argument");
+    for (int k = 0; k < count; k++)
+        if (!weights[k]) return fail(AHIP_ERR_INVALID_ARGUMENT, "null weight");
+    HIP_OR(hipSetDevice(ctx->device), "hipSetDevice");
+    int i = 0;
+    return time_launches(ctx, iters, avg, [&](hipStream_t st) {
+        const DevMatrix& w = ((OwnedMatrix*)weights[i++ % count])->m;
+        return launch_gemv(w, nullptr, dx, nullptr, 0.f, dy, GEMV_STORE, st);
+    });
+}
+
+extern "C" int ahip_dev_attention_decode(ahip_context* ctx, const float* dq, const void* dkc, const void* dvc,
+                                         int capacity, int length, int heads, int kv_heads, int hd, float* dout,
+                                         int iters, double* avg) {
+    if (!ctx || !dq || !dkc || !dvc || !dout || length <= 0 || length > capacity || kv_heads <= 0 ||
+        heads % kv_heads || iters < 0)
+        return fail(AHIP_ERR_INVALID_ARGUMENT, "bad argument");
+    if (!attention_decode_supported(heads, kv_heads, hd) ||
+        attention_decode_split_len(capacity) > attention_decode_max_split_len())
+        return fail(AHIP_ERR_UNSUPPORTED, "decode attention shape");
+    HIP_OR(hipSetDevice(ctx->device), "hipSetDevice");
+    const int sl = attention_decode_split_len(capacity), splits = (length - 1 + sl) / sl;
+    DevBuf part;
+    if (int rc = part.alloc((size_t)heads * splits * (hd + 2) * 4)) return rc;
+    return time_launches(ctx, iters, avg, [&](hipStream_t st) {
+        hipError_t e = launch_attention_decode(dq, dkc, dvc, 1, capacity, heads, kv_heads, hd, length, nullptr, sl,
+                                               splits, part.as<float>(), st);
+        if (e != hipSuccess) return e;
+        return launch_attention_merge(part.as<float>(), heads, hd, splits, dout, st);
+    });
+}
+
 extern "C" int ahip_dev_gemm(ahip_context* ctx, void* weight, const float* dx, int m, float* dy, int precision,
                              int iters, double* avg) {
     if (!ctx || !weight || !dx || !dy || m <= 0 || iters < 0) return fail(AHIP_ERR_INVALID_ARGUMENT, "bad argument");

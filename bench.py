@@ -22,8 +22,9 @@ embeddings), random-init synthetic weights, all resident in HBM.
   * roofline_prefill: the dominant prefill GEMM (MFMA, f16 operands, f32
     accumulate): algorithmic FLOPs per launch / mean launch time from the
     session's per-stage HIP events; peak 2.5 PFLOP/s dense fp16.  issued_frac
-    doubles it: the default prefill enters activations as two f16 terms, so
-    the MFMA units execute twice the algorithmic multiply-adds.
+    counts the MFMA work issued: the QKV GEMM takes its activations as two f16
+    terms on every row (twice the multiply-adds), the other GEMMs on the
+    prompt's last 256 rows only.
   * prefill_mfma_frac: the whole 4096-token prefill (projections + causal
     attention, algorithmic FLOPs) over its wall time, against the same peak.
   * prefill_weight_cache: the same prefill on a model created with the
@@ -43,6 +44,14 @@ embeddings), random-init synthetic weights, all resident in HBM.
     CPU-runnable case (a 128-token prompt, then 16
     greedy tokens) as prefill and decode tok/s; nproc and the CPU model are
     recorded.
+  * kernels: isolated-kernel figures on device-resident inputs (ahip_dev_*):
+    the decode GEMV's GB/s per matrix shape (C1's projections and logits, the
+    C4 and C5 FFN matrices), warm (Infinity-Cache resident) and cold (cycling
+    over copies larger than the cache); C2's two isolated GEMMs' MFMA
+    fraction; C3's flash attention (T = 4096) and decode attention (one query
+    over 2048 rows).  decode_cache_check: a C1 decode launch's GPU time with the
+    previous token's data in the 256 MB Infinity Cache and after evicting it.
+    --kernels-only prints just the kernel figures (for kernel traces).
   * roofline.traffic: HBM bytes per decode launch from the committed counter
     summary (profiles/c1_decode_hbm_counters.md), used only when the summary
     was measured on the decode kernel's current sources (it records a hash of
@@ -166,8 +175,183 @@ def other_config(ctx, spec, ctx_len: int, prefill_tokens: int, steps: int = 64, 
             "prefill_note": "wall clock of forward, GEMMs + causal attention + last-token logits",
             "prefill_stages": stages,
             "prefill_stages_note": ("one profiled one-stream prefill; frac = algorithmic 2*M*N*K (attention: "
-                                    "causal QK^T + PV) per launch / launch time / 2.5 PFLOP/s; the two-term "
-                                    "activations issue twice that MFMA work") if stages else None}
+                                    "causal QK^T + PV) per launch / launch time / 2.5 PFLOP/s; the QKV GEMM "
+                                    "issues twice that MFMA work (two-term input on every row), the others about "
+                                    "that (two terms on the last 256 rows)") if stages else None}
+
+
+class DevBuffers:
+    """Device buffers through the C ABI's thin shim (ahip_malloc / ahip_memcpy_htod), freed together."""
+
+    def __init__(self, ctx):
+        self.ctx, self.ptrs = ctx, []
+
+    def put(self, arr) -> "object":
+        import ctypes as C
+
+        from alpaca_amd import _lib as L
+        p = C.c_void_p()
+        L.check(L.lib().ahip_malloc(self.ctx.handle, max(int(arr.nbytes), 4), C.byref(p)))
+        self.ptrs.append(p)
+        L.check(L.lib().ahip_memcpy_htod(self.ctx.handle, p, arr.ctypes.data, arr.nbytes))
+        return p
+
+    def empty(self, nbytes: int):
+        import ctypes as C
+
+        from alpaca_amd import _lib as L
+        p = C.c_void_p()
+        L.check(L.lib().ahip_malloc(self.ctx.handle, max(int(nbytes), 4), C.byref(p)))
+        self.ptrs.append(p)
+        return p
+
+    def close(self) -> None:
+        from alpaca_amd import _lib as L
+        for p in self.ptrs:
+            L.lib().ahip_free(self.ctx.handle, p)
+        self.ptrs = []
+
+
+# Decode GEMV shapes (rows, cols, format) whose kernel-level rate is reported:
+# C1's projections and tied logits, C4's FFN matrix and C5's FFN matrix.
+GEMV_SHAPES = (("C1 qkv", 960, 576, "q8_0"), ("C1 wo", 576, 576, "q8_0"), ("C1 gate (or up)", 1536, 576, "q8_0"),
+               ("C1 down", 576, 1536, "q8_0"), ("C1 logits", 49152, 576, "q8_0"),
+               ("C4 gate (or up)", 2560, 960, "q4_0"), ("C5 gate (or up)", 8192, 2048, "q8_0"),
+               ("C5 down", 2048, 8192, "q8_0"))
+MALL_BYTES = 256 << 20  # MI355X Infinity Cache
+
+
+def kernel_figures(ctx, iters: int = 200) -> dict:
+    """Isolated-kernel figures on device-resident inputs, timed with HIP events
+    around back-to-back launches (ahip_dev_*): the decode GEMV per matrix shape
+    warm (one matrix, which stays in the 256 MB Infinity Cache once read) and
+    cold (launches cycle over copies totalling more than twice that cache, so
+    each streams from HBM); C2's two isolated GEMMs; C3's flash attention and
+    decode attention."""
+    import ctypes as C
+
+    import numpy as np
+
+    from alpaca_amd import _lib as L
+    from alpaca_amd import synth
+    from alpaca_amd.tensor import Q4_0, Q8_0, encode
+    lib = L.lib()
+    bufs = DevBuffers(ctx)
+    out = {"timing": f"HIP events around {iters} back-to-back launches on the context stream (ahip_dev_*)"}
+    try:
+        rows = []
+        for name, n, k, fmt in GEMV_SHAPES:
+            dt = Q8_0 if fmt == "q8_0" else Q4_0
+            w = encode(synth.normal(synth.tensor_seed(9, n + k), n * k, 0.02).reshape(n, k), dt)
+            wbytes = n * k // 32 * (34 if fmt == "q8_0" else 18)
+            moved = wbytes + 4 * k + 4 * n
+            copies = max(1, -(-2 * MALL_BYTES // wbytes))
+            handles = []
+            for _ in range(copies):
+                h = C.c_void_p()
+                L.check(lib.ahip_dev_pack_weight(ctx.handle, dt, w.data.ctypes.data, n, k, C.byref(h)))
+                handles.append(h)
+            dx = bufs.put(synth.normal(synth.tensor_seed(9, 7), k, 1.0))
+            dy = bufs.empty(4 * n)
+            warm, cold = C.c_double(), C.c_double()
+            arr = (C.c_void_p * copies)(*[h.value for h in handles])
+            L.check(lib.ahip_dev_gemv_cycle(ctx.handle, arr, 1, dx, dy, 20, C.byref(warm)))  # untimed warm-up
+            L.check(lib.ahip_dev_gemv_cycle(ctx.handle, arr, 1, dx, dy, iters, C.byref(warm)))
+            L.check(lib.ahip_dev_gemv_cycle(ctx.handle, arr, copies, dx, dy, max(iters, 2 * copies), C.byref(cold)))
+            for h in handles:
+                lib.ahip_dev_weight_free(ctx.handle, h)
+            rows.append({"matrix": name, "shape": f"{n}x{k} {fmt}", "bytes": moved,
+                         "warm_us": round(warm.value * 1e6, 3), "warm_GBs": round(moved / warm.value / 1e9, 1),
+                         "cold_us": round(cold.value * 1e6, 3), "cold_GBs": round(moved / cold.value / 1e9, 1),
+                         "cold_hbm_frac": round(moved / cold.value / 1e9 / HBM_PEAK_GBS, 4), "cold_copies": copies})
+        out["gemv"] = rows
+        out["gemv_note"] = ("gemv_kernel (the multi-kernel decode's GEMV; the persistent decode kernel runs the same "
+                            "per-chunk dot products inside its phases): bytes = quantised weights + f32 input + f32 "
+                            "output; warm repeats one matrix (Infinity Cache resident once read), cold cycles over "
+                            "copies totalling over 512 MB; hbm_frac against 8 TB/s")
+        # C2: the two isolated Q8_0 GEMMs (M = 2048), fp32 A and C
+        gem = []
+        for n, k in ((1536, 576), (576, 1536)):
+            x, w = synth.c2_gemm_case(n, k)
+            m = x.shape[0]
+            h = C.c_void_p()
+            L.check(lib.ahip_dev_pack_weight(ctx.handle, w.dtype, w.data.ctypes.data, n, k, C.byref(h)))
+            dx, dy = bufs.put(np.ascontiguousarray(x)), bufs.empty(4 * m * n)
+            flops = 2 * m * n * k
+            row = {"shape": f"M={m} N={n} K={k} q8_0", "flops": flops}
+            for prec, code, issued in (("fast", L.GEMM_FAST, 2), ("fast_f16", L.GEMM_FAST_F16, 1),
+                                       ("exact", L.GEMM_EXACT, 1)):
+                t = C.c_double()
+                L.check(lib.ahip_dev_gemm(ctx.handle, h, dx, m, dy, code, 5, C.byref(t)))
+                L.check(lib.ahip_dev_gemm(ctx.handle, h, dx, m, dy, code, 50, C.byref(t)))
+                tf = flops / t.value / 1e12
+                row[prec] = {"us": round(t.value * 1e6, 2), "TFLOPs": round(tf, 1),
+                             "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                             "issued_frac": round(issued * tf / MFMA_F16_PEAK_TFLOPS, 4)}
+            lib.ahip_dev_weight_free(ctx.handle, h)
+            gem.append(row)
+        out["c2_gemm"] = gem
+        out["c2_note"] = ("frac = 2*M*N*K / time / 2.5 PFLOP/s dense f16; issued_frac counts the MFMA work issued "
+                          "(fast: two activation terms on every row, twice the algorithmic; exact is SIMT float32)")
+        # C3: causal GQA flash attention at T = 4096 (one f16 term for Q and P, as the
+        # prefill's query blocks before the last row's), and decode of one query over 2048 rows
+        q, kk, v = synth.c3_attention_case()
+        T, H, KVH, hd = q.shape[0], q.shape[1], kk.shape[1], q.shape[2]
+        dq, dk, dv = bufs.put(np.ascontiguousarray(q)), bufs.put(np.ascontiguousarray(kk)), bufs.put(np.ascontiguousarray(v))
+        do = bufs.empty(4 * T * H * hd)
+        t = C.c_double()
+        L.check(lib.ahip_dev_attention(ctx.handle, dq, dk, dv, T, H, KVH, hd, 0, do, 3, C.byref(t)))
+        L.check(lib.ahip_dev_attention(ctx.handle, dq, dk, dv, T, H, KVH, hd, 0, do, 30, C.byref(t)))
+        af = 2 * hd * H * T * (T + 1)
+        out["c3_prefill_attention"] = {"us": round(t.value * 1e6, 2), "flops": af,
+                                       "TFLOPs": round(af / t.value / 1e12, 1),
+                                       "frac": round(af / t.value / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                                       "kernel": "flash_attn_kernel, one f16 term for Q and P"}
+        L_vis = 2048
+        kc = np.ascontiguousarray(kk.transpose(1, 0, 2))  # [kv_heads][capacity][hd]
+        vc = np.ascontiguousarray(v.transpose(1, 0, 2))
+        dkc, dvc = bufs.put(kc), bufs.put(vc)
+        dq1 = bufs.put(np.ascontiguousarray(q[L_vis - 1].astype(np.float32)))
+        do1 = bufs.empty(4 * H * hd)
+        L.check(lib.ahip_dev_attention_decode(ctx.handle, dq1, dkc, dvc, T, L_vis, H, KVH, hd, do1, 20, C.byref(t)))
+        L.check(lib.ahip_dev_attention_decode(ctx.handle, dq1, dkc, dvc, T, L_vis, H, KVH, hd, do1, iters, C.byref(t)))
+        ab = 2 * L_vis * KVH * hd * 2
+        out["c3_decode_attention"] = {"us": round(t.value * 1e6, 3), "bytes": ab,
+                                      "GBs": round(ab / t.value / 1e9, 1),
+                                      "hbm_frac": round(ab / t.value / 1e9 / HBM_PEAK_GBS, 4),
+                                      "kernel": "attn_decode_split_kernel + attn_merge_kernel (one query, "
+                                                "2048 visible f16 rows of 3 KV heads)"}
+    finally:
+        bufs.close()
+    return out
+
+
+def mall_check(ctx, session, token: int, steps: int = 24) -> dict:
+    """Whether the Infinity Cache serves a C1 decode token's 190 MB: the
+    persistent launch's GPU time (HIP events of the call) with the previous
+    token's data left in the cache, against the same launch after 1 GiB of
+    device writes evicted it."""
+    import ctypes as C
+
+    import numpy as np
+
+    from alpaca_amd import _lib as L
+    bufs = DevBuffers(ctx)
+    try:
+        ev = bufs.empty(1 << 30)
+        warm, cold = [], []
+        for i in range(steps):
+            if i % 2:
+                L.check(L.lib().ahip_memset(ctx.handle, ev, i & 0xFF, 1 << 30))
+            logits = session.decode(token)
+            (cold if i % 2 else warm).append(session.last_gpu_seconds)
+            token = int(np.argmax(logits))
+        w, c = float(np.median(warm[1:])), float(np.median(cold[1:]))
+        return {"warm_us": round(w * 1e6, 1), "after_eviction_us": round(c * 1e6, 1), "ratio": round(c / w, 3),
+                "note": "decode() GPU time per launch; 'after eviction' follows 1 GiB of device writes (4x the "
+                        "256 MB Infinity Cache)"}
+    finally:
+        bufs.close()
 
 
 def stage_table(profile: dict, units: dict, scale: float, unit: str, per: int = 1) -> dict:
@@ -339,6 +523,9 @@ def main() -> int:
     ap.add_argument("--prefill-only", action="store_true",
                     help="only --prefill-runs unprofiled 4096-token prefills of --config (for counter passes and "
                          "traces of the prefill kernels)")
+    ap.add_argument("--no-kernels", action="store_true", help="skip the isolated-kernel figures and the cache check")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="only the isolated-kernel figures (GEMV per shape, C2 GEMMs, C3 attention), for traces")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only a device-to-device copy of 256 MiB, the reference the HBM byte counters are scaled by")
     ap.add_argument("--counter-summary", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
@@ -373,6 +560,12 @@ def main() -> int:
 
     from alpaca_amd import synth
     from alpaca_amd.model import HIPContext, HIPLlamaModel
+
+    if args.kernels_only:
+        kctx = HIPContext(0)
+        print(json.dumps({"kernels": kernel_figures(kctx)}), flush=True)
+        kctx.close()
+        return 0
 
     # --config picks another BASELINE config for a --decode-only run (counter passes of its decode)
     spec = {"C1": synth.C1, "C4": synth.C4, "C5": synth.C5}[args.config]
@@ -494,12 +687,15 @@ def main() -> int:
         gemm_s = sum(profp[k].seconds for k in profp if k in fl and k != "attention")
         gemm_f = sum(fl[k] * profp[k].dispatches for k in profp if k in fl and k != "attention")
         roof_p["all_prefill_gemms_frac"] = round(gemm_f / gemm_s / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
-        # The default prefill enters the activations as two f16 terms (hi + lo), so each
-        # algorithmic multiply-add is issued twice on the MFMA units (QK^T and PV likewise).
-        roof_p["issued_frac"] = round(2 * roof_p["frac"], 4)
-        roof_p["all_prefill_gemms_issued_frac"] = round(2 * roof_p["all_prefill_gemms_frac"], 4)
-        roof_p["note"] = ("frac counts 2*M*N*K algorithmic FLOPs per GEMM; issued_frac counts the MFMA work the "
-                          "two-term activations actually issue (twice that), both against 2.5 PFLOP/s dense f16")
+        # MFMA work issued per algorithmic multiply-add: the QKV input enters as two f16 terms on
+        # every row, the other GEMMs' inputs on the last 256 rows of the prompt only.
+        issue = lambda k: 2.0 if k == "qkv projections" else 1.0 + 256 / PREFILL_TOKENS  # noqa: E731
+        roof_p["issued_frac"] = round(issue(domp) * roof_p["frac"], 4)
+        gemm_fi = sum(issue(k) * fl[k] * profp[k].dispatches for k in profp if k in fl and k != "attention")
+        roof_p["all_prefill_gemms_issued_frac"] = round(gemm_fi / gemm_s / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
+        roof_p["note"] = ("frac counts 2*M*N*K algorithmic FLOPs per GEMM; issued_frac the MFMA work issued (the QKV "
+                          "GEMM takes two f16 activation terms on every row, the others on the last 256 rows), "
+                          "both against 2.5 PFLOP/s dense f16")
         log(f"prefill dominant GEMM: {domp} {ach:.1f} TFLOP/s")
 
     # ---------------------------------------------------------------- prefill with the weight cache
@@ -541,6 +737,24 @@ def main() -> int:
             log(f"{key}: decode {others[key]['decode_tok_s']} tok/s at ctx {ctx_len} "
                 f"({100 * others[key]['decode_hbm_frac']:.1f}% of HBM), prefill {others[key]['prefill_tok_s']} tok/s")
 
+    # ---------------------------------------------------------------- isolated kernels, cache check
+    kernels, mall = None, None
+    if not args.no_kernels:
+        kernels = kernel_figures(ctx)
+        for r in kernels["gemv"]:
+            log(f"gemv {r['matrix']} {r['shape']}: warm {r['warm_GBs']} GB/s, cold {r['cold_GBs']} GB/s "
+                f"({100 * r['cold_hbm_frac']:.1f}% of HBM)")
+        for r in kernels["c2_gemm"]:
+            log(f"C2 {r['shape']}: fast {r['fast']['TFLOPs']} TFLOP/s ({100 * r['fast']['frac']:.1f}%), "
+                f"fast-f16 {r['fast_f16']['TFLOPs']}")
+        log(f"C3 flash {kernels['c3_prefill_attention']['TFLOPs']} TFLOP/s, decode attention "
+            f"{kernels['c3_decode_attention']['GBs']} GB/s")
+        ms = model.make_session(capacity=DECODE_CTX + 64, max_batch=PREFILL_TOKENS)
+        mt = int(np.argmax(ms.forward(prompt[:DECODE_CTX])))
+        mall = mall_check(ctx, ms, mt)
+        ms.close()
+        log(f"decode launch {mall['warm_us']} us warm, {mall['after_eviction_us']} us after evicting the cache")
+
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
     if not args.no_cpu_baseline:
@@ -560,8 +774,9 @@ def main() -> int:
                    "layers": c.layer_count, "hidden": c.hidden_size, "heads": f"{c.head_count}/{c.kv_head_count}",
                    "head_dim": c.head_dim, "ffn": c.feed_forward_size, "vocab": c.vocab_size,
                    "kv_cache": "f16",
-                   "prefill_precision": "fast: f16 MFMA, activations as two f16 terms (hi + lo), exact integer "
-                                        "quants, per-block f32 scaling, f32 accumulate",
+                   "prefill_precision": "fast: f16 MFMA with exact integer quants, per-block f32 scaling and f32 "
+                                        "accumulation; activations as two f16 terms (hi + lo) for the QKV input "
+                                        "and on the prompt's last 256 rows, one term elsewhere",
                    "greedy_depth": args.depth},
         "prefill_tok_s": round(prefill_tok_s, 1),
         "prefill_mfma_frac": round(c.layer_count * sum(prefill_stage_flops(c, PREFILL_TOKENS).values()) *
@@ -571,6 +786,7 @@ def main() -> int:
         "decode_ms_per_token": round(el / args.steps * 1e3, 4),
         "roofline": roof, "roofline_prefill": roof_p, "cpu_baseline": cpu,
         "stages_decode_per_token": stages_d, "stages_prefill": stages_p,
+        "kernels": kernels, "decode_cache_check": mall,
         "reference_m5": {"prefill_tok_s_4096": 24069, "decode_tok_s_ctx2048": 456,
                          "note": "Apple M5, real SmolLM2-135M Q8_0 (BASELINE.md); context only"},
     }

@@ -434,6 +434,11 @@ int ahip_module_launch(ahip_module* m, const char* kernel, const uint32_t grid[3
 int ahip_dev_pack_weight(ahip_context* ctx, int dtype, const void* host_w, int rows, int cols, void** handle);
 int ahip_dev_weight_free(ahip_context* ctx, void* handle);
 int ahip_dev_gemv(ahip_context* ctx, void* weight, const float* dx, float* dy, int iters, double* avg_seconds);
+/* The same GEMV, launch i on weights[i % count]: with copies that together
+ * exceed the device's last-level cache (MI355X: 256 MB of Infinity Cache),
+ * every launch streams its matrix from HBM. */
+int ahip_dev_gemv_cycle(ahip_context* ctx, void* const* weights, int count, const float* dx, float* dy, int iters,
+                        double* avg_seconds);
 /* Prefill GEMM: y[m,n] = x[m,k] W^T; x given as f32 on device, converted to
  * f16 once before timing (fast path) or used as f32 (exact). */
 int ahip_dev_gemm(ahip_context* ctx, void* weight, const float* dx, int m, float* dy, int gemm_precision,
@@ -442,6 +447,13 @@ int ahip_dev_gemm(ahip_context* ctx, void* weight, const float* dx, int m, float
  * filled from device f16 k/v [t, kv_heads, hd]; writes f32 out. */
 int ahip_dev_attention(ahip_context* ctx, const void* dq, const void* dk, const void* dv, int tokens, int heads,
                        int kv_heads, int head_dim, int start, float* dout, int iters, double* avg_seconds);
+/* Decode attention (attn_decode_split + attn_decode_merge, attention_decode.
+ * metal:27-133): one f32 query dq [heads, hd] over the first `length` rows of
+ * a device f16 cache dkc / dvc [kv_heads][capacity][hd]; the split-K kernel
+ * and its merge timed together; writes f32 dout [heads, hd]. */
+int ahip_dev_attention_decode(ahip_context* ctx, const float* dq, const void* dkc, const void* dvc, int capacity,
+                              int length, int heads, int kv_heads, int head_dim, float* dout, int iters,
+                              double* avg_seconds);
 
 #ifdef __cplusplus
 }
