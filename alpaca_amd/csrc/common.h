@@ -268,6 +268,8 @@ hipError_t launch_gemv_ex(const DevMatrix& w, const DevMatrix* w_up, const GemvI
                           float* out, int mode, hipStream_t st);
 hipError_t launch_gemv(const DevMatrix& w, const DevMatrix* w_up, const float* x, const float* norm, float eps,
                        float* out, int mode, hipStream_t st);
+// Whether w's decode products take the streamed GEMV (large matrices).
+bool gemv_streams(const DevMatrix& w);
 
 // prefill GEMM (kernels_gemm.hip)
 enum { GEMM_STORE = 0, GEMM_ACC = 1, GEMM_SWIGLU = 2, GEMM_QKV_ROPE = 3 };
@@ -395,6 +397,7 @@ size_t attention_partial_floats(int heads, int tokens, int splits, int hd);
 // else `length`; `splits` workgroups of split_len positions (<= 256) each.
 bool attention_decode_supported(int heads, int kv_heads, int hd);
 int attention_decode_split_len(int capacity);
+int attention_decode_split_len(int capacity, int kv_heads);
 int attention_decode_max_split_len();
 hipError_t launch_attention_decode(const float* q, const void* kc, const void* vc, int kv_f16, int capacity,
                                    int heads, int kv_heads, int hd, int length, const int* pos_dev, int split_len,

@@ -18,18 +18,58 @@ __device__ __forceinline__ int chunks_of(int K) {
     return FMT == DT_Q8_0 ? K >> 4 : FMT == DT_Q4_0 ? K >> 5 : K >> 3;
 }
 
+// The chunk's quants and its block scale, the scale kept as the f16 it is
+// stored as: converting it where it is loaded made the compiler wait for each
+// scale load before issuing the next quant load, which held a prefetched row
+// back by a memory round trip.
 template <int FMT>
-__device__ __forceinline__ void load_chunk(const DevMatrix& m, int64_t row, int K, int c, int4& q, float& d) {
+__device__ __forceinline__ void load_chunk(const DevMatrix& m, int64_t row, int K, int c, int4& q, f16& d) {
     if (FMT == DT_Q8_0) {
         q = gload_i4(m.q + row * K + 16 * c);
-        d = (float)*gptr(m.s + row * (K >> 5) + (c >> 1));
+        d = *gptr(m.s + row * (K >> 5) + (c >> 1));
     } else if (FMT == DT_Q4_0) {
         q = gload_i4(m.q + row * (K >> 1) + 16 * c);
-        d = (float)*gptr(m.s + row * (K >> 5) + c);
+        d = *gptr(m.s + row * (K >> 5) + c);
     } else {
         q = gload_i4(m.q + (row * K + 8 * c) * 2);
-        d = 1.f;
+        d = (f16)1.0f;
     }
+}
+
+// Byte offsets of row `row`'s chunk c in the quant stream and of its scale
+// (f16) in the scale stream.  With the matrix's base pointers wave-uniform,
+// loads through load_q / load_s become global loads with the base in SGPRs,
+// one 32-bit VGPR offset and an immediate: the chunks c0 + u * LPR of a row
+// share one offset VGPR.  (With 64-bit per-load addresses, the compiler reused
+// the address registers of loads still in flight as destinations of later
+// loads and waited for those loads to retire first, which held the row's quant
+// loads back behind its scale loads.)  Every operand spans less than 4 GiB.
+template <int FMT>
+__device__ __forceinline__ uint32_t chunk_qoff(int64_t row, int K, int c) {
+    return FMT == DT_Q8_0   ? (uint32_t)(row * K + 16 * c)
+           : FMT == DT_Q4_0 ? (uint32_t)(row * (K >> 1) + 16 * c)
+                            : (uint32_t)(row * K * 2 + 16 * c);
+}
+template <int FMT>
+__device__ __forceinline__ uint32_t chunk_soff(int64_t row, int K, int c) {
+    return FMT == DT_Q8_0 ? (uint32_t)(2 * (row * (K >> 5) + (c >> 1))) : (uint32_t)(2 * (row * (K >> 5) + c));
+}
+// Byte steps between chunk c and chunk c + LPR (LPR even).
+template <int FMT, int LPR>
+constexpr uint32_t chunk_qstep() {
+    return 16 * LPR;
+}
+template <int FMT, int LPR>
+constexpr uint32_t chunk_sstep() {
+    return FMT == DT_Q8_0 ? LPR : 2 * LPR;
+}
+__device__ __forceinline__ int4 load_q(const void* base, uint32_t off) {
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    const v4i v = *(const AS_GLOBAL v4i*)((const AS_GLOBAL char*)base + off);
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ f16 load_s(const void* base, uint32_t off) {
+    return *(const AS_GLOBAL f16*)((const AS_GLOBAL char*)base + off);
 }
 
 template <int FMT>
@@ -82,7 +122,7 @@ __device__ __forceinline__ float chunk_dot(const int4& q, float d, int c, const 
 template <int FMT, int LPR, int kUnroll = 4>
 struct RowStream {
     int4 q[kUnroll];
-    float d[kUnroll];
+    f16 d[kUnroll];
     __device__ __forceinline__ void prefetch(const DevMatrix& m, int64_t row, int K, int li) {
         const int nch = chunks_of<FMT>(K);
 #pragma unroll
@@ -97,7 +137,7 @@ struct RowStream {
 #pragma unroll
         for (int u = 0; u < kUnroll; u++) {
             const int c = li + u * LPR;
-            if (c < nch) acc += chunk_dot<FMT>(q[u], d[u], c, xs);
+            if (c < nch) acc += chunk_dot<FMT>(q[u], (float)d[u], c, xs);
         }
         for (int c0 = li + kUnroll * LPR; c0 < nch; c0 += kUnroll * LPR) {
 #pragma unroll
@@ -108,7 +148,7 @@ struct RowStream {
 #pragma unroll
             for (int u = 0; u < kUnroll; u++) {
                 const int c = c0 + u * LPR;
-                if (c < nch) acc += chunk_dot<FMT>(q[u], d[u], c, xs);
+                if (c < nch) acc += chunk_dot<FMT>(q[u], (float)d[u], c, xs);
             }
         }
         return acc;

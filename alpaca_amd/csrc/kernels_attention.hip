@@ -33,6 +33,8 @@
 // and for the exact / f32-KV / odd head-dim cases (attention.metal).
 #include "common.h"
 
+#include <algorithm>
+
 #include <cstdlib>
 #include <type_traits>
 
@@ -554,15 +556,62 @@ __global__ void attn_merge_kernel(const float* partials, int H, int hd, int spli
     }
 }
 
+// The same merge for up to kMergePer splits per thread: a workgroup of 256
+// threads per query head, thread t taking dim t % hd of the splits s = t / hd
+// (mod 256 / hd).  Every load (the splits' max and sum, the thread's outputs)
+// goes out before the first wait, so the merge costs one round trip to the
+// partials rather than one per batch of splits; the groups' sums are added
+// through LDS.
+constexpr int kMergePer = 16;
+__global__ __launch_bounds__(256) void attn_merge_wide_kernel(const float* partials, int hd, int splits, float* out) {
+    __shared__ float wsh[64];
+    __shared__ float part[256];
+    __shared__ float lsh;
+    const int th = blockIdx.x;
+    const float* pp = partials + (int64_t)th * splits * (hd + 2);
+    const int groups = 256 / hd, t = threadIdx.x, d = t % hd, grp = min(t / hd, groups - 1);
+    // unconditional loads (indices clamped, surplus values unused)
+    const int sm = min(t, splits - 1);
+    const float m_raw = pp[sm * (hd + 2)], l_raw = pp[sm * (hd + 2) + 1];
+    float o[kMergePer];
+#pragma unroll
+    for (int i = 0; i < kMergePer; i++) o[i] = pp[min(grp + i * groups, splits - 1) * (hd + 2) + 2 + d];
+    if (t < 64) {
+        const float ms = t < splits ? m_raw : -INFINITY;
+        const float ls = t < splits ? l_raw : 0.f;
+        const float mx = wave_max(ms);
+        const float w = ms == -INFINITY ? 0.f : expf(ms - mx);
+        wsh[t] = w;
+        const float l = wave_sum(ls * w);
+        if (t == 0) lsh = l;
+    }
+    __syncthreads();
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMergePer; i++) {
+        const int s = grp + i * groups;
+        if (s < splits) acc += o[i] * wsh[s];
+    }
+    if (t < groups * hd) part[t] = acc;
+    __syncthreads();
+    if (t < hd) {
+        float sum = 0.f;
+        for (int g = 0; g < groups; g++) sum += part[g * hd + t];
+        out[(int64_t)th * hd + t] = sum / lsh;
+    }
+}
+
 // ------------------------------------------------------------------ decode split-K
 // One workgroup per (KV head, split of the context) serves all G query heads
 // of that KV head, so every cached K/V row is read once per token.  Scores:
-// one thread per position (a 16-byte-vectorised K row each, coalesced across
-// the wave); probabilities go to LDS; P.V: hd/8 threads per V row with 16-byte
-// loads, partial sums reduced across rows with shuffles and LDS.  Writes the
-// split's (max, sum, unnormalised output) per query head; the Wo projection
-// merges the splits (attention_decode.metal:27-133 does split + merge
-// kernels).
+// one thread per position (a 16-byte-vectorised K row each); probabilities go
+// to LDS; P.V: hd/8 threads per V row with 16-byte loads, partial sums
+// reduced across rows with shuffles and LDS.  With an f16 cache the thread's
+// K row and its first V rows are loaded before anything else (after its q
+// values, which are needed first), so the workgroup waits for HBM once rather
+// than for K and then for V.  Writes the split's (max, sum, unnormalised
+// output) per query head; the Wo projection merges the splits
+// (attention_decode.metal:27-133 does split + merge kernels).
 constexpr int kDecThreads = 256;
 constexpr int kMaxSplitLen = 256;
 constexpr int kMaxGroup = 16;
@@ -575,6 +624,10 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_split_kernel(const fl
     constexpr int VEC = 16 / sizeof(KV);    // elements per 16-byte load
     constexpr int TPR = HD / 8;             // threads per V row (8 dims each)
     constexpr int RPP = kDecThreads / TPR;  // V rows in flight per pass
+    constexpr bool PRE = sizeof(KV) == 2;   // f16 cache: K row and first V rows loaded up front
+    constexpr int KCH = HD / VEC;           // 16-byte chunks per K row
+    constexpr int VPF = PRE ? (kMaxSplitLen / RPP < 8 ? kMaxSplitLen / RPP : 8) : 1;  // V rows per thread up front
+    constexpr int QPT = (GM * HD + kDecThreads - 1) / kDecThreads;                    // q values per thread
     __shared__ float qs[GM][HD];
     __shared__ float es[GM][kMaxSplitLen];
     __shared__ float red[GM][8];
@@ -586,25 +639,94 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_split_kernel(const fl
     const int p0 = sp * split_len;
     const int p1 = min(p0 + split_len, length);
     const int n = p1 - p0;
-    for (int i = tid; i < G * HD; i += kDecThreads) qs[i / HD][i % HD] = q[(kvh * G + i / HD) * HD + i % HD] * scale_log2;
+    const int tr = tid % TPR, rowq = tid / TPR;
+    float qv[QPT];
+#pragma unroll
+    for (int j = 0; j < QPT; j++) {  // (clamped index: an unconditional load)
+        const int i = min(tid + j * kDecThreads, G * HD - 1);
+        qv[j] = q[(kvh * G + i / HD) * HD + i % HD];
+    }
+    // the q loads stay ahead of the K/V loads: waiting for them then leaves the
+    // K/V loads in flight (loads retire in issue order)
+    asm volatile("" ::: "memory");
+    int4 kraw[PRE ? KCH : 1];
+    int4 vpre[VPF];
+    // f16 cache: KCH lanes share a K row (lane kj takes its 16-byte chunk kj), so a
+    // load instruction reads 64 / KCH whole rows; the lane's KCH loads cover rows
+    // kr0 + i * (kDecThreads / KCH)
+    constexpr int KRP = kDecThreads / KCH;  // K rows per load instruction
+    const int kj = tid % KCH, kr0 = tid / KCH;
+    if constexpr (PRE) {
+        // rows past the split's end are clamped to its last row (to its first
+        // when it is empty, p0 < cap), so every load goes out unconditionally and
+        // the compiler's wait counts stay exact; their values are unused
+        const int last = max(n - 1, 0);
+#pragma unroll
+        for (int i = 0; i < KCH; i++) {
+            const int r = min(kr0 + i * KRP, last);
+            kraw[i] = *(const int4*)(kc + ((int64_t)kvh * cap + p0 + r) * HD + kj * VEC);
+        }
+#pragma unroll
+        for (int k = 0; k < VPF; k++) {
+            const int r = min(rowq + k * RPP, last);
+            vpre[k] = *(const int4*)(vc + ((int64_t)kvh * cap + p0 + r) * HD + tr * 8);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < QPT; j++) {
+        const int i = tid + j * kDecThreads;
+        if (i < G * HD) qs[i / HD][i % HD] = qv[j] * scale_log2;
+    }
     __syncthreads();
 
-    // scores in base-2 exponent units: one thread per position
+    // scores in base-2 exponent units; thread `tid` ends with the scores of
+    // position `pr` (a permutation of 0..255)
     float sc[GM];
+    int pr = tid;
+    if constexpr (PRE) {
+        // Each lane's partial dot products over its 8 dims for its KCH rows are
+        // summed over the KCH lanes of the row group by a reduce-scatter: at
+        // every step a lane keeps half of its rows and adds the partner's sums
+        // for them, so lane kj ends with row i = kj complete.
+        pr = kr0 + kj * KRP;
 #pragma unroll
-    for (int g = 0; g < GM; g++) sc[g] = (tid < n && g < G) ? 0.f : -INFINITY;
-    if (tid < n) {
-        const KV* kr = kc + ((int64_t)kvh * cap + p0 + tid) * HD;
+        for (int g = 0; g < GM; g++) {
+            float part[KCH];
 #pragma unroll
-        for (int c = 0; c < HD / VEC; c++) {
-            const int4 raw = *(const int4*)(kr + c * VEC);
-            const KV* kv = (const KV*)&raw;
+            for (int i = 0; i < KCH; i++) {
+                const KV* kv = (const KV*)&kraw[i];
+                float a = 0.f;
 #pragma unroll
-            for (int j = 0; j < VEC; j++) {
-                const float kf = (float)kv[j];
+                for (int e = 0; e < VEC; e++) a += qs[g < G ? g : 0][kj * VEC + e] * (float)kv[e];
+                part[i] = a;
+            }
 #pragma unroll
-                for (int g = 0; g < GM; g++)
-                    if (g < G) sc[g] += qs[g][c * VEC + j] * kf;
+            for (int h = KCH / 2; h >= 1; h >>= 1) {
+                const bool hi = kj & h;
+#pragma unroll
+                for (int i = 0; i < h; i++) {
+                    const float keep = hi ? part[i + h] : part[i], give = hi ? part[i] : part[i + h];
+                    part[i] = keep + __shfl_xor(give, h, 64);
+                }
+            }
+            sc[g] = (pr < n && g < G) ? part[0] : -INFINITY;
+        }
+    } else {
+#pragma unroll
+        for (int g = 0; g < GM; g++) sc[g] = (tid < n && g < G) ? 0.f : -INFINITY;
+        if (tid < n) {
+            const KV* kr = kc + ((int64_t)kvh * cap + p0 + tid) * HD;
+#pragma unroll
+            for (int c = 0; c < HD / VEC; c++) {
+                const int4 raw = *(const int4*)(kr + c * VEC);
+                const KV* kv = (const KV*)&raw;
+#pragma unroll
+                for (int j = 0; j < VEC; j++) {
+                    const float kf = (float)kv[j];
+#pragma unroll
+                    for (int g = 0; g < GM; g++)
+                        if (g < G) sc[g] += qs[g][c * VEC + j] * kf;
+                }
             }
         }
     }
@@ -619,21 +741,43 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_split_kernel(const fl
     for (int g = 0; g < GM; g++) mloc[g] = fmaxf(fmaxf(red[g][0], red[g][1]), fmaxf(red[g][2], red[g][3]));
 #pragma unroll
     for (int g = 0; g < GM; g++) {
-        const float e = (tid < n && g < G) ? exp2f(sc[g] - mloc[g]) : 0.f;
-        if (tid < kMaxSplitLen) es[g][tid] = e;
+        const float e = (pr < n && g < G) ? exp2f(sc[g] - mloc[g]) : 0.f;
+        if (pr < kMaxSplitLen) es[g][pr] = e;
         const float sum = wave_sum(e);
         if (lane == 0) red[g][4 + wave] = sum;
     }
     __syncthreads();
 
     // P.V: TPR threads per V row, RPP rows per pass
-    const int tr = tid % TPR, rowq = tid / TPR;
     float acc[GM][8];
 #pragma unroll
     for (int g = 0; g < GM; g++)
 #pragma unroll
         for (int j = 0; j < 8; j++) acc[g][j] = 0.f;
-    for (int r = rowq; r < n; r += RPP) {
+    auto add_row = [&](int r, const float* vf) {
+#pragma unroll
+        for (int g = 0; g < GM; g++) {
+            const float e = es[g][r];
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[g][j] += e * vf[j];
+        }
+    };
+    int r0 = rowq;
+    if constexpr (PRE) {
+#pragma unroll
+        for (int k = 0; k < VPF; k++) {
+            const int r = rowq + k * RPP;
+            if (r < n) {
+                const KV* v = (const KV*)&vpre[k];
+                float vf[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) vf[j] = (float)v[j];
+                add_row(r, vf);
+            }
+        }
+        r0 = rowq + VPF * RPP;
+    }
+    for (int r = r0; r < n; r += RPP) {
         const KV* vr = vc + ((int64_t)kvh * cap + p0 + r) * HD + tr * 8;
         float vf[8];
         if constexpr (sizeof(KV) == 2) {
@@ -642,18 +786,13 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_split_kernel(const fl
 #pragma unroll
             for (int j = 0; j < 8; j++) vf[j] = (float)v[j];
         } else {
-            const int4 r0 = *(const int4*)vr, r1 = *(const int4*)(vr + 4);
-            const float* a = (const float*)&r0;
-            const float* b = (const float*)&r1;
+            const int4 r0v = *(const int4*)vr, r1v = *(const int4*)(vr + 4);
+            const float* a = (const float*)&r0v;
+            const float* b = (const float*)&r1v;
 #pragma unroll
             for (int j = 0; j < 4; j++) { vf[j] = a[j]; vf[4 + j] = b[j]; }
         }
-#pragma unroll
-        for (int g = 0; g < GM; g++) {
-            const float e = es[g][r];
-#pragma unroll
-            for (int j = 0; j < 8; j++) acc[g][j] += e * vf[j];
-        }
+        add_row(r, vf);
     }
     // reduce the rows held by one wave (lane bits >= log2(TPR)), then the 4 waves
 #pragma unroll
@@ -778,6 +917,10 @@ hipError_t launch_attention_decode(const float* q, const void* kc, const void* v
 
 hipError_t launch_attention_merge(const float* partials, int heads, int hd, int splits, float* out, hipStream_t st) {
     if (splits < 1 || splits > 64) return hipErrorInvalidValue;  // one split per lane of a wave
+    if (hd <= 256 && splits <= (256 / hd) * kMergePer) {
+        attn_merge_wide_kernel<<<heads, 256, 0, st>>>(partials, hd, splits, out);
+        return hipGetLastError();
+    }
     int bt = hd < 64 ? 64 : (hd > 256 ? 256 : (hd + 63) / 64 * 64);
     attn_merge_kernel<<<heads, bt, 0, st>>>(partials, heads, hd, splits, out);
     return hipGetLastError();
@@ -788,6 +931,28 @@ int attention_decode_split_len(int capacity) {
     int l = (capacity + 63) / 64;
     l = (l + 31) / 32 * 32;
     return l < 128 ? 128 : l;
+}
+
+// A session's split length: 64 to 256 positions (a multiple of 32) aiming at
+// about two workgroups per CU over all KV heads at full capacity, and at most
+// 64 splits.  A grid past what the CUs hold at once runs a second, partial
+// round of workgroups: 128-position splits gave the 1.7B shape (32 KV heads,
+// 4,176 positions) 1,056 workgroups; 256-position splits give 544.
+int attention_decode_split_len(int capacity, int kv_heads) {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+        cus[dev] = n;
+    }
+    const int64_t target = 2 * (int64_t)cus[dev];
+    int l = (int)(((int64_t)capacity * kv_heads + target - 1) / target);
+    const int fewest = (capacity + 63) / 64;  // at most 64 splits
+    l = std::max(std::max(l, fewest), 64);
+    l = (l + 31) / 32 * 32;
+    return l < kMaxSplitLen ? l : (fewest <= kMaxSplitLen ? kMaxSplitLen : l);
 }
 int attention_decode_max_split_len() { return kMaxSplitLen; }
 

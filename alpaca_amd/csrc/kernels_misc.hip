@@ -164,7 +164,28 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, int n
     __shared__ int si[16];
     float v = -INFINITY;
     int idx = INT_MAX;
-    for (int i = threadIdx.x; i < n; i += 1024) {
+    // 16-byte loads, sixteen in flight per thread (a 64K-entry vocabulary in
+    // one batch; indices past the end clamped to the last quad and their
+    // values skipped, so the loads go out unconditionally); each thread visits
+    // its indices in increasing order, so it keeps the first of equal maxima
+    const int n4 = ((uintptr_t)logits & 15) ? 0 : n / 4;
+    const float4* l4 = (const float4*)logits;
+    for (int base = threadIdx.x; base < n4; base += 16 * 1024) {
+        float4 x[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) x[u] = l4[min(base + u * 1024, n4 - 1)];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int i = 4 * (base + u * 1024);
+            if (i < 4 * n4) {
+                if (x[u].x > v) { v = x[u].x; idx = i; }
+                if (x[u].y > v) { v = x[u].y; idx = i + 1; }
+                if (x[u].z > v) { v = x[u].z; idx = i + 2; }
+                if (x[u].w > v) { v = x[u].w; idx = i + 3; }
+            }
+        }
+    }
+    for (int i = 4 * n4 + threadIdx.x; i < n; i += 1024) {
         float x = logits[i];
         if (x > v) { v = x; idx = i; }
     }

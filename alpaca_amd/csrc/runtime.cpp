@@ -873,8 +873,14 @@ static int pdec_reset_words(ahip_session* s) {
 
 // Chooses the persistent decode kernel when the model and device allow it:
 // f16 KV cache, one weight format for every layer matrix, head_dim 64/128,
-// cooperative launch support and enough LDS.  ALPACA_HIP_PERSISTENT_DECODE=0
-// turns it off; ALPACA_HIP_DECODE_WGS sets the workgroup count (default: one
+// cooperative launch support and enough LDS, and layers whose matrices are
+// below the streamed GEMV's size.  Where every projection of a layer streams
+// (each at least 4 MB: the 1.7B shape), the multi-kernel step (streamed GEMVs,
+// split-K attention and merge, one HIP graph per greedy step) moves more bytes
+// per microsecond than the persistent kernel's one workgroup per CU: 1.7B
+// shape at context 4,096, 942 against 1,172 us per token.
+// ALPACA_HIP_PERSISTENT_DECODE=0 turns the persistent kernel off, =2 takes it
+// for large layers too; ALPACA_HIP_DECODE_WGS sets the workgroup count (default: one
 // per CU); ALPACA_HIP_DECODE_ITEMS the attention items aimed for;
 // ALPACA_HIP_DECODE_TIMEOUT_US the bound on each wait inside the kernel;
 // ALPACA_HIP_DECODE_ABORT_LAYER (failure-path tests) makes every launch abort
@@ -893,7 +899,14 @@ static int pdec_reset_words(ahip_session* s) {
 static int setup_persistent_decode(ahip_session* s) {
     ahip_model* m = s->m;
     const ahip_llama_config& c = m->c;
-    if (!env_int("ALPACA_HIP_PERSISTENT_DECODE", 1) || !s->kv_f16) return AHIP_OK;
+    const int mode = env_int("ALPACA_HIP_PERSISTENT_DECODE", 1);
+    if (!mode || !s->kv_f16) return AHIP_OK;
+    {
+        const ahip_model::Layer& L0 = *m->layers[0];
+        bool streams = s->dec_split;
+        for (const OwnedMatrix* om : {&L0.qkv, &L0.wo, &L0.gate, &L0.up, &L0.down}) streams = streams && gemv_streams(om->m);
+        if (streams && mode != 2) return AHIP_OK;
+    }
     const int fmt = m->layers[0]->qkv.m.dtype;
     for (auto& L : m->layers)
         for (const OwnedMatrix* om : {&L->qkv, &L->wo, &L->gate, &L->up, &L->down})
@@ -1182,9 +1195,9 @@ extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, i
         return fail(AHIP_ERR_ALLOC, "pinned host allocation failed");
     HIP_OR(hipHostGetDevicePointer((void**)&s->emitted_mapped, s->emitted_host, 0), "hipHostGetDevicePointer");
     s->dec_split = attention_decode_supported(c.head_count, c.kv_head_count, c.head_dim) &&
-                   attention_decode_split_len(capacity) <= attention_decode_max_split_len();
+                   attention_decode_split_len(capacity, c.kv_head_count) <= attention_decode_max_split_len();
     if (s->dec_split) {
-        s->dec_split_len = attention_decode_split_len(capacity);
+        s->dec_split_len = attention_decode_split_len(capacity, c.kv_head_count);
         s->dec_splits = (capacity + s->dec_split_len - 1) / s->dec_split_len;
     }
     if (int rc = setup_persistent_decode(s.get())) return rc;
@@ -1281,7 +1294,15 @@ static int encode_decode_layer(ahip_session* s, int li, int pos, const int* pos_
         att.x = s->ctx.as<float>();
     }
     s->stage("attn out projection (+residual)");
-    LAUNCH(launch_gemv_ex(L.wo.m, nullptr, att, nullptr, x, GEMV_ADD, st));
+    // A Wo large enough for the streamed GEMV takes the merged context row from
+    // its own kernel: folded into Wo's input stage, every workgroup would read
+    // all heads' partials (the 1.7B shape: 16.2 us against 4.7 + 4.8 us).
+    if (att.partials && gemv_streams(L.wo.m)) {
+        LAUNCH(launch_attention_merge(att.partials, c.head_count, hd, att.splits, s->ctx.as<float>(), st));
+        LAUNCH(launch_gemv(L.wo.m, nullptr, s->ctx.as<float>(), nullptr, 0.f, x, GEMV_ADD, st));
+    } else {
+        LAUNCH(launch_gemv_ex(L.wo.m, nullptr, att, nullptr, x, GEMV_ADD, st));
+    }
     s->stage("ffn gate+up+silu (fused norm)");
     LAUNCH(launch_gemv(L.gate.m, &L.up.m, x, L.ffn_norm.as<float>(), c.rms_norm_eps, s->ffn.as<float>(), GEMV_SWIGLU,
                        st));

@@ -361,13 +361,13 @@ def test_gemm_second_term_from_a_row_on(hip_ops, name, dt):
 @pytest.mark.parametrize("n,k,name,dt", [(49152, 576, "q8_0", Q8_0), (8192, 2048, "q8_0", Q8_0),
                                          (2048, 8192, "q8_0", Q8_0), (12288, 960, "q4_0", Q4_0),
                                          (4100, 1024, "f16", F16)])
-def test_tall_gemv(hip_ops, n, k, name, dt):
-    """Matrices of at least 4 MB take the persistent tall-matrix GEMV (the C1
-    logits, the C5 FFN matrices, a Q4_0 and an F16 one with a partial last
-    tile): within the exact GEMV's 2e-4 + 1e-4 |y| of the oracle, for the
-    store, residual and SwiGLU epilogues, and equal to the one-tile-per-
-    workgroup kernel (ALPACA_HIP_GEMV_TALL=0, read per launch) to float32
-    rounding (both sum each lane's chunks in order, then across lanes)."""
+def test_stream_gemv(hip_ops, n, k, name, dt):
+    """Matrices of at least 4 MB take the streamed GEMV (the C1 logits, the
+    C5 FFN matrices, a Q4_0 and an F16 one with a partial last tile): within
+    the exact GEMV's 2e-4 + 1e-4 |y| of the oracle, for the store, residual
+    and SwiGLU epilogues, and equal to the one-tile-per-workgroup kernel
+    (ALPACA_HIP_GEMV_STREAM=0, read per launch) to float32 rounding (both sum
+    each lane's chunks in order, then across lanes)."""
     w = encode(rand((n, k), 6161 + n, 0.05), dt)
     wu = encode(rand((n, k), 6262 + n, 0.05), dt)
     x = rand((1, k), 6363 + k)
@@ -375,11 +375,11 @@ def test_tall_gemv(hip_ops, n, k, name, dt):
     y = orc.linear(x, dt, w.data, n)
     u = orc.linear(x, dt, wu.data, n)
     outs = (hip_ops.linear(x, w, "exact"), hip_ops.linear_add(x, w, res, "exact"), hip_ops.gate_up_silu(x, w, wu, "exact"))
-    with env(ALPACA_HIP_GEMV_TALL=0):
+    with env(ALPACA_HIP_GEMV_STREAM=0):
         other = (hip_ops.linear(x, w, "exact"), hip_ops.linear_add(x, w, res, "exact"),
                  hip_ops.gate_up_silu(x, w, wu, "exact"))
     for i, (what, e) in enumerate((("store", y), ("residual", orc.add(res, y)),
                                    ("swiglu", orc.mul(orc.silu(y), u)))):
-        assert_close(outs[i], e, 2e-4, 1e-4, f"tall gemv {name} {n}x{k} {what}")
+        assert_close(outs[i], e, 2e-4, 1e-4, f"streamed gemv {name} {n}x{k} {what}")
         d = np.abs(outs[i].astype(np.float64) - other[i])
-        assert d.max() <= 1e-5 * max(1.0, float(np.abs(other[i]).max())), f"{what}: tall vs other kernel {d.max():.3e}"
+        assert d.max() <= 1e-5 * max(1.0, float(np.abs(other[i]).max())), f"{what}: streamed vs other kernel {d.max():.3e}"
