@@ -394,11 +394,12 @@ size_t attention_partial_floats(int heads, int tokens, int splits, int hd);
 // per-split partials [heads][splits][hd+2] merged by launch_attention_merge or
 // by the Wo GEMV prologue.  Needs hd 64/128, heads/kv_heads <= 16.
 // Context length = *pos_dev + 1 when pos_dev is set (device-side position),
-// else `length`; `splits` workgroups of split_len positions (<= 256) each.
+// else `length`; `splits` workgroups of split_len positions each (<= 256, or
+// <= 512 for at most 2 query heads per KV head).
+// attention_decode_session_split_len: the split length sessions and the
+// single-query ops take for a cache of `capacity` rows (0: unsupported).
 bool attention_decode_supported(int heads, int kv_heads, int hd);
-int attention_decode_split_len(int capacity);
-int attention_decode_split_len(int capacity, int kv_heads);
-int attention_decode_max_split_len();
+int attention_decode_session_split_len(int capacity, int heads, int kv_heads);
 hipError_t launch_attention_decode(const float* q, const void* kc, const void* vc, int kv_f16, int capacity,
                                    int heads, int kv_heads, int hd, int length, const int* pos_dev, int split_len,
                                    int splits, float* partials, hipStream_t st);

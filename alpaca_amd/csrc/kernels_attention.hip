@@ -613,25 +613,28 @@ __global__ __launch_bounds__(256) void attn_merge_wide_kernel(const float* parti
 // output) per query head; the Wo projection merges the splits
 // (attention_decode.metal:27-133 does split + merge kernels).
 constexpr int kDecThreads = 256;
-constexpr int kMaxSplitLen = 256;
+constexpr int kMaxSplitLen = 256;     // positions per workgroup of kDecThreads threads
+constexpr int kMaxSplitLenWide = 512;  // with 512-thread workgroups (groups of at most 2 query heads)
 constexpr int kMaxGroup = 16;
 
-template <int HD, int GM, typename KV>
-__global__ __launch_bounds__(kDecThreads) void attn_decode_split_kernel(const float* q, const KV* kc, const KV* vc,
+// NT threads, one position each: split_len <= NT.
+template <int HD, int GM, typename KV, int NT = kDecThreads>
+__global__ __launch_bounds__(NT) void attn_decode_split_kernel(const float* q, const KV* kc, const KV* vc,
                                                                         int cap, int H, int KVH, int length,
                                                                         const int* pos_dev, int split_len,
                                                                         float scale_log2, float* partials) {
     constexpr int VEC = 16 / sizeof(KV);    // elements per 16-byte load
     constexpr int TPR = HD / 8;             // threads per V row (8 dims each)
-    constexpr int RPP = kDecThreads / TPR;  // V rows in flight per pass
+    constexpr int WV = NT / 64;             // waves
+    constexpr int RPP = NT / TPR;           // V rows in flight per pass
     constexpr bool PRE = sizeof(KV) == 2;   // f16 cache: K row and first V rows loaded up front
     constexpr int KCH = HD / VEC;           // 16-byte chunks per K row
-    constexpr int VPF = PRE ? (kMaxSplitLen / RPP < 8 ? kMaxSplitLen / RPP : 8) : 1;  // V rows per thread up front
-    constexpr int QPT = (GM * HD + kDecThreads - 1) / kDecThreads;                    // q values per thread
+    constexpr int VPF = PRE ? (NT / RPP < 8 ? NT / RPP : 8) : 1;  // V rows per thread up front
+    constexpr int QPT = (GM * HD + NT - 1) / NT;                  // q values per thread
     __shared__ float qs[GM][HD];
-    __shared__ float es[GM][kMaxSplitLen];
-    __shared__ float red[GM][8];
-    __shared__ float ws[4][GM][HD];
+    __shared__ float es[GM][NT];
+    __shared__ float red[GM][2 * WV];
+    __shared__ float ws[WV][GM][HD];
     const int G = H / KVH;
     const int sp = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -643,7 +646,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_split_kernel(const fl
     float qv[QPT];
 #pragma unroll
     for (int j = 0; j < QPT; j++) {  // (clamped index: an unconditional load)
-        const int i = min(tid + j * kDecThreads, G * HD - 1);
+        const int i = min(tid + j * NT, G * HD - 1);
         qv[j] = q[(kvh * G + i / HD) * HD + i % HD];
     }
     // the q loads stay ahead of the K/V loads: waiting for them then leaves the
@@ -653,8 +656,8 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_split_kernel(const fl
     int4 vpre[VPF];
     // f16 cache: KCH lanes share a K row (lane kj takes its 16-byte chunk kj), so a
     // load instruction reads 64 / KCH whole rows; the lane's KCH loads cover rows
-    // kr0 + i * (kDecThreads / KCH)
-    constexpr int KRP = kDecThreads / KCH;  // K rows per load instruction
+    // kr0 + i * (NT / KCH)
+    constexpr int KRP = NT / KCH;  // K rows per load instruction
     const int kj = tid % KCH, kr0 = tid / KCH;
     if constexpr (PRE) {
         // rows past the split's end are clamped to its last row (to its first
@@ -674,7 +677,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_split_kernel(const fl
     }
 #pragma unroll
     for (int j = 0; j < QPT; j++) {
-        const int i = tid + j * kDecThreads;
+        const int i = tid + j * NT;
         if (i < G * HD) qs[i / HD][i % HD] = qv[j] * scale_log2;
     }
     __syncthreads();
@@ -738,13 +741,17 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_split_kernel(const fl
     __syncthreads();
     float mloc[GM];
 #pragma unroll
-    for (int g = 0; g < GM; g++) mloc[g] = fmaxf(fmaxf(red[g][0], red[g][1]), fmaxf(red[g][2], red[g][3]));
+    for (int g = 0; g < GM; g++) {
+        mloc[g] = fmaxf(fmaxf(red[g][0], red[g][1]), fmaxf(red[g][2], red[g][3]));
+#pragma unroll
+        for (int w = 4; w < WV; w++) mloc[g] = fmaxf(mloc[g], red[g][w]);
+    }
 #pragma unroll
     for (int g = 0; g < GM; g++) {
         const float e = (pr < n && g < G) ? exp2f(sc[g] - mloc[g]) : 0.f;
-        if (pr < kMaxSplitLen) es[g][pr] = e;
+        es[g][pr] = e;
         const float sum = wave_sum(e);
-        if (lane == 0) red[g][4 + wave] = sum;
+        if (lane == 0) red[g][WV + wave] = sum;
     }
     __syncthreads();
 
@@ -807,15 +814,20 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_split_kernel(const fl
 #pragma unroll
             for (int j = 0; j < 8; j++) ws[wave][g][tr * 8 + j] = acc[g][j];
     __syncthreads();
-    for (int i = tid; i < G * HD; i += kDecThreads) {
+    for (int i = tid; i < G * HD; i += NT) {
         const int g = i / HD, d = i % HD;
         float* pp = partials + ((int64_t)(kvh * G + g) * gridDim.x + sp) * (HD + 2);
-        pp[2 + d] = ws[0][g][d] + ws[1][g][d] + ws[2][g][d] + ws[3][g][d];
+        float o = ws[0][g][d];
+#pragma unroll
+        for (int w = 1; w < WV; w++) o += ws[w][g][d];
+        pp[2 + d] = o;
         if (d == 0) {
             // the running max is kept in base-2 units; partials carry natural-log units
-            pp[0] = n > 0 ? fmaxf(fmaxf(red[g][0], red[g][1]), fmaxf(red[g][2], red[g][3])) * 0.69314718055994531f
-                          : -INFINITY;
-            pp[1] = red[g][4] + red[g][5] + red[g][6] + red[g][7];
+            float l = red[g][WV];
+#pragma unroll
+            for (int w = 1; w < WV; w++) l += red[g][WV + w];
+            pp[0] = n > 0 ? mloc[g] * 0.69314718055994531f : -INFINITY;
+            pp[1] = l;
         }
     }
 }
@@ -825,6 +837,11 @@ hipError_t decode_dispatch(int G, dim3 grid, hipStream_t st, const float* q, con
                            int H, int KVH, int length, const int* pos_dev, int split_len, float sl2, float* partials) {
     const KV* k = (const KV*)kc;
     const KV* v = (const KV*)vc;
+    if (split_len > kMaxSplitLen) {  // (the launcher allows this for groups of at most 2 heads only)
+        if (G <= 1) attn_decode_split_kernel<HD, 1, KV, 512><<<grid, 512, 0, st>>>(q, k, v, cap, H, KVH, length, pos_dev, split_len, sl2, partials);
+        else attn_decode_split_kernel<HD, 2, KV, 512><<<grid, 512, 0, st>>>(q, k, v, cap, H, KVH, length, pos_dev, split_len, sl2, partials);
+        return hipGetLastError();
+    }
     if (G <= 1) attn_decode_split_kernel<HD, 1, KV><<<grid, kDecThreads, 0, st>>>(q, k, v, cap, H, KVH, length, pos_dev, split_len, sl2, partials);
     else if (G <= 2) attn_decode_split_kernel<HD, 2, KV><<<grid, kDecThreads, 0, st>>>(q, k, v, cap, H, KVH, length, pos_dev, split_len, sl2, partials);
     else if (G <= 4) attn_decode_split_kernel<HD, 4, KV><<<grid, kDecThreads, 0, st>>>(q, k, v, cap, H, KVH, length, pos_dev, split_len, sl2, partials);
@@ -904,7 +921,8 @@ hipError_t launch_attention_decode(const float* q, const void* kc, const void* v
                                    int heads, int kv_heads, int hd, int length, const int* pos_dev, int split_len,
                                    int splits, float* partials, hipStream_t st) {
     const int G = heads / kv_heads;
-    if (split_len > kMaxSplitLen || G > kMaxGroup || heads % kv_heads || (hd != 64 && hd != 128))
+    if (split_len < 1 || split_len > (G <= 2 ? kMaxSplitLenWide : kMaxSplitLen) || G > kMaxGroup || heads % kv_heads ||
+        (hd != 64 && hd != 128))
         return hipErrorInvalidValue;
     const float sl2 = 1.4426950408889634f / sqrtf((float)hd);
     dim3 grid(splits, kv_heads);
@@ -926,19 +944,14 @@ hipError_t launch_attention_merge(const float* partials, int heads, int hd, int 
     return hipGetLastError();
 }
 
-int attention_decode_split_len(int capacity) {
-    // 128 positions per split, widened so a context never needs more than 64 splits
-    int l = (capacity + 63) / 64;
-    l = (l + 31) / 32 * 32;
-    return l < 128 ? 128 : l;
-}
-
-// A session's split length: 64 to 256 positions (a multiple of 32) aiming at
-// about two workgroups per CU over all KV heads at full capacity, and at most
-// 64 splits.  A grid past what the CUs hold at once runs a second, partial
-// round of workgroups: 128-position splits gave the 1.7B shape (32 KV heads,
-// 4,176 positions) 1,056 workgroups; 256-position splits give 544.
-int attention_decode_split_len(int capacity, int kv_heads) {
+// A session's split length: 64 to 256 positions (512 for groups of at most
+// two query heads), a multiple of 32, aiming at no more than two workgroups
+// per CU over all KV heads at full capacity, and at most 64 splits (0: none
+// fits).  More workgroups than that put a third on some CUs, which then set
+// the kernel's time: 128-position splits gave the 1.7B shape (32 KV heads,
+// 4,176 positions) 1,056 workgroups and 256-position splits 544; 288-position
+// splits give 480.
+int attention_decode_session_split_len(int capacity, int heads, int kv_heads) {
     static int cus[64] = {0};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
@@ -947,14 +960,15 @@ int attention_decode_split_len(int capacity, int kv_heads) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
         cus[dev] = n;
     }
+    const int most = kv_heads > 0 && heads / kv_heads <= 2 ? kMaxSplitLenWide : kMaxSplitLen;
     const int64_t target = 2 * (int64_t)cus[dev];
     int l = (int)(((int64_t)capacity * kv_heads + target - 1) / target);
     const int fewest = (capacity + 63) / 64;  // at most 64 splits
     l = std::max(std::max(l, fewest), 64);
     l = (l + 31) / 32 * 32;
-    return l < kMaxSplitLen ? l : (fewest <= kMaxSplitLen ? kMaxSplitLen : l);
+    if (l <= most) return l;
+    return fewest <= most ? most : 0;
 }
-int attention_decode_max_split_len() { return kMaxSplitLen; }
 
 bool attention_decode_supported(int heads, int kv_heads, int hd) {
     return (hd == 64 || hd == 128) && heads % kv_heads == 0 && heads / kv_heads <= kMaxGroup;

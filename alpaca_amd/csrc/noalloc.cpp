@@ -56,18 +56,19 @@ extern "C" int ahip_attention_decode_noalloc(ahip_context* ctx, const float* q, 
         return ahip_fail(AHIP_ERR_INVALID_ARGUMENT, "bad kv precision");
     if (heads <= 0 || kv_heads <= 0 || capacity <= 0 || length <= 0 || length > capacity)
         return ahip_fail(AHIP_ERR_INVALID_ARGUMENT, "attention shapes");
-    if (!attention_decode_supported(heads, kv_heads, head_dim) ||
-        attention_decode_split_len(capacity) > attention_decode_max_split_len())
-        return ahip_fail(AHIP_ERR_UNSUPPORTED, "head_dim 64 or 128, at most 8 query heads per KV head");
     if (stream && stream->device != ctx->device)
         return ahip_fail(AHIP_ERR_INVALID_ARGUMENT, "stream and context belong to different devices");
-    const int sl = attention_decode_split_len(capacity), splits = (length + sl - 1) / sl;
+    if (hipSetDevice(ctx->device) != hipSuccess) return ahip_fail(AHIP_ERR_COMMAND_FAILED, "hipSetDevice");
+    // the split length ahip_op_attention takes for one query
+    const int sl = attention_decode_supported(heads, kv_heads, head_dim)
+                       ? attention_decode_session_split_len(capacity, heads, kv_heads) : 0;
+    if (sl <= 0) return ahip_fail(AHIP_ERR_UNSUPPORTED, "head_dim 64 or 128, at most 16 query heads per KV head");
+    const int splits = (length + sl - 1) / sl;
     const size_t need = (size_t)heads * splits * (head_dim + 2);
     if (need > kScratchFloats)
         return ahip_fail(AHIP_ERR_INVALID_ARGUMENT,
                          "split partials need " + std::to_string(need) + " floats, more than the " +
                              std::to_string(kScratchFloats) + "-float scratch array holds");
-    if (hipSetDevice(ctx->device) != hipSuccess) return ahip_fail(AHIP_ERR_COMMAND_FAILED, "hipSetDevice");
     float* part = nullptr;
     {
         std::lock_guard<std::mutex> g(g_lock);

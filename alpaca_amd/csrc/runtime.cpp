@@ -1195,9 +1195,9 @@ extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, i
         return fail(AHIP_ERR_ALLOC, "pinned host allocation failed");
     HIP_OR(hipHostGetDevicePointer((void**)&s->emitted_mapped, s->emitted_host, 0), "hipHostGetDevicePointer");
     s->dec_split = attention_decode_supported(c.head_count, c.kv_head_count, c.head_dim) &&
-                   attention_decode_split_len(capacity, c.kv_head_count) <= attention_decode_max_split_len();
+                   attention_decode_session_split_len(capacity, c.head_count, c.kv_head_count) > 0;
     if (s->dec_split) {
-        s->dec_split_len = attention_decode_split_len(capacity, c.kv_head_count);
+        s->dec_split_len = attention_decode_session_split_len(capacity, c.head_count, c.kv_head_count);
         s->dec_splits = (capacity + s->dec_split_len - 1) / s->dec_split_len;
     }
     if (int rc = setup_persistent_decode(s.get())) return rc;
@@ -2072,9 +2072,9 @@ extern "C" int ahip_op_attention(ahip_context* ctx, const float* q, int tokens, 
                                           dv.as<f16>(), capacity, tokens, heads, kv_heads, hd, start, dout.as<float>(),
                                           nullptr, nullptr, st));
         } else if (tokens == 1 && attention_decode_supported(heads, kv_heads, hd) &&
-                   attention_decode_split_len(capacity) <= attention_decode_max_split_len()) {
+                   attention_decode_session_split_len(capacity, heads, kv_heads) > 0) {
             if (int rc = upload(dq, q, qn * 4, st)) return rc;
-            const int sl = attention_decode_split_len(capacity), splits = (start + sl) / sl;
+            const int sl = attention_decode_session_split_len(capacity, heads, kv_heads), splits = (start + sl) / sl;
             DevBuf part;
             if (int rc = part.alloc((size_t)heads * splits * (hd + 2) * 4)) return rc;
             LAUNCH(launch_attention_decode(dq.as<float>(), dk.p, dv.p, f16kv, capacity, heads, kv_heads, hd, start + 1,
@@ -2258,11 +2258,11 @@ extern "C" int ahip_dev_attention_decode(ahip_context* ctx, const float* dq, con
     if (!ctx || !dq || !dkc || !dvc || !dout || length <= 0 || length > capacity || kv_heads <= 0 ||
         heads % kv_heads || iters < 0)
         return fail(AHIP_ERR_INVALID_ARGUMENT, "bad argument");
-    if (!attention_decode_supported(heads, kv_heads, hd) ||
-        attention_decode_split_len(capacity) > attention_decode_max_split_len())
-        return fail(AHIP_ERR_UNSUPPORTED, "decode attention shape");
     HIP_OR(hipSetDevice(ctx->device), "hipSetDevice");
-    const int sl = attention_decode_split_len(capacity), splits = (length - 1 + sl) / sl;
+    const int sl = attention_decode_supported(heads, kv_heads, hd)
+                       ? attention_decode_session_split_len(capacity, heads, kv_heads) : 0;
+    if (sl <= 0) return fail(AHIP_ERR_UNSUPPORTED, "decode attention shape");
+    const int splits = (length - 1 + sl) / sl;
     DevBuf part;
     if (int rc = part.alloc((size_t)heads * splits * (hd + 2) * 4)) return rc;
     return time_launches(ctx, iters, avg, [&](hipStream_t st) {

@@ -72,8 +72,8 @@ def test_noalloc_refuses_shapes_past_its_scratch(hip_ctx):
     p = C.c_void_p()
     L.check(lib.ahip_malloc(ctx, 1 << 20, C.byref(p)))
     try:
-        # 128 heads x 64 splits x 130 floats > the 2.5 MiB array: refused before any launch
-        rc = lib.ahip_attention_decode_noalloc(ctx, p, p, p, L.KV_F16, 8192, 128, 16, 128, 8192, p, None)
+        # 256 heads x 32 splits (of 256 positions) x 130 floats > the 2.5 MiB array: refused before any launch
+        rc = lib.ahip_attention_decode_noalloc(ctx, p, p, p, L.KV_F16, 8192, 256, 32, 128, 8192, p, None)
         assert rc == L.INVALID_ARGUMENT
         assert b"scratch" in lib.ahip_last_error()
         # length past the capacity
