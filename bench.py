@@ -139,6 +139,11 @@ def other_config(ctx, spec, ctx_len: int, prefill_tokens: int, steps: int = 64, 
     el = time.perf_counter() - t0
     launch = s.last_gpu_seconds / steps
     tok_bytes = decode_token_bytes(c, ctx_len + (steps - 1) / 2 + 1, 18 if spec.dtype == Q4_0 else 34)
+    # which decode step the session took: a profiled single-token decode leaves
+    # persistent-launch stamps only on the persistent kernel
+    s.profiling_enabled = True
+    s.decode(first)
+    persistent = s.decode_timeline[0].size > 0
     s.close()
     p = model.make_session(capacity=prefill_tokens, max_batch=4096)
     for _ in range(2):
@@ -168,7 +173,9 @@ def other_config(ctx, spec, ctx_len: int, prefill_tokens: int, steps: int = 64, 
                                  "frac": round(fl[label] / avg / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
     p.close()
     model.close()
-    return {"decode_ctx": ctx_len, "decode_tok_s": round(steps / el, 1), "decode_avg_launch_us": round(launch * 1e6, 1),
+    return {"decode_ctx": ctx_len, "decode_tok_s": round(steps / el, 1), "decode_avg_step_us": round(launch * 1e6, 1),
+            "decode_path": ("persistent decode kernel, one launch per token" if persistent else
+                            "multi-kernel step in one HIP graph per token (streamed GEMVs, split-K attention, merge)"),
             "decode_hbm_frac": round(tok_bytes / launch / 1e9 / HBM_PEAK_GBS, 4),
             "prefill_tokens": prefill_tokens, "prefill_tok_s": round(prefill_tokens / wall, 1),
             "prefill_mfma_frac": round(flops / wall / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
