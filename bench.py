@@ -431,6 +431,8 @@ def counter_summary(dirs: dict, kernel: str, gemm: bool = False) -> int:
         return out
 
     cf, cw = values(dirs["copy_fetch"], "copyBuffer", "FETCH_SIZE"), values(dirs["copy_write"], "copyBuffer", "WRITE_SIZE")
+    if kernel == "decode-step-kernels":
+        return counter_table(dirs, cf, cw, values)
     kf, kw = values(dirs["fetch"], kernel, "FETCH_SIZE"), values(dirs["write"], kernel, "WRITE_SIZE")
     if not (cf and cw and kf and kw):
         print("missing counter rows", file=sys.stderr)
@@ -449,6 +451,49 @@ def counter_summary(dirs: dict, kernel: str, gemm: bool = False) -> int:
               f"{sum(v) / len(v) * sc * 1024 / 1e6:.1f} |")
     label, src = ("GEMM", GEMM_SOURCES) if gemm else ("Decode", DECODE_SOURCES)
     print(f"\nTraffic per launch: {traffic:.1f} MB\n\n{label} source hash: {source_hash(root, src)}")
+    return 0
+
+
+def counter_table(dirs: dict, cf: list, cw: list, values) -> int:
+    """Per-kernel HBM bytes of a multi-kernel decode run (--counter-kernel
+    decode-step-kernels): every kernel of the decode step with its dispatches
+    and scaled FETCH_SIZE / WRITE_SIZE per dispatch, and the sum per decode
+    step (one arg-max dispatch per step)."""
+    import glob
+    import re
+    import sqlite3
+
+    def per_kernel(d: str, counter: str) -> dict:
+        out = {}
+        for db in glob.glob(os.path.join(d, "**", "*results.db"), recursive=True):
+            con = sqlite3.connect(db)
+            for k, c, v in con.execute("select kernel_name, counter_name, value from counters_collection"):
+                if c == counter:
+                    out.setdefault(re.sub(r"\(anonymous namespace\)::", "", k), []).append(v)
+        return out
+
+    if not (cf and cw):
+        print("missing calibration rows", file=sys.stderr)
+        return 1
+    sf, sw = 256 * 1024 / max(cf), 256 * 1024 / max(cw)
+    f, w = per_kernel(dirs["fetch"], "FETCH_SIZE"), per_kernel(dirs["write"], "WRITE_SIZE")
+    step = ("gemv", "attn_decode", "attn_merge", "argmax", "embed")
+    names = [k for k in f if k in w and any(t in k for t in step)]
+    steps = max((len(f[k]) for k in names if "argmax" in k), default=0)
+    if not names or not steps:
+        print("missing decode kernel rows", file=sys.stderr)
+        return 1
+    print(f"Calibration: a 256 MiB device-to-device copy reads FETCH_SIZE = {max(cf):,.0f} KiB and "
+          f"WRITE_SIZE = {max(cw):,.0f} KiB: FETCH_SIZE is scaled by {sf:.2f}, WRITE_SIZE by {sw:.2f}.\n")
+    print("| kernel | dispatches | fetch MB / dispatch | write MB / dispatch | MB per decode step |")
+    print("|---|---:|---:|---:|---:|")
+    total = 0.0
+    for k in sorted(names, key=lambda k: -sum(f[k]) * sf):
+        mf, mw = sum(f[k]) / len(f[k]) * sf * 1024 / 1e6, sum(w[k]) / len(w[k]) * sw * 1024 / 1e6
+        per_step = (sum(f[k]) * sf + sum(w[k]) * sw) * 1024 / 1e6 / steps
+        total += per_step
+        print(f"| `{k[:90]}` | {len(f[k])} | {mf:.2f} | {mw:.3f} | {per_step:.1f} |")
+    print(f"\nDecode steps (arg-max dispatches): {steps}; traffic per decode step: {total:.1f} MB")
     return 0
 
 
