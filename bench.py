@@ -431,8 +431,8 @@ def counter_summary(dirs: dict, kernel: str, gemm: bool = False) -> int:
         return out
 
     cf, cw = values(dirs["copy_fetch"], "copyBuffer", "FETCH_SIZE"), values(dirs["copy_write"], "copyBuffer", "WRITE_SIZE")
-    if kernel == "decode-step-kernels":
-        return counter_table(dirs, cf, cw, values)
+    if kernel in ("decode-step-kernels", "prefill-kernels"):
+        return counter_table(dirs, cf, cw, values, prefill=kernel == "prefill-kernels")
     kf, kw = values(dirs["fetch"], kernel, "FETCH_SIZE"), values(dirs["write"], kernel, "WRITE_SIZE")
     if not (cf and cw and kf and kw):
         print("missing counter rows", file=sys.stderr)
@@ -454,11 +454,12 @@ def counter_summary(dirs: dict, kernel: str, gemm: bool = False) -> int:
     return 0
 
 
-def counter_table(dirs: dict, cf: list, cw: list, values) -> int:
-    """Per-kernel HBM bytes of a multi-kernel decode run (--counter-kernel
-    decode-step-kernels): every kernel of the decode step with its dispatches
-    and scaled FETCH_SIZE / WRITE_SIZE per dispatch, and the sum per decode
-    step (one arg-max dispatch per step)."""
+def counter_table(dirs: dict, cf: list, cw: list, values, prefill: bool = False) -> int:
+    """Per-kernel HBM bytes: every kernel of a multi-kernel decode run
+    (--counter-kernel decode-step-kernels) with its dispatches and scaled
+    FETCH_SIZE / WRITE_SIZE per dispatch, and the sum per decode step (one
+    arg-max dispatch per step); or every GEMM, attention and RMSNorm kernel of
+    a prefill run (--counter-kernel prefill-kernels), per dispatch."""
     import glob
     import re
     import sqlite3
@@ -477,23 +478,26 @@ def counter_table(dirs: dict, cf: list, cw: list, values) -> int:
         return 1
     sf, sw = 256 * 1024 / max(cf), 256 * 1024 / max(cw)
     f, w = per_kernel(dirs["fetch"], "FETCH_SIZE"), per_kernel(dirs["write"], "WRITE_SIZE")
-    step = ("gemv", "attn_decode", "attn_merge", "argmax", "embed")
-    names = [k for k in f if k in w and any(t in k for t in step)]
-    steps = max((len(f[k]) for k in names if "argmax" in k), default=0)
+    kinds = ("dgemm_kernel", "flash_attn", "rmsnorm_rows") if prefill else \
+        ("gemv", "attn_decode", "attn_merge", "argmax", "embed")
+    names = [k for k in f if k in w and any(t in k for t in kinds)]
+    steps = 1 if prefill else max((len(f[k]) for k in names if "argmax" in k), default=0)
     if not names or not steps:
-        print("missing decode kernel rows", file=sys.stderr)
+        print("missing kernel rows", file=sys.stderr)
         return 1
     print(f"Calibration: a 256 MiB device-to-device copy reads FETCH_SIZE = {max(cf):,.0f} KiB and "
           f"WRITE_SIZE = {max(cw):,.0f} KiB: FETCH_SIZE is scaled by {sf:.2f}, WRITE_SIZE by {sw:.2f}.\n")
-    print("| kernel | dispatches | fetch MB / dispatch | write MB / dispatch | MB per decode step |")
+    print("| kernel | dispatches | fetch MB / dispatch | write MB / dispatch | " +
+          ("MB / dispatch |" if prefill else "MB per decode step |"))
     print("|---|---:|---:|---:|---:|")
     total = 0.0
     for k in sorted(names, key=lambda k: -sum(f[k]) * sf):
         mf, mw = sum(f[k]) / len(f[k]) * sf * 1024 / 1e6, sum(w[k]) / len(w[k]) * sw * 1024 / 1e6
         per_step = (sum(f[k]) * sf + sum(w[k]) * sw) * 1024 / 1e6 / steps
         total += per_step
-        print(f"| `{k[:90]}` | {len(f[k])} | {mf:.2f} | {mw:.3f} | {per_step:.1f} |")
-    print(f"\nDecode steps (arg-max dispatches): {steps}; traffic per decode step: {total:.1f} MB")
+        print(f"| `{k[:90]}` | {len(f[k])} | {mf:.2f} | {mw:.3f} | {mf + mw if prefill else per_step:.1f} |")
+    if not prefill:
+        print(f"\nDecode steps (arg-max dispatches): {steps}; traffic per decode step: {total:.1f} MB")
     return 0
 
 
