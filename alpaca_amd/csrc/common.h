@@ -384,7 +384,13 @@ hipError_t launch_decode_step(int fmt, const DecodeParams& p, int grid, size_t l
 // the 64-query blocks holding a row >= lo_q0 (qlo must be valid there).
 hipError_t launch_flash_attention(const f16* q, const f16* qlo, int ldq, const f16* kc, const f16* vc, int capacity,
                                   int tokens, int heads, int kv_heads, int hd, int start, float* out_f32, f16* out_f16,
-                                  f16* out_f16_lo, hipStream_t st, int p_terms = 0, int lo_q0 = 0, int lo_out0 = 0);
+                                  f16* out_f16_lo, hipStream_t st, int p_terms = 0, int lo_q0 = 0, int lo_out0 = 0,
+                                  unsigned* last_arrive = nullptr, float* last_part = nullptr);
+// With last_arrive and last_part the flash launch computes the last query row
+// in float32 (key splits merged by the last split workgroup of each head):
+// last_arrive holds `heads` counters, zero between launches; last_part
+// flash_last_part_floats(heads, hd) floats.
+size_t flash_last_part_floats(int heads, int hd);
 // Generic online-softmax attention, any hd <= 256, f16 or f32 cache, keys
 // split into `splits` ranges merged by a second kernel when splits > 1.
 int attention_splits(int length, int heads, int tokens);

@@ -54,9 +54,18 @@ struct FlashArgs {
     // two-term launches: query blocks holding a row >= lo_q0 take the second
     // terms of Q and P
     int lo_q0, lo_out0;
+    // exact_last: the last query row (T - 1) is computed in float32 by the
+    // first last_splits rows of workgroups (last_keys keys each; per head a
+    // counter last_arrive, zero between launches, and last_splits x (hd + 2)
+    // floats of last_part), q as its two f16 terms; the query blocks do not
+    // write it
+    int exact_last, last_splits, last_keys;
+    unsigned* last_arrive;
+    float* last_part;
 };
 
 constexpr int BQ = 64, BKV = 64;
+constexpr int kFlashLastSplits = 64;  // key splits of the float32 last row (FlashArgs.exact_last)
 
 // Chunk swizzle of the K and V blocks in LDS: 16-byte chunk c of key row r
 // sits at slot c ^ kv_swz(r), kv_swz(r) = (r0^r3, r0^r2, r1) (bits of r).
@@ -145,7 +154,7 @@ __device__ __forceinline__ void flash_attn_body(const FlashArgs& a, uint8_t* sta
     static_assert(FlashLds<HD, NSET>::BYTES == NSET * NSTAGE * 2 * TILE, "stage buffer size");
 
     const int h = blockIdx.x;
-    const int qb = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks first
+    const int qb = gridDim.y - 1 - blockIdx.y;  // longest (latest) query blocks first (after the exact_last rows)
     const int kvh = h / (a.H / a.KVH);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -424,7 +433,7 @@ __device__ __forceinline__ void flash_attn_body(const FlashArgs& a, uint8_t* sta
                 for (int r = 0; r < 4; r++) oacc[d][r] = fmaf(xo[(d * 4 + r) * 64 + lane], as, oacc[d][r]);
         }
     }
-    if (qi >= a.T) return;
+    if (qi >= a.T - a.exact_last) return;
     const float inv = 1.0f / lsum;  // lsum and O both carry the 2^14
     // oacc[d][r] = O(query qi, dim 16d + 4g + r)
 #pragma unroll
@@ -444,11 +453,176 @@ __device__ __forceinline__ void flash_attn_body(const FlashArgs& a, uint8_t* sta
     }
 }
 
+// The last query row (T - 1, the row whose logits a prefill returns) of head
+// blockIdx.x in float32, split over the keys: workgroup blockIdx.y takes keys
+// [y * last_keys, (y + 1) * last_keys) in chunks of NT / KT keys (KT threads
+// per key, 64 dims each), q = hi + lo (its two f16 terms), scores, running max
+// and P.V (HD / 8 threads per V row) in float32; each chunk's K and V rows are
+// loaded together (V does not wait for the scores).  The split's (max, sum,
+// output) go out as agent-scope stores (written through to the device's point
+// of coherence) and the last split workgroup of the head to arrive (a counter
+// per head, which it returns to zero) merges them with agent-scope loads and
+// writes the row as the kernel writes every row.  These workgroups come first
+// in dispatch order and walk at most two chunks each, so they end long before
+// the kernel's critical path, the longest query block (whose second terms of
+// Q and P this replaces: C1's attention per layer 48.9 -> 40.1-41.0 us).
+template <int HD, int NT, bool OUT16>
+__device__ __forceinline__ void flash_last_row(const FlashArgs& a, uint8_t* lds) {
+    constexpr int KT = HD / 64, CK = NT / KT;  // threads per key, keys per chunk
+    constexpr int TPR = HD / 8, RPP = NT / TPR, VR = CK / RPP;  // P.V: threads per row, rows per pass, passes
+    constexpr int WV = NT / 64;
+    static_assert(VR * RPP == CK && KT * 64 == HD, "shape");
+    float* qs = (float*)lds;  // HD, scaled by scale_log2
+    float* ps = qs + HD;      // CK probabilities of the chunk
+    float* red = ps + CK;     // 2 * WV
+    float* ws = red + 2 * WV; // WV x HD partial outputs
+    const int h = blockIdx.x, sp = blockIdx.y, S = a.last_splits;
+    const int kvh = h / (a.H / a.KVH), tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row = a.T - 1, kend = a.start + a.T;  // keys [0, kend)
+    const int k0 = sp * a.last_keys, k1 = min(k0 + a.last_keys, kend);  // k0 < kend (the launcher's split count)
+    const f16* kbase = a.kc + (int64_t)kvh * a.cap * HD;
+    const f16* vbase = a.vc + (int64_t)kvh * a.cap * HD;
+    if (tid < HD) {
+        const int64_t o = (int64_t)row * a.ldq + h * HD + tid;
+        const float v = a.qlo ? (float)a.q[o] + (float)a.qlo[o] : (float)a.q[o];
+        qs[tid] = v * a.scale_log2;
+    }
+    __syncthreads();
+    const int kl = tid / KT, kp = tid % KT;   // the thread's key in the chunk, its 64-dim part
+    const int tr = tid % TPR, rq = tid / TPR;  // P.V: dims 8 tr .. 8 tr + 7 of rows rq + i RPP
+    float m = -INFINITY, l = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int c0 = k0; c0 < k1; c0 += CK) {
+        // q is read from LDS at every use (not held in 64 registers across chunks)
+        asm volatile("" ::: "memory");
+        // K and V rows past k1 are clamped to row k1 - 1 (loaded, unused)
+        int4 kr[8], vr[VR];
+        const f16* krow = kbase + (int64_t)min(c0 + kl, k1 - 1) * HD + kp * 64;
+#pragma unroll
+        for (int j = 0; j < 8; j++) kr[j] = *(const int4*)(krow + 8 * j);
+#pragma unroll
+        for (int i = 0; i < VR; i++) vr[i] = *(const int4*)(vbase + (int64_t)min(c0 + rq + i * RPP, k1 - 1) * HD + tr * 8);
+        float sc = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const f16* kv = (const f16*)&kr[j];
+#pragma unroll
+            for (int e = 0; e < 8; e++) sc = fmaf(qs[kp * 64 + 8 * j + e], (float)kv[e], sc);
+        }
+        if constexpr (KT == 2) sc += __shfl_xor(sc, 1, 64);
+        if (c0 + kl >= k1) sc = -INFINITY;
+        const float wm = wave_max(sc);
+        if (lane == 0) red[wave] = wm;
+        __syncthreads();
+        float mc = red[0];
+#pragma unroll
+        for (int w = 1; w < WV; w++) mc = fmaxf(mc, red[w]);
+        const float mn = fmaxf(m, mc);  // finite: the chunk holds key c0 < k1
+        const float alpha = exp2f(m - mn);
+        const float pk = exp2f(sc - mn);
+        if (kp == 0) ps[kl] = pk;
+        const float wsum = wave_sum(kp == 0 ? pk : 0.f);
+        if (lane == 0) red[WV + wave] = wsum;
+        __syncthreads();
+        float lc = 0.f;
+#pragma unroll
+        for (int w = 0; w < WV; w++) lc += red[WV + w];
+        l = l * alpha + lc;
+        m = mn;
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[j] *= alpha;
+#pragma unroll
+        for (int i = 0; i < VR; i++) {
+            const float p = ps[rq + i * RPP];  // 0 past k1
+            const f16* v = (const f16*)&vr[i];
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[j] = fmaf(p, (float)v[j], acc[j]);
+        }
+        __syncthreads();  // ps and red are rewritten by the next chunk
+    }
+    // sum the rows of a wave (lanes with one tr), then the waves
+#pragma unroll
+    for (int o = TPR; o < 64; o <<= 1)
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[j] += __shfl_xor(acc[j], o, 64);
+    if (lane < TPR)
+#pragma unroll
+        for (int j = 0; j < 8; j++) ws[wave * HD + tr * 8 + j] = acc[j];
+    __syncthreads();
+    float* pp = a.last_part + ((int64_t)h * S + sp) * (HD + 2);
+    if (tid < HD) {
+        float o = ws[tid];
+#pragma unroll
+        for (int w = 1; w < WV; w++) o += ws[w * HD + tid];
+        __hip_atomic_store(pp + 2 + tid, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) {
+            __hip_atomic_store(pp, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(pp + 1, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    // Each thread waits for its stores to be acknowledged before the barrier,
+    // so the arrival counted after it follows them.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    unsigned* last_s = (unsigned*)(ws + WV * HD);
+    if (tid == 0)
+        *last_s = __hip_atomic_fetch_add(a.last_arrive + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                  (unsigned)(S - 1);
+    __syncthreads();
+    if (!*last_s) return;
+    if (tid == 0) __hip_atomic_store(a.last_arrive + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the merge: the first wave takes the splits' maxima and sums (S <= 64),
+    // then thread groups of HD take every G-th split's outputs, added through LDS
+    auto ld = [](const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    const float* hp = a.last_part + (int64_t)h * S * (HD + 2);
+    float* wts = ps;  // S weights
+    float* part = ws; // NT partial sums
+    if (tid < 64) {
+        const int j = min(tid, S - 1);
+        const float mj = ld(hp + j * (HD + 2)), lj = ld(hp + j * (HD + 2) + 1);
+        const float mt = wave_max(tid < S ? mj : -INFINITY);
+        const float w = tid < S ? exp2f(mj - mt) : 0.f;
+        wts[tid] = w;
+        const float lt = wave_sum(w * lj);
+        if (tid == 0) red[0] = lt;
+    }
+    __syncthreads();
+    constexpr int G = NT / HD;
+    {
+        const int d = tid % HD, grp = tid / HD;
+        float o = 0.f;
+        for (int j = grp; j < S; j += G) o = fmaf(ld(hp + j * (HD + 2) + 2 + d), wts[j], o);
+        part[tid] = o;
+    }
+    __syncthreads();
+    if (tid < HD) {
+        float o = part[tid];
+#pragma unroll
+        for (int g = 1; g < G; g++) o += part[g * HD + tid];
+        o /= red[0];
+        const int64_t oi = ((int64_t)row * a.H + h) * HD + tid;
+        if constexpr (OUT16) {
+            const f16 hi = (f16)o;
+            a.out16[oi] = hi;
+            if (a.out16lo && row >= a.lo_out0) a.out16lo[oi] = (f16)(o - (float)hi);
+        } else {
+            a.out32[oi] = o;
+        }
+    }
+}
+
 // Query blocks holding a row at or past a.lo_q0 take Q and P as TT / PT
-// terms; the others (of a two-term launch) as one f16 term each.
+// terms; the others (of a two-term launch) as one f16 term each.  With
+// a.exact_last the first row of workgroups computes the last query row
+// (flash_last_row) and the query blocks follow.
 template <int HD, int NSET, bool OUT16, bool TT, bool PT>
 __global__ __launch_bounds__(256 * NSET) void flash_attn_kernel(FlashArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t stage_lds[FlashLds<HD, NSET>::BYTES];
+    if constexpr (!TT && !PT && NSET == 2) {
+        if (a.exact_last && (int)blockIdx.y < a.last_splits) {
+            flash_last_row<HD, 256 * NSET, OUT16>(a, stage_lds);
+            return;
+        }
+    }
     if constexpr (TT || PT) {
         const int qb = gridDim.y - 1 - blockIdx.y;
         if ((qb + 1) * BQ > a.lo_q0) flash_attn_body<HD, NSET, OUT16, TT, PT>(a, stage_lds);
@@ -889,7 +1063,8 @@ hipError_t flash_dispatch(const FlashArgs& a, dim3 grid, int hd, bool out16, hip
 
 hipError_t launch_flash_attention(const f16* q, const f16* qlo, int ldq, const f16* kc, const f16* vc, int capacity,
                                   int tokens, int heads, int kv_heads, int hd, int start, float* out_f32, f16* out_f16,
-                                  f16* out_f16_lo, hipStream_t st, int p_terms, int lo_q0, int lo_out0) {
+                                  f16* out_f16_lo, hipStream_t st, int p_terms, int lo_q0, int lo_out0,
+                                  unsigned* last_arrive, float* last_part) {
     if (tokens <= 0) return hipSuccess;
     FlashArgs a;
     a.q = q;
@@ -908,12 +1083,36 @@ hipError_t launch_flash_attention(const f16* q, const f16* qlo, int ldq, const f
     a.out16lo = out_f16_lo;
     a.lo_q0 = lo_q0;
     a.lo_out0 = lo_out0;
-    dim3 grid(heads, (tokens + BQ - 1) / BQ);
+    // The float32 last row pays where the query blocks run as two wave-sets
+    // (small grids: the two-term last block is then the kernel's critical path);
+    // on larger grids (one set) the last block's second terms cost less than the
+    // extra workgroups, and the launch takes lo_q0 as given.
+    const dim3 qgrid(heads, (tokens + BQ - 1) / BQ);
+    a.exact_last = last_arrive && last_part && hd == 64 && flash_sets(qgrid) == 2 ? 1 : 0;
+    a.last_arrive = last_arrive;
+    a.last_part = last_part;
+    a.last_splits = 0;
+    a.last_keys = 0;
+    if (a.exact_last) {
+        // two chunks of 512 keys per split workgroup, at most kFlashLastSplits splits
+        const int ck = 512, kend = start + tokens;
+        a.last_splits = std::min(kFlashLastSplits, (kend + 2 * ck - 1) / (2 * ck));
+        a.last_keys = (kend + a.last_splits - 1) / a.last_splits;
+        a.last_splits = (kend + a.last_keys - 1) / a.last_keys;  // every split holds a key
+    }
+    dim3 grid(heads, (tokens + BQ - 1) / BQ + a.last_splits);
+    if (a.exact_last) {
+        // (two sets, as for the query grid alone)
+        flash_launch64<2, false, false>(a, grid, out_f16, st);
+        return hipGetLastError();
+    }
     const bool pt = p_terms ? p_terms == 2 : qlo != nullptr;
     if (!qlo) return pt ? flash_dispatch<false, true>(a, grid, hd, out_f16, st)
                         : flash_dispatch<false, false>(a, grid, hd, out_f16, st);
     return pt ? flash_dispatch<true, true>(a, grid, hd, out_f16, st) : flash_dispatch<true, false>(a, grid, hd, out_f16, st);
 }
+
+size_t flash_last_part_floats(int heads, int hd) { return (size_t)heads * kFlashLastSplits * (hd + 2); }
 
 // Splits for the generic kernel: decode spreads the context over >= 64-key
 // splits (up to 64 of them); batched queries already fill the chip.

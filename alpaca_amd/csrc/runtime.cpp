@@ -663,6 +663,8 @@ struct ahip_session {
     bool lo_all_rows = false;  // second terms on every row, not only the last row's tiles
     bool qkv_lo_all = false;   // the QKV GEMM's q columns take the second term on every row too
     int fuse_qkv_rope = 1;  // ALPACA_HIP_FUSE_QKV_ROPE at creation; 0: RoPE + KV append as their own kernel
+    int exact_last_row = 1;  // ALPACA_HIP_EXACT_LAST_ROW at creation; 0: two-term last query block instead
+    DevBuf last_arrive, last_part;  // the float32 last row of the flash launch: counters per head, split partials
     // Numerics diagnostics, read at creation: ALPACA_HIP_PREFILL_ATTENTION=generic runs the fast prefill's
     // attention as the float32 kernel the exact prefill uses; ALPACA_HIP_PREFILL_GEMM=f32 its projections as
     // the exact float32 GEMMs.
@@ -1169,6 +1171,12 @@ extern "C" int ahip_session_create(ahip_model* m, int capacity, int max_batch, i
         s->qkv_lo_all = s->lo_all_rows || !(q && !std::strcmp(q, "kv"));
     }
     s->fuse_qkv_rope = env_int("ALPACA_HIP_FUSE_QKV_ROPE", 1) != 0;
+    s->exact_last_row = s->two_term && env_int("ALPACA_HIP_EXACT_LAST_ROW", 1) != 0;
+    if (s->exact_last_row) {
+        if (int rc = s->last_arrive.alloc((size_t)c.head_count * 4)) return rc;
+        if (int rc = s->last_part.alloc(flash_last_part_floats(c.head_count, c.head_dim) * 4)) return rc;
+        HIP_OR(hipMemset(s->last_arrive.p, 0, (size_t)c.head_count * 4), "hipMemset");
+    }
     {
         const char* a = std::getenv("ALPACA_HIP_PREFILL_ATTENTION");
         const char* g = std::getenv("ALPACA_HIP_PREFILL_GEMM");
@@ -1394,11 +1402,17 @@ static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, 
     for (int k = 0; k < n_before; k++) HIP_OR(hipStreamWaitEvent(st, before_attn[k], 0), "hipStreamWaitEvent");
     s->stage("attention");
     if (flash) {
-        // Q and P take their second terms only in the query block of the last row (the
-        // longest of the causal walk; a two-term block takes twice the MFMA work).
+        // The last row, whose logits the call returns, is computed in float32 by
+        // workgroups of its own (q as its two f16 terms) while the query blocks take
+        // one f16 term of Q and P (ALPACA_HIP_EXACT_LAST_ROW=0: instead Q and P take
+        // their second terms in the last row's query block, the longest of the causal
+        // walk, where the doubled MFMA work sets the kernel's time); with second
+        // terms on every row, every query block takes them.
+        const bool exact_last = !all && qhlo && s->exact_last_row;
         LAUNCH(launch_flash_attention(qh, qhlo, QW, (const f16*)kc, (const f16*)vc, s->capacity, n, c.head_count,
                                       c.kv_head_count, hd, pos, nullptr, ctxh, ctxhlo, st, p_terms,
-                                      all ? 0 : n - 1, tail0));
+                                      all ? 0 : n - 1, tail0, exact_last ? s->last_arrive.as<unsigned>() : nullptr,
+                                      exact_last ? s->last_part.as<float>() : nullptr));
     } else {
         LAUNCH(launch_attention_generic(qkv, LDQKV, kc, vc, s->kv_f16, s->capacity, n, c.head_count, c.kv_head_count,
                                         hd, pos, 1, nullptr, ctx, st));

@@ -169,6 +169,48 @@ def test_two_stream_prefill_matches_one_stream(hip_ctx, spec, prec, rows):
     model.close()
 
 
+# ------------------------------------------------------------------ float32 last row
+
+@pytest.mark.parametrize("spec", [C1_2L, C4_LONG], ids=lambda s: s.name)
+def test_float32_last_row_matches_two_term_last_block(hip_ctx, spec):
+    """Where the flash launch runs two wave-sets (head dim 64, small grids),
+    the last query row of a prefill that returns logits is computed in
+    float32 by workgroups of its own (key splits merged by the last one to
+    arrive, a counter per head) and the other rows take one f16 term of Q and
+    P; with ALPACA_HIP_EXACT_LAST_ROW=0 (read at session creation) the last
+    row's query block takes both second terms instead.  Both approximate the
+    same float32 attention: the logits agree to 2.5e-4 of the peak (the other
+    rows of that block round Q and P differently) with the same greedy token,
+    over one split (100 tokens), several (1000), a two-stream chunk (3100) and
+    a second chunk at position 1200.  A repeated prefill on the same session
+    is bit-identical (the counters return to zero, the merge order is fixed).
+    Each path is held to the CPU oracle at full size by the workload tests."""
+    model = HIPLlamaModel(hip_ctx, spec.config, built(spec))
+    prompt = synth.prompt_tokens(spec, 3100)
+    a = model.make_session(capacity=3200, max_batch=3200)
+    with env(ALPACA_HIP_EXACT_LAST_ROW=0):
+        b = model.make_session(capacity=3200, max_batch=3200)
+    for chunks in ([100], [1000], [3100], [1200, 500]):
+        outs = []
+        for s in (a, b, a):
+            s.reset()
+            p0 = 0
+            for n in chunks:
+                g = s.forward(prompt[p0:p0 + n])
+                p0 += n
+            outs.append(g)
+        ga, gb, ga2 = outs
+        assert np.array_equal(ga, ga2), f"{spec.name} {chunks}: repeated prefill differs"
+        d = float(np.abs(ga - gb).max())
+        print(f"[metrics] {spec.name} chunks {chunks}: float32 last row vs two-term block max |d| {d:.2e} "
+              f"({d / float(np.abs(gb).max()):.2e} of the peak)")
+        assert d <= 2.5e-4 * float(np.abs(gb).max()), f"{spec.name} {chunks}: max |d| {d:.3e}"
+        assert int(np.argmax(ga)) == int(np.argmax(gb))
+    a.close()
+    b.close()
+    model.close()
+
+
 # ------------------------------------------------------------------ prefill weight cache
 
 LAYER_MATS = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
