@@ -247,6 +247,9 @@ enum { GEMV_STORE = 0, GEMV_ADD = 1, GEMV_SWIGLU = 2, GEMV_QKV_ROPE = 3 };
 // pos_dev set, only the splits covering positions 0..*pos_dev are read).
 struct GemvInput {
     const float* x = nullptr;
+    // or the row as two f16 terms (x = xh + xl): the last row of a prefill GEMM
+    const f16* xh = nullptr;
+    const f16* xl = nullptr;
     const float* norm = nullptr;
     float eps = 0.f;
     const float* partials = nullptr;
@@ -268,6 +271,12 @@ hipError_t launch_gemv_ex(const DevMatrix& w, const DevMatrix* w_up, const GemvI
                           float* out, int mode, hipStream_t st);
 hipError_t launch_gemv(const DevMatrix& w, const DevMatrix* w_up, const float* x, const float* norm, float eps,
                        float* out, int mode, hipStream_t st);
+// The last row of a prefill GEMM in float32 from its two f16 terms (x = xh +
+// xl): GEMV_ADD adds W x to out (the residual row); GEMV_SWIGLU writes
+// silu(Wg x) * (Wu x) as two f16 terms (outh, outl), the down projection's
+// input row.
+hipError_t launch_gemv_pair(const DevMatrix& w, const DevMatrix* w_up, const f16* xh, const f16* xl, float* out,
+                            f16* outh, f16* outl, int mode, hipStream_t st);
 // Whether w's decode products take the streamed GEMV (large matrices).
 bool gemv_streams(const DevMatrix& w);
 

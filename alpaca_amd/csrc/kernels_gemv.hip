@@ -41,9 +41,23 @@ struct GemvArgs {
     GemvInput in;
     GemvRope rope;
     float* out;
+    f16* outh = nullptr;  // GEMV_SWIGLU with f16 output: the two terms of each value
+    f16* outl = nullptr;
 };
 
-enum { IN_X = 0, IN_NORM = 1, IN_MERGE = 2 };
+enum { IN_X = 0, IN_NORM = 1, IN_MERGE = 2, IN_PAIR = 3 };
+
+// out[row] = silu(g) * u, as float32 or (outh set) as two f16 terms.
+__device__ __forceinline__ void swiglu_store(const GemvArgs& a, int64_t row, float g, float u) {
+    const float v = (g / (1.0f + expf(-g))) * u;
+    if (a.outh) {
+        const f16 hi = (f16)v;
+        a.outh[row] = hi;
+        a.outl[row] = (f16)(v - (float)hi);
+    } else {
+        a.out[row] = v;
+    }
+}
 
 // Stages the input row (K floats) into LDS.
 template <int INP>
@@ -86,6 +100,8 @@ __device__ __forceinline__ void stage_input(const GemvInput& in, int K, float* x
         ss = block_sum(ss, red);
         const float scale = 1.0f / sqrtf(ss / (float)K + in.eps);
         for (int i = threadIdx.x; i < K; i += kThreads) xs[i] = (in.x[i] * scale) * in.norm[i];
+    } else if constexpr (INP == IN_PAIR) {
+        for (int i = threadIdx.x; i < K; i += kThreads) xs[i] = (float)in.xh[i] + (float)in.xl[i];
     } else {
         for (int i = threadIdx.x; i < K; i += kThreads) xs[i] = in.x[i];
     }
@@ -173,7 +189,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     if (valid && li == 0) {
         if (MODE == GEMV_STORE) a.out[row] = acc;
         else if (MODE == GEMV_ADD) a.out[row] += acc;
-        else a.out[row] = (acc / (1.0f + expf(-acc))) * acc2;
+        else swiglu_store(a, row, acc, acc2);
     }
 }
 
@@ -258,11 +274,17 @@ __device__ __forceinline__ float chunk_dot_rot(const int4& q, float d, int c, co
 template <int FMT, int INP, int XQ>
 struct StageRow {
     float4 xv[XQ], gv[XQ];
+    uint2 ph[INP == IN_PAIR ? XQ : 1], pl[INP == IN_PAIR ? XQ : 1];  // IN_PAIR: the quad's two f16 terms
     __device__ __forceinline__ void issue(const GemvInput& in, int nq) {
 #pragma unroll
         for (int i = 0; i < XQ; i++) {
             const int Q = min((int)threadIdx.x + i * kThreads, nq - 1);
-            xv[i] = ((const float4*)in.x)[Q];
+            if constexpr (INP == IN_PAIR) {
+                ph[i] = ((const uint2*)in.xh)[Q];
+                pl[i] = ((const uint2*)in.xl)[Q];
+            } else {
+                xv[i] = ((const float4*)in.x)[Q];
+            }
             if constexpr (INP == IN_NORM) gv[i] = ((const float4*)in.norm)[Q];
         }
     }
@@ -281,7 +303,15 @@ struct StageRow {
         for (int i = 0; i < XQ; i++) {
             const int Q = threadIdx.x + i * kThreads;
             if (Q < nq) {
-                float4 v = xv[i];
+                float4 v;
+                if constexpr (INP == IN_PAIR) {
+                    const f16* h = (const f16*)&ph[i];
+                    const f16* l = (const f16*)&pl[i];
+                    v = make_float4((float)h[0] + (float)l[0], (float)h[1] + (float)l[1], (float)h[2] + (float)l[2],
+                                    (float)h[3] + (float)l[3]);
+                } else {
+                    v = xv[i];
+                }
                 if constexpr (INP == IN_NORM) {
                     v.x = (v.x * scale) * gv[i].x;
                     v.y = (v.y * scale) * gv[i].y;
@@ -364,7 +394,7 @@ __global__ __launch_bounds__(kThreads) void gemv_stream_kernel(GemvArgs a, int t
         } else if (row < rows && li == 0) {
             if (MODE == GEMV_STORE) a.out[row] = acc[0];
             else if (MODE == GEMV_ADD) a.out[row] += acc[0];
-            else a.out[row] = (acc[0] / (1.0f + expf(-acc[0]))) * acc[NM - 1];
+            else swiglu_store(a, row, acc[0], acc[NM - 1]);
         }
     };
     // The next tile's loads go out before this tile is multiplied; the two
@@ -484,10 +514,12 @@ template <int FMT>
 hipError_t dispatch_fmt(int lpr, int mode, int inp, const GemvArgs& a, hipStream_t st) {
     if (mode == GEMV_STORE) return inp == IN_NORM ? dispatch<FMT, GEMV_STORE, IN_NORM>(lpr, a, st)
                                                   : dispatch<FMT, GEMV_STORE, IN_X>(lpr, a, st);
-    if (mode == GEMV_ADD) return inp == IN_MERGE ? dispatch<FMT, GEMV_ADD, IN_MERGE>(lpr, a, st)
-                                                 : dispatch<FMT, GEMV_ADD, IN_X>(lpr, a, st);
-    if (mode == GEMV_SWIGLU) return inp == IN_NORM ? dispatch<FMT, GEMV_SWIGLU, IN_NORM>(lpr, a, st)
-                                                   : dispatch<FMT, GEMV_SWIGLU, IN_X>(lpr, a, st);
+    if (mode == GEMV_ADD) return inp == IN_MERGE  ? dispatch<FMT, GEMV_ADD, IN_MERGE>(lpr, a, st)
+                                 : inp == IN_PAIR ? dispatch<FMT, GEMV_ADD, IN_PAIR>(lpr, a, st)
+                                                  : dispatch<FMT, GEMV_ADD, IN_X>(lpr, a, st);
+    if (mode == GEMV_SWIGLU) return inp == IN_NORM   ? dispatch<FMT, GEMV_SWIGLU, IN_NORM>(lpr, a, st)
+                                    : inp == IN_PAIR ? dispatch<FMT, GEMV_SWIGLU, IN_PAIR>(lpr, a, st)
+                                                     : dispatch<FMT, GEMV_SWIGLU, IN_X>(lpr, a, st);
     return dispatch<FMT, GEMV_QKV_ROPE, IN_NORM>(lpr, a, st);
 }
 
@@ -521,7 +553,9 @@ static bool stream_pays(const DevMatrix& w, const GemvInput& in, int mode, int i
     const char* e = std::getenv("ALPACA_HIP_GEMV_STREAM");
     if (e && e[0] == '0') return false;
     if (bytes < (4 << 20) || nch > 64 * 8 || w.cols % 4 || w.cols / 4 > kMaxStageQuads * kThreads) return false;
-    if (inp == IN_MERGE || ((uintptr_t)in.x & 15) || (inp == IN_NORM && ((uintptr_t)in.norm & 15))) return false;
+    if (inp == IN_MERGE || ((uintptr_t)in.x & 15) || (inp == IN_NORM && ((uintptr_t)in.norm & 15)) ||
+        (inp == IN_PAIR && (((uintptr_t)in.xh | (uintptr_t)in.xl) & 7)))
+        return false;
     return mode != GEMV_QKV_ROPE || tall_shape(nch).lpr <= 32;
 }
 
@@ -536,15 +570,18 @@ hipError_t dispatch_stream_fmt(int mode, int inp, const GemvArgs& a, hipStream_t
     if (mode == GEMV_QKV_ROPE && ts.lpr > 32) return hipErrorInvalidValue;
     if (mode == GEMV_STORE) return inp == IN_NORM ? dispatch_stream<FMT, GEMV_STORE, IN_NORM>(ts, a, st)
                                                   : dispatch_stream<FMT, GEMV_STORE, IN_X>(ts, a, st);
-    if (mode == GEMV_ADD) return dispatch_stream<FMT, GEMV_ADD, IN_X>(ts, a, st);
-    if (mode == GEMV_SWIGLU) return inp == IN_NORM ? dispatch_stream<FMT, GEMV_SWIGLU, IN_NORM>(ts, a, st)
-                                                   : dispatch_stream<FMT, GEMV_SWIGLU, IN_X>(ts, a, st);
+    if (mode == GEMV_ADD) return inp == IN_PAIR ? dispatch_stream<FMT, GEMV_ADD, IN_PAIR>(ts, a, st)
+                                                : dispatch_stream<FMT, GEMV_ADD, IN_X>(ts, a, st);
+    if (mode == GEMV_SWIGLU) return inp == IN_NORM   ? dispatch_stream<FMT, GEMV_SWIGLU, IN_NORM>(ts, a, st)
+                                    : inp == IN_PAIR ? dispatch_stream<FMT, GEMV_SWIGLU, IN_PAIR>(ts, a, st)
+                                                     : dispatch_stream<FMT, GEMV_SWIGLU, IN_X>(ts, a, st);
     return dispatch_stream<FMT, GEMV_QKV_ROPE, IN_NORM>(ts, a, st);
 }
 
 hipError_t launch_gemv_ex(const DevMatrix& w, const DevMatrix* w_up, const GemvInput& in, const GemvRope* rope,
                           float* out, int mode, hipStream_t st) {
-    const int inp = in.partials ? IN_MERGE : in.norm ? IN_NORM : IN_X;
+    const int inp = in.partials ? IN_MERGE : in.norm ? IN_NORM : in.xh ? IN_PAIR : IN_X;
+    if (inp == IN_PAIR && (!in.xl || (mode != GEMV_ADD && mode != GEMV_SWIGLU))) return hipErrorInvalidValue;
     if (inp == IN_MERGE && ((long)in.heads * in.splits > 4096 || in.heads > 256 || mode != GEMV_ADD))
         return hipErrorInvalidValue;
     if (mode == GEMV_QKV_ROPE && (!rope || inp != IN_NORM)) return hipErrorInvalidValue;
@@ -582,4 +619,34 @@ hipError_t launch_gemv(const DevMatrix& w, const DevMatrix* w_up, const float* x
     in.norm = norm;
     in.eps = eps;
     return launch_gemv_ex(w, w_up, in, nullptr, out, mode, st);
+}
+
+hipError_t launch_gemv_pair(const DevMatrix& w, const DevMatrix* w_up, const f16* xh, const f16* xl, float* out,
+                            f16* outh, f16* outl, int mode, hipStream_t st) {
+    if (!xh || !xl || (mode == GEMV_SWIGLU && (!w_up || !outh || !outl)) || (mode == GEMV_ADD && !out) ||
+        (mode != GEMV_ADD && mode != GEMV_SWIGLU))
+        return hipErrorInvalidValue;
+    GemvInput in;
+    in.xh = xh;
+    in.xl = xl;
+    GemvArgs a;
+    a.w = w;
+    a.u = w_up ? *w_up : w;
+    a.in = in;
+    a.out = out;
+    a.outh = outh;
+    a.outl = outl;
+    if (stream_pays(w, in, mode, IN_PAIR)) {
+        switch (w.dtype) {
+        case DT_Q8_0: return dispatch_stream_fmt<DT_Q8_0>(mode, IN_PAIR, a, st);
+        case DT_Q4_0: return dispatch_stream_fmt<DT_Q4_0>(mode, IN_PAIR, a, st);
+        default: return dispatch_stream_fmt<DT_F16>(mode, IN_PAIR, a, st);
+        }
+    }
+    const int lpr = pick_lpr(w.rows);
+    switch (w.dtype) {
+    case DT_Q8_0: return dispatch_fmt<DT_Q8_0>(lpr, mode, IN_PAIR, a, st);
+    case DT_Q4_0: return dispatch_fmt<DT_Q4_0>(lpr, mode, IN_PAIR, a, st);
+    default: return dispatch_fmt<DT_F16>(lpr, mode, IN_PAIR, a, st);
+    }
 }

@@ -1326,6 +1326,24 @@ static int encode_decode_layer(ahip_session* s, int li, int pos, const int* pos_
 // set) is recorded once these rows' K/V are in the cache; the attention first
 // waits for the n_before events of before_attn (earlier rows' K/V).
 // `last`: these rows end with the row whose logits the call returns.
+// Which of a layer's Wo, gate/up and down GEMMs take the returned row as a
+// float32 GEMV (encode_mfma_layer): those whose weights (gate and up
+// together) are at least 1 MB.  Per layer at 4,096 rows against the tail
+// rows' second terms, the GEMMs gain (us) 0.6 / 8 / 0.4 at the 135M shape,
+// 3.5 / 16 / 12 at the 360M shape and 13 / 42 / 50 at the 1.7B shape, for
+// about 3 us per GEMV launch on the small matrices.
+// ALPACA_HIP_LAST_ROW_GEMV (read per call): a mask of kSide* bits instead.
+enum : int { kSideWo = 1, kSideGateUp = 2, kSideDown = 4 };
+static int last_row_gemv_mask(const ahip_model::Layer& L) {
+    const int forced = env_int("ALPACA_HIP_LAST_ROW_GEMV", -1);
+    if (forced >= 0) return forced & 7;
+    auto bytes = [](const DevMatrix& w) { return raw_bytes(w.dtype, (int64_t)w.rows * w.cols); };
+    const int64_t mb = 1 << 20;
+    return (bytes(L.pre(L.wo, L.wo16)) >= mb ? kSideWo : 0) |
+           (bytes(L.pre(L.gate, L.gate16)) + bytes(L.pre(L.up, L.up16)) >= mb ? kSideGateUp : 0) |
+           (bytes(L.pre(L.down, L.down16)) >= mb ? kSideDown : 0);
+}
+
 static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, bool flash, bool last, hipStream_t st,
                              hipEvent_t after_qkv, const hipEvent_t* before_attn = nullptr, int n_before = 0) {
     ahip_model* m = s->m;
@@ -1402,13 +1420,17 @@ static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, 
     for (int k = 0; k < n_before; k++) HIP_OR(hipStreamWaitEvent(st, before_attn[k], 0), "hipStreamWaitEvent");
     s->stage("attention");
     if (flash) {
-        // The last row, whose logits the call returns, is computed in float32 by
-        // workgroups of its own (q as its two f16 terms) while the query blocks take
-        // one f16 term of Q and P (ALPACA_HIP_EXACT_LAST_ROW=0: instead Q and P take
-        // their second terms in the last row's query block, the longest of the causal
-        // walk, where the doubled MFMA work sets the kernel's time); with second
-        // terms on every row, every query block takes them.
-        const bool exact_last = !all && qhlo && s->exact_last_row;
+        // Past the first 256 rows the last row, whose logits the call returns, is
+        // computed in float32 by workgroups of its own (q as its two f16 terms)
+        // while the query blocks take one f16 term of Q and P
+        // (ALPACA_HIP_EXACT_LAST_ROW=0: instead Q and P take their second terms in
+        // the last row's query block, the longest of the causal walk, where the
+        // doubled MFMA work sets the kernel's time).  Shorter calls keep the second
+        // terms on the whole block: there the other rows of the block are most of
+        // the K/V rows later tokens read (a 40-token prompt of a 256-wide model
+        // with weights of standard deviation 0.1 then missed the logit bound by a
+        // decode step).  With second terms on every row, every block takes them.
+        const bool exact_last = !all && qhlo && s->exact_last_row && tail0 > 0;
         LAUNCH(launch_flash_attention(qh, qhlo, QW, (const f16*)kc, (const f16*)vc, s->capacity, n, c.head_count,
                                       c.kv_head_count, hd, pos, nullptr, ctxh, ctxhlo, st, p_terms,
                                       all ? 0 : n - 1, tail0, exact_last ? s->last_arrive.as<unsigned>() : nullptr,
@@ -1418,17 +1440,45 @@ static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, 
                                         hd, pos, 1, nullptr, ctx, st));
         LAUNCH(launch_f32_to_f16(ctx, ctxh, ctxhlo, (int64_t)n * QW, st));
     }
+    // Wo, gate/up and down: the returned row either takes the second term of
+    // its input inside the GEMM (with the tail rows from tail0, whose tiles then
+    // run twice the MFMA work), or (last_row_gemv, past the first 256 rows as
+    // for attention) the GEMM covers rows [0, n - 1) with one term and the last
+    // row is a float32 GEMV over its two f16 terms (launch_gemv_pair): one more
+    // launch against the tail tiles' second terms, which set the time of GEMMs
+    // over about one round of workgroups and add a sixteenth of the work of
+    // larger ones.
+    const int side = (!all && last && tail0 > 0) ? last_row_gemv_mask(L) : 0;
+    const int64_t lr = n - 1;  // the last row
     s->stage("attn out projection (+residual)");
-    LAUNCH(launch_gemm_mfma(ctxh, ctxhlo, QW, n, L.pre(L.wo, L.wo16), nullptr, x, nullptr, nullptr, H, GEMM_ACC, st,
-                            lo_tile));
+    const DevMatrix& wo = L.pre(L.wo, L.wo16);
+    if ((side & kSideWo) && ctxhlo) {
+        LAUNCH(launch_gemm_mfma(ctxh, nullptr, QW, n - 1, wo, nullptr, x, nullptr, nullptr, H, GEMM_ACC, st));
+        LAUNCH(launch_gemv_pair(wo, nullptr, ctxh + lr * QW, ctxhlo + lr * QW, x + lr * H, nullptr, nullptr, GEMV_ADD,
+                                st));
+    } else {
+        LAUNCH(launch_gemm_mfma(ctxh, ctxhlo, QW, n, wo, nullptr, x, nullptr, nullptr, H, GEMM_ACC, st, lo_tile));
+    }
     s->stage("rmsnorm");
     LAUNCH(launch_rmsnorm(x, L.ffn_norm.as<float>(), nullptr, xh, xhlo_ffn, n, H, c.rms_norm_eps, st, tail0));
     s->stage("ffn gate+up+silu");
-    LAUNCH(launch_gemm_mfma(xh, xhlo_ffn, H, n, L.pre(L.gate, L.gate16), &L.pre(L.up, L.up16), nullptr, ffnh, ffnhlo, F,
-                            GEMM_SWIGLU, st, lo_tile, tail0));
+    const DevMatrix &wg = L.pre(L.gate, L.gate16), &wu = L.pre(L.up, L.up16);
+    if ((side & kSideGateUp) && xhlo_ffn && ffnhlo) {
+        LAUNCH(launch_gemm_mfma(xh, nullptr, H, n - 1, wg, &wu, nullptr, ffnh, ffnhlo, F, GEMM_SWIGLU, st, 0, tail0));
+        LAUNCH(launch_gemv_pair(wg, &wu, xh + lr * H, xhlo_ffn + lr * H, nullptr, ffnh + lr * F, ffnhlo + lr * F,
+                                GEMV_SWIGLU, st));
+    } else {
+        LAUNCH(launch_gemm_mfma(xh, xhlo_ffn, H, n, wg, &wu, nullptr, ffnh, ffnhlo, F, GEMM_SWIGLU, st, lo_tile, tail0));
+    }
     s->stage("ffn down (+residual)");
-    LAUNCH(launch_gemm_mfma(ffnh, ffnhlo, F, n, L.pre(L.down, L.down16), nullptr, x, nullptr, nullptr, H, GEMM_ACC,
-                            st, lo_tile));
+    const DevMatrix& wd = L.pre(L.down, L.down16);
+    if ((side & kSideDown) && ffnhlo) {
+        LAUNCH(launch_gemm_mfma(ffnh, nullptr, F, n - 1, wd, nullptr, x, nullptr, nullptr, H, GEMM_ACC, st));
+        LAUNCH(launch_gemv_pair(wd, nullptr, ffnh + lr * F, ffnhlo + lr * F, x + lr * H, nullptr, nullptr, GEMV_ADD,
+                                st));
+    } else {
+        LAUNCH(launch_gemm_mfma(ffnh, ffnhlo, F, n, wd, nullptr, x, nullptr, nullptr, H, GEMM_ACC, st, lo_tile));
+    }
     return AHIP_OK;
 }
 

@@ -172,40 +172,56 @@ def test_two_stream_prefill_matches_one_stream(hip_ctx, spec, prec, rows):
 # ------------------------------------------------------------------ float32 last row
 
 @pytest.mark.parametrize("spec", [C1_2L, C4_LONG], ids=lambda s: s.name)
-def test_float32_last_row_matches_two_term_last_block(hip_ctx, spec):
-    """Where the flash launch runs two wave-sets (head dim 64, small grids),
-    the last query row of a prefill that returns logits is computed in
-    float32 by workgroups of its own (key splits merged by the last one to
-    arrive, a counter per head) and the other rows take one f16 term of Q and
-    P; with ALPACA_HIP_EXACT_LAST_ROW=0 (read at session creation) the last
-    row's query block takes both second terms instead.  Both approximate the
-    same float32 attention: the logits agree to 2.5e-4 of the peak (the other
-    rows of that block round Q and P differently) with the same greedy token,
-    over one split (100 tokens), several (1000), a two-stream chunk (3100) and
-    a second chunk at position 1200.  A repeated prefill on the same session
-    is bit-identical (the counters return to zero, the merge order is fixed).
-    Each path is held to the CPU oracle at full size by the workload tests."""
+def test_float32_last_row_matches_two_term_tail(hip_ctx, spec):
+    """The row a prefill returns (its last), past the first 256 rows of a call:
+    - attention: where the flash launch runs two wave-sets (head dim 64, small
+      grids) the row is computed in float32 by workgroups of its own (key
+      splits merged by the last one to arrive, a counter per head) and the
+      other rows take one f16 term of Q and P; ALPACA_HIP_EXACT_LAST_ROW=0 (read
+      at session creation) keeps both second terms on the row's query block;
+    - Wo, gate/up and down: GEMMs of at least 1 MB of weights cover the other
+      rows with one term and the row is a float32 GEMV over its two f16 terms;
+      ALPACA_HIP_LAST_ROW_GEMV (a mask, read per call: 0 none, 7 all three)
+      chooses, and with 0 the tail rows from the last rounded down to 256 take
+      their second terms in the GEMMs.
+    Every form approximates the same float32 row: the logits agree with the
+    all-second-terms form to 2.5e-4 of the peak (the tail's other rows round
+    differently) with the same greedy token, over one attention split (300
+    tokens), several (1000), a two-stream chunk (3100) and a second chunk at
+    position 1200.  A repeated prefill on the same session is bit-identical
+    (the counters return to zero, the merge order is fixed), and a 100-token
+    call, below 256 rows, keeps the second terms (bit-identical to them).
+    Each default path is held to the CPU oracle at full size by the workload
+    tests."""
     model = HIPLlamaModel(hip_ctx, spec.config, built(spec))
     prompt = synth.prompt_tokens(spec, 3100)
     a = model.make_session(capacity=3200, max_batch=3200)
     with env(ALPACA_HIP_EXACT_LAST_ROW=0):
         b = model.make_session(capacity=3200, max_batch=3200)
-    for chunks in ([100], [1000], [3100], [1200, 500]):
-        outs = []
-        for s in (a, b, a):
-            s.reset()
-            p0 = 0
+
+    def run(s, mask):
+        s.reset()
+        p0 = 0
+        with env(ALPACA_HIP_LAST_ROW_GEMV=mask):
             for n in chunks:
                 g = s.forward(prompt[p0:p0 + n])
                 p0 += n
-            outs.append(g)
-        ga, gb, ga2 = outs
-        assert np.array_equal(ga, ga2), f"{spec.name} {chunks}: repeated prefill differs"
-        d = float(np.abs(ga - gb).max())
-        print(f"[metrics] {spec.name} chunks {chunks}: float32 last row vs two-term block max |d| {d:.2e} "
-              f"({d / float(np.abs(gb).max()):.2e} of the peak)")
-        assert d <= 2.5e-4 * float(np.abs(gb).max()), f"{spec.name} {chunks}: max |d| {d:.3e}"
-        assert int(np.argmax(ga)) == int(np.argmax(gb))
+        return g
+
+    for chunks in ([100], [300], [1000], [3100], [1200, 500]):
+        ref = run(b, "0")  # second terms on the tail, no float32 row
+        forms = {"default": run(a, None), "all GEMVs": run(a, "7"), "attention only": run(a, "0"),
+                 "GEMVs only": run(b, None)}
+        assert np.array_equal(forms["default"], run(a, None)), f"{spec.name} {chunks}: repeated prefill differs"
+        for name, g in forms.items():
+            if chunks == [100]:
+                assert np.array_equal(g, ref), f"{spec.name} {name}: a 100-token prefill left the second terms"
+                continue
+            d = float(np.abs(g - ref).max())
+            print(f"[metrics] {spec.name} chunks {chunks} {name}: float32 last row vs second terms max |d| {d:.2e} "
+                  f"({d / float(np.abs(ref).max()):.2e} of the peak)")
+            assert d <= 2.5e-4 * float(np.abs(ref).max()), f"{spec.name} {chunks} {name}: max |d| {d:.3e}"
+            assert int(np.argmax(g)) == int(np.argmax(ref))
     a.close()
     b.close()
     model.close()
