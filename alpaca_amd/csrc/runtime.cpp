@@ -1326,22 +1326,25 @@ static int encode_decode_layer(ahip_session* s, int li, int pos, const int* pos_
 // set) is recorded once these rows' K/V are in the cache; the attention first
 // waits for the n_before events of before_attn (earlier rows' K/V).
 // `last`: these rows end with the row whose logits the call returns.
-// Which of a layer's Wo, gate/up and down GEMMs take the returned row as a
-// float32 GEMV (encode_mfma_layer): those whose weights (gate and up
-// together) are at least 1 MB.  Per layer at 4,096 rows against the tail
-// rows' second terms, the GEMMs gain (us) 0.6 / 8 / 0.4 at the 135M shape,
-// 3.5 / 16 / 12 at the 360M shape and 13 / 42 / 50 at the 1.7B shape, for
-// about 3 us per GEMV launch on the small matrices.
+// Which of a layer's Wo, gate/up and down GEMMs over n rows take the returned
+// row as a float32 GEMV (encode_mfma_layer): from 2,048 rows, those with at
+// least 2M weights (gate and up together).  The GEMV is one more launch of
+// 3-10 us in the layer's chain; the tail rows' second terms it replaces cost
+// more only on large GEMMs.  Measured 4096-token prefills (two halves of 2,048
+// rows at the 135M and 360M shapes, one stream at the 1.7B shape), tok/s with
+// no GEMV -> this rule: 360M 520k -> 564-579k, 1.7B 149k -> 163k; every GEMV on
+// the 135M shape 1,023-1,035k -> 951-956k, at the 360M shape over 2,048 tokens
+// (halves of 1,024 rows) 467-472k -> 406-412k.
 // ALPACA_HIP_LAST_ROW_GEMV (read per call): a mask of kSide* bits instead.
 enum : int { kSideWo = 1, kSideGateUp = 2, kSideDown = 4 };
-static int last_row_gemv_mask(const ahip_model::Layer& L) {
+static int last_row_gemv_mask(const ahip_model::Layer& L, int n) {
     const int forced = env_int("ALPACA_HIP_LAST_ROW_GEMV", -1);
     if (forced >= 0) return forced & 7;
-    auto bytes = [](const DevMatrix& w) { return raw_bytes(w.dtype, (int64_t)w.rows * w.cols); };
-    const int64_t mb = 1 << 20;
-    return (bytes(L.pre(L.wo, L.wo16)) >= mb ? kSideWo : 0) |
-           (bytes(L.pre(L.gate, L.gate16)) + bytes(L.pre(L.up, L.up16)) >= mb ? kSideGateUp : 0) |
-           (bytes(L.pre(L.down, L.down16)) >= mb ? kSideDown : 0);
+    if (n < 2048) return 0;
+    auto weights = [](const DevMatrix& w) { return (int64_t)w.rows * w.cols; };
+    const int64_t lim = 1 << 21;
+    return (weights(L.wo.m) >= lim ? kSideWo : 0) |
+           (weights(L.gate.m) + weights(L.up.m) >= lim ? kSideGateUp : 0) | (weights(L.down.m) >= lim ? kSideDown : 0);
 }
 
 static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, bool flash, bool last, hipStream_t st,
@@ -1448,7 +1451,7 @@ static int encode_mfma_layer(ahip_session* s, int li, int row0, int n, int pos, 
     // launch against the tail tiles' second terms, which set the time of GEMMs
     // over about one round of workgroups and add a sixteenth of the work of
     // larger ones.
-    const int side = (!all && last && tail0 > 0) ? last_row_gemv_mask(L) : 0;
+    const int side = (!all && last && tail0 > 0) ? last_row_gemv_mask(L, n) : 0;
     const int64_t lr = n - 1;  // the last row
     s->stage("attn out projection (+residual)");
     const DevMatrix& wo = L.pre(L.wo, L.wo16);

@@ -179,11 +179,11 @@ def test_float32_last_row_matches_two_term_tail(hip_ctx, spec):
       splits merged by the last one to arrive, a counter per head) and the
       other rows take one f16 term of Q and P; ALPACA_HIP_EXACT_LAST_ROW=0 (read
       at session creation) keeps both second terms on the row's query block;
-    - Wo, gate/up and down: GEMMs of at least 1 MB of weights cover the other
-      rows with one term and the row is a float32 GEMV over its two f16 terms;
-      ALPACA_HIP_LAST_ROW_GEMV (a mask, read per call: 0 none, 7 all three)
-      chooses, and with 0 the tail rows from the last rounded down to 256 take
-      their second terms in the GEMMs.
+    - Wo, gate/up and down: over 2,048 rows and more, GEMMs of at least 2M
+      weights cover the other rows with one term and the row is a float32 GEMV
+      over its two f16 terms; ALPACA_HIP_LAST_ROW_GEMV (a mask, read per call:
+      0 none, 7 all three) forces the choice, and with 0 the tail rows from the
+      last rounded down to 256 take their second terms in the GEMMs.
     Every form approximates the same float32 row: the logits agree with the
     all-second-terms form to 2.5e-4 of the peak (the tail's other rows round
     differently) with the same greedy token, over one attention split (300
