@@ -504,6 +504,36 @@ def counter_table(dirs: dict, cf: list, cw: list, values, prefill: bool = False)
     return 0
 
 
+def library_gemm(iters: int = 50) -> list:
+    """torch.matmul on f16 operands (hipBLASLt / rocBLAS) at the M = 4096 prefill GEMM shapes of C1 and
+    C5 (N counts gate and up together), f16 out, no epilogue: what a plain library f16 GEMM reaches at
+    these shapes, beside the quantised two-term kernels of this library (HIP events around `iters`
+    back-to-back launches after five untimed ones)."""
+    import torch
+    shapes = (("C1 qkv", 960, 576), ("C1 wo", 576, 576), ("C1 gate+up", 3072, 576), ("C1 down", 576, 1536),
+              ("C5 qkv", 6144, 2048), ("C5 wo", 2048, 2048), ("C5 gate+up", 16384, 2048), ("C5 down", 2048, 8192))
+    out = []
+    m = PREFILL_TOKENS
+    for name, n, k in shapes:
+        a = torch.randn(m, k, device="cuda", dtype=torch.float16)
+        b = torch.randn(k, n, device="cuda", dtype=torch.float16)
+        for _ in range(5):
+            c = a @ b
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(iters):
+            c = a @ b
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / iters * 1e3
+        tf = 2 * m * n * k / us / 1e6
+        out.append({"gemm": name, "shape": f"M={m} N={n} K={k} f16", "us": round(us, 2), "TFLOPs": round(tf, 1),
+                    "frac": round(tf / 2500, 4)})
+        del a, b, c
+    return out
+
+
 def cpu_info() -> dict:
     model = None
     try:
@@ -585,6 +615,9 @@ def main() -> int:
     ap.add_argument("--no-kernels", action="store_true", help="skip the isolated-kernel figures and the cache check")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the isolated-kernel figures (GEMV per shape, C2 GEMMs, C3 attention), for traces")
+    ap.add_argument("--library-gemm", action="store_true",
+                    help="only torch's f16 GEMM (the ROCm BLAS libraries) at the prefill GEMM shapes of C1 and C5: "
+                         "a reference for what a plain f16 GEMM reaches at those shapes")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only a device-to-device copy of 256 MiB, the reference the HBM byte counters are scaled by")
     ap.add_argument("--counter-summary", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
@@ -620,6 +653,9 @@ def main() -> int:
     from alpaca_amd import synth
     from alpaca_amd.model import HIPContext, HIPLlamaModel
 
+    if args.library_gemm:
+        print(json.dumps({"library_f16_gemm": library_gemm()}), flush=True)
+        return 0
     if args.kernels_only:
         kctx = HIPContext(0)
         print(json.dumps({"kernels": kernel_figures(kctx)}), flush=True)
