@@ -134,7 +134,9 @@ def test_two_stream_prefill_matches_one_stream(hip_ctx, spec, prec, rows):
     ALPACA_HIP_PREFILL_STREAMS=1 (read per call) to 1e-5 of the logit peak.
     By default only the QKV input and the rows from the last row rounded down
     to a multiple of 256 (the same rows in both runs: the split point is a
-    multiple of 256) take two terms; a float32 value that differs in its last
+    multiple of 256) take two terms, and past 256 rows the returned row is
+    computed in float32 where its launch allows it (the flash launch's wave-sets
+    and the GEMM sizes can differ for a half); a float32 value that differs in its last
     bit can then round to the neighbouring f16 (2^-11 relative) in the one-term
     rows, so the runs agree to 2.5e-4 of the peak, and each is held to the
     CPU oracle at full size by the C1P workload test.  (One-term activations
@@ -260,6 +262,12 @@ def test_prefill_weight_cache_is_the_f16_model(hip_ctx, spec):
     prompt = synth.prompt_tokens(spec, 100)
     a = cached.make_session(capacity=160, gemm_precision="fast").forward(prompt)
     b = ref.make_session(capacity=160, gemm_precision="fast").forward(prompt)
+    assert np.array_equal(a, b)
+    # past 256 rows, with the returned row's float32 GEMVs forced on (they read the cache too)
+    long_prompt = synth.prompt_tokens(spec, 300)
+    with env(ALPACA_HIP_LAST_ROW_GEMV=7):
+        a = cached.make_session(capacity=320, gemm_precision="fast").forward(long_prompt)
+        b = ref.make_session(capacity=320, gemm_precision="fast").forward(long_prompt)
     assert np.array_equal(a, b)
     # exact prefill and decode read the quantised weights
     s1, s2 = cached.make_session(capacity=160, gemm_precision="exact"), plain.make_session(capacity=160,
