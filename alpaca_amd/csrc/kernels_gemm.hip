@@ -54,6 +54,9 @@ struct GemmArgs {
     // take the activations' second term, the others one term; the second term
     // of f16 outputs is written for rows >= lo_out_row0 only.
     int lo_row0 = 0, lo_out_row0 = 0, lo_col0 = 1 << 30;
+    // Tiles in row groups of group_m row blocks, column by column inside a
+    // group (0: row by row); set per launch by run_dgemm.
+    int group_m = 0;
     QkvRope qkv;  // GEMM_QKV_ROPE only (yh = qkv.qh, ldy = heads * hd)
 };
 
@@ -788,11 +791,22 @@ __global__ __launch_bounds__(64 * (BM / WM) * (BN / WN) * KS) void dgemm_kernel(
             b -= pad;
         }
     }
+    int tm_i = t / tiles_n, tn_i = t % tiles_n;
     if (!tail_tile) {
         const int tiles = main_m * tiles_n, xcd = b % 8, q = tiles / 8, rem = tiles % 8;
         t = xcd * q + min(xcd, rem) + b / 8;  // XCD-major tile order (bijective)
+        tm_i = t / tiles_n;
+        tn_i = t % tiles_n;
+        if (p.group_m > 0) {
+            // a group holds rows [g * group_m, + gr) x every column, taken
+            // column by column (the last group may have fewer rows; bijective)
+            const int gsz = p.group_m * tiles_n, g = t / gsz, r = t - g * gsz;
+            const int gr = min(p.group_m, main_m - g * p.group_m);
+            tm_i = g * p.group_m + r % gr;
+            tn_i = r / gr;
+        }
     }
-    const int m0 = (t / tiles_n) * BM, n0 = (t % tiles_n) * BN;
+    const int m0 = tm_i * BM, n0 = tn_i * BN;
     const int lane = threadIdx.x & 63;
     const int wave = wave_all % NW;  // within the K set
     const int wm = wave / (BN / WN), wn = wave % (BN / WN);
@@ -1090,9 +1104,31 @@ __global__ __launch_bounds__(64 * (BM / WM) * (BN / WN) * KS) void dgemm_kernel(
         }
 }
 
+// Row groups of the tile order.  Each XCD takes a contiguous range of tiles;
+// row by row, the tiles it runs at once cover one or two row blocks and a wide
+// band of columns, so where the weights exceed its 4 MB L2 it streams every
+// weight column again for each of its row blocks.  In groups of four row
+// blocks, taken column by column, the tiles running at once share each weight
+// column four times.  Measured over 4,096-token prefills (us per layer, row by
+// row against groups of 2 / 4 / 8 / 16): at the 1.7B shape (weights 4.5-36 MB
+// per GEMM) QKV 243 -> 240 / 236 / 238 / 241, gate+up 390 -> 385 / 381 / 385
+// / 389, down 212 -> 209 / 206 / 211 / 213 (165k -> 169k tok/s with 4); at
+// the 135M and 360M shapes (weights of 0.35-2.8 MB, which every XCD's L2
+// holds) no change.  ALPACA_HIP_GEMM_GROUP=<rows> forces the group (0: row by
+// row; tuning and tests; read on every launch).
+int gemm_group_rows(const GemmArgs& a, int mats) {
+    if (const char* e = std::getenv("ALPACA_HIP_GEMM_GROUP")) return std::max(0, std::atoi(e));
+    const DevMatrix& w = a.w;
+    const int64_t per = (int64_t)w.rows * w.cols;
+    const int64_t bytes = (w.dtype == DT_Q8_0 ? per * 34 / 32 : w.dtype == DT_Q4_0 ? per * 18 / 32 : per * 2) * mats;
+    return bytes >= (int64_t)4 << 20 ? 4 : 0;
+}
+
 template <int FMT, int BM, int BN, int WM, int WN, int MODE, int RH, bool TT, int KS = 1, bool TAIL = false>
-hipError_t run_dgemm(const GemmArgs& a, hipStream_t st) {
-    const int tm = (a.M + BM - 1) / BM, tn = (a.w.rows + BN - 1) / BN;
+hipError_t run_dgemm(const GemmArgs& args, hipStream_t st) {
+    const int tm = (args.M + BM - 1) / BM, tn = (args.w.rows + BN - 1) / BN;
+    GemmArgs a = args;
+    a.group_m = gemm_group_rows(a, MODE == GEMM_SWIGLU ? 2 : 1);
     int grid = tm * tn;
     if constexpr (TAIL) {
         if (a.lo_row0 % BM) return hipErrorInvalidValue;  // tail tiles start at lo_row0

@@ -128,7 +128,14 @@ def test_gemm_tile_families_agree_at_large_grids(hip_ops, name, dt):
             ident = hip_ops.linear(onehot, w, "fast")
         bad = np.argwhere(ident != deq.T[np.arange(m) % k])
         assert bad.size == 0, f"{name} tile {tile}: {len(bad)} weights differ, first at (m, n) = {bad[0]}"
-    for tile in ("128x64", "128x128", "256", "128x256", "64x64"):
+    # The tile order (row groups of ALPACA_HIP_GEMM_GROUP row blocks, 3 leaving
+    # a partial last group) moves tiles between workgroups, not their sums.
+    for tile, group in ((None, "3"), (None, "4"), ("64x64", "3"), ("128x256", "5")):
+        with env(ALPACA_HIP_GEMM_TILE=tile, ALPACA_HIP_GEMM_GROUP=group):
+            outs[(tile, group)] = (hip_ops.linear(x, w, "fast"), hip_ops.linear_add(x, w, res, "fast"),
+                                   hip_ops.gate_up_silu(x, w, wu, "fast"))
+    for tile in ("128x64", "128x128", "256", "128x256", "64x64", (None, "3"), (None, "4"), ("64x64", "3"),
+                 ("128x256", "5")):
         for i, what in enumerate(("store", "residual", "swiglu")):
             a, b = outs[tile][i], outs[None][i]
             assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{name} {what}: tile {tile} != default"
@@ -337,6 +344,13 @@ def test_gemm_second_term_from_a_row_on(hip_ops, name, dt):
         with env(ALPACA_HIP_OP_LO_ROW0=lo_row0):
             tail = (hip_ops.linear(x, w, "fast"), hip_ops.linear_add(x, w, res, "fast"),
                     hip_ops.gate_up_silu(x, w, wu, "fast"))
+        # row groups of the tile order (3 row blocks: a partial last group) before the tail tiles
+        with env(ALPACA_HIP_OP_LO_ROW0=lo_row0, ALPACA_HIP_GEMM_GROUP=3):
+            grouped = (hip_ops.linear(x, w, "fast"), hip_ops.linear_add(x, w, res, "fast"),
+                       hip_ops.gate_up_silu(x, w, wu, "fast"))
+        for i, what in enumerate(("store", "residual", "swiglu")):
+            assert np.array_equal(grouped[i].view(np.uint32), tail[i].view(np.uint32)), \
+                f"{name} {what} m={m}: row groups of 3 change the result"
         y = orc.linear(x, dt, w.data, n)
         u = orc.linear(x, dt, wu.data, n)
         cpu = (y, orc.add(res, y), orc.mul(orc.silu(y), u))
