@@ -268,6 +268,10 @@ __device__ __forceinline__ void flash_attn_body(const FlashArgs& a, uint8_t* sta
     // With one set (three waves per SIMD, registers to spare) the block's V^T
     // fragments are read before the softmax, so their LDS latency overlaps it.
     constexpr bool kEarlyV = NSET == 1 && HD == 64;
+    // The exponentials are pinned ahead of the rescale branch (below) with two
+    // sets (C1's attention per layer 41.4-41.8 -> 40.7-41.1 us), not with one,
+    // three waves per SIMD (C5's 104.0 -> 105.9 us).
+    constexpr bool kPinExp = NSET == 2;
     auto softmax_pv = [&](const f32x4* sacc, const uint8_t* Vt) {
         f16x8 vpre[kEarlyV ? 2 : 1][kEarlyV ? DT : 1];
         if constexpr (kEarlyV) {
@@ -309,6 +313,15 @@ __device__ __forceinline__ void flash_attn_body(const FlashArgs& a, uint8_t* sta
                 ph[t][pr] = h;
                 if constexpr (PT) pl[t][pr] = pack_f16x2(minus_f16_lo(h, e0), minus_f16_hi(h, e1));
             }
+        // The exponentials are computed here, ahead of the rescale branch,
+        // where they can issue among the next block's score MFMAs (left to
+        // itself the compiler sinks them past the branch, to their use).
+        if constexpr (kPinExp) {
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int pr = 0; pr < 2; pr++) asm volatile("" : "+v"(ph[t][pr]));
+        }
         // alpha is exactly 1 in every lane whose running max did not move (the
         // usual case past the first blocks): the wave then skips the rescale.
         if (__builtin_amdgcn_ballot_w64(m != mn)) {
