@@ -218,8 +218,9 @@ SPLIT_CASES = [(0, 9, 3, 64), (1, 9, 3, 64), (7, 9, 3, 64), (255, 9, 3, 64), (25
                (511, 9, 3, 64), (1000, 9, 3, 64), (2047, 9, 3, 64), (300, 8, 2, 128), (700, 8, 8, 64),
                (90, 32, 4, 128), (500, 4, 1, 64), (4095, 15, 5, 64),
                # splits past 256 positions: 512-thread workgroups (the 1.7B shape's 32 KV heads
-               # at 4,176 positions: 288-position splits; two heads per KV head, head dim 128)
-               (4175, 32, 32, 64), (9000, 32, 16, 128)]
+               # at 4,176 positions: 288-position splits; two heads per KV head, head dim 128;
+               # 384- and 448-position splits)
+               (4175, 32, 32, 64), (9000, 32, 16, 128), (5999, 64, 32, 64), (6999, 32, 32, 64)]
 
 
 @pytest.mark.parametrize("start,heads,kv,hd", SPLIT_CASES)
