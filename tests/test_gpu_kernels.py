@@ -160,6 +160,38 @@ def test_gemm_tile_families_agree_at_large_grids(hip_ops, name, dt):
         assert (err <= tol).all(), f"{name} {what}: worst error / tolerance {(err / tol).max():.3f}"
 
 
+@pytest.mark.parametrize("name,dt", [("q8_0", Q8_0), ("q4_0", Q4_0)])
+def test_gemm_row_groups_by_default_on_large_weights(hip_ops, name, dt):
+    """Weights of 4 MiB and more (4096x1024 in Q8_0, 4.5 MB; 4096x2048 in Q4_0, 4.7 MB) take the
+    tile order in row groups of four row blocks by default; it moves tiles between workgroups, not
+    their sums, so the store, residual and SwiGLU epilogues equal the row-by-row order
+    (ALPACA_HIP_GEMM_GROUP=0) bit for bit, and the default stays within the exact GEMM's
+    tolerance 2e-4 + 1e-4 |y| of the oracle, over M = 1100 rows (a partial last row block and a
+    partial last group)."""
+    m = 1100
+    n, k = (4096, 1024) if dt == Q8_0 else (4096, 2048)
+    w = encode(rand((n, k), 6161 + dt, 0.3), dt)
+    wu = encode(rand((n, k), 6262 + dt, 0.3), dt)
+    x = rand((m, k), 6363)
+    res = rand((m, n), 6464, 5)
+    outs = {}
+    for group in (None, "0"):
+        with env(ALPACA_HIP_GEMM_GROUP=group):
+            outs[group] = (hip_ops.linear(x, w, "fast"), hip_ops.linear_add(x, w, res, "fast"),
+                           hip_ops.gate_up_silu(x, w, wu, "fast"))
+    y = orc.linear(x, dt, w.data, n)
+    u = orc.linear(x, dt, wu.data, n)
+    cpu = (y, orc.add(res, y), orc.mul(orc.silu(y), u))
+    for i, what in enumerate(("store", "residual", "swiglu")):
+        a, b = outs[None][i], outs["0"][i]
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{name} {what}: row groups != row by row"
+        e = cpu[i].astype(np.float64)
+        err = np.abs(a.astype(np.float64) - e)
+        tol = 2e-4 + 1e-4 * np.abs(e)
+        print(f"[metrics] row-group GEMM {name} {what} M={m} K={k} N={n}: worst error / tol {(err / tol).max():.4f}")
+        assert (err <= tol).all(), f"{name} {what}: worst error / tolerance {(err / tol).max():.3f}"
+
+
 def test_fused_gate_up_silu(hip_ops):  # KernelTests.swift:219-244
     k, n = 576, 200
     for t in [1, 3, 16, 40, 100]:
