@@ -1041,15 +1041,19 @@ hipError_t decode_dispatch(int G, dim3 grid, hipStream_t st, const float* q, con
 
 // Wave-sets per workgroup at head dim 64 (ALPACA_HIP_FLASH_SETS = 1 or 2,
 // read per launch, forces a count).  One-set workgroups (48 KB of LDS) run
-// three per CU: below three per CU the causal critical path dominates and
-// two sets win.  Four sets (one 1024-thread workgroup per CU) were slower at
-// every measured shape: the kernel is bound by the SIMDs' issue, not by the
+// three per CU, two-set ones two: below four query blocks per CU the causal
+// critical path dominates and two sets win (attention per layer, one set ->
+// two: 360M shape at 3,584 and 4,096 rows, 840 and 960 workgroups, 56.8 ->
+// 49.8 and 66.4 -> 60.0 us; 1.7B shape at 1,536 rows, 768 workgroups, 29.0 ->
+// 27.7; 1,024 workgroups 38.2 either way; 1,280 and 1,536 workgroups 2-3%
+// slower).  Four sets (one 1024-thread workgroup per CU) were slower at every
+// measured shape: the kernel is bound by the SIMDs' issue, not by the
 // longest query block's walk.
 static int flash_sets(dim3 grid) {
     const char* e = std::getenv("ALPACA_HIP_FLASH_SETS");
     const int forced = e ? std::atoi(e) : 0;
     if (forced == 1 || forced == 2) return forced;
-    return (int64_t)grid.x * grid.y < 3 * 256 ? 2 : 1;
+    return (int64_t)grid.x * grid.y < 4 * 256 ? 2 : 1;
 }
 
 template <int NSET, bool TT, bool PT>

@@ -271,7 +271,7 @@ def test_split_decode_attention(hip_ops, start, heads, kv, hd):  # KernelTests.s
 TILED = [(8, 0, 9, 3, 64), (31, 0, 9, 3, 64), (32, 0, 9, 3, 64), (33, 0, 9, 3, 64), (100, 0, 9, 3, 64),
          (64, 200, 9, 3, 64), (45, 7, 8, 2, 128), (128, 128, 4, 4, 128), (17, 3, 6, 3, 64), (200, 0, 8, 2, 64),
          (16, 0, 9, 3, 64), (300, 40, 15, 5, 64), (1024, 0, 9, 3, 64), (515, 77, 8, 2, 128),
-         (1536, 0, 32, 8, 64)]  # the last: 768 workgroups, the one-wave-set kernel
+         (1536, 0, 32, 8, 64), (2048, 0, 32, 8, 64)]  # 768 workgroups: two wave-sets; 1,024: one
 
 
 @pytest.mark.parametrize("t,start,heads,kv,hd", TILED)
