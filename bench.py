@@ -633,7 +633,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures the single-GPU hot path only: this build runs on one GPU "
-              "(sharding is described in DESIGN.md, not implemented); run with --gpus 1.", file=sys.stderr)
+              "(sharding over several GPUs is not implemented); run with --gpus 1.", file=sys.stderr)
         return 2
     if args.steps < 1 or args.warmup < 0 or args.warmup >= DECODE_CTX:
         print("need steps >= 1 and 0 <= warmup < 2048", file=sys.stderr)
