@@ -160,16 +160,17 @@ def test_gemm_tile_families_agree_at_large_grids(hip_ops, name, dt):
         assert (err <= tol).all(), f"{name} {what}: worst error / tolerance {(err / tol).max():.3f}"
 
 
-@pytest.mark.parametrize("name,dt", [("q8_0", Q8_0), ("q4_0", Q4_0)])
+@pytest.mark.parametrize("name,dt", FORMATS)
 def test_gemm_row_groups_by_default_on_large_weights(hip_ops, name, dt):
-    """Weights of 4 MiB and more (4096x1024 in Q8_0, 4.5 MB; 4096x2048 in Q4_0, 4.7 MB) take the
+    """Weights of 4 MiB and more (4096x1024 in Q8_0, 4.5 MB; 4096x2048 in Q4_0, 4.7 MB; 2048x1024
+    in F16, 4.2 MB, the prefill weight cache's format) take the
     tile order in row groups of four row blocks by default; it moves tiles between workgroups, not
     their sums, so the store, residual and SwiGLU epilogues equal the row-by-row order
     (ALPACA_HIP_GEMM_GROUP=0) bit for bit, and the default stays within the exact GEMM's
     tolerance 2e-4 + 1e-4 |y| of the oracle, over M = 1100 rows (a partial last row block and a
     partial last group)."""
     m = 1100
-    n, k = (4096, 1024) if dt == Q8_0 else (4096, 2048)
+    n, k = {Q8_0: (4096, 1024), Q4_0: (4096, 2048), F16: (2048, 1024)}[dt]
     w = encode(rand((n, k), 6161 + dt, 0.3), dt)
     wu = encode(rand((n, k), 6262 + dt, 0.3), dt)
     x = rand((m, k), 6363)
